@@ -1,0 +1,212 @@
+/*
+ * lora_merge.h -- C ABI of the MI355X (gfx950) LoRA-merge library
+ * (libpiper_lora_merge.so, built from piper-offload_amd/csrc).
+ *
+ * Each entry point replaces one function of piper-offload's fused merge
+ * path.  Citations use P/ = src/piper_offload/ of the reference:
+ *
+ *   lm_int8_merge   <- merge_int8_lora     P/_triton_int8_lora.py:267-407
+ *   lm_fp8_merge    <- merge_float8_lora   P/_triton_float8_lora.py:486-588
+ *   lm_nvfp4_merge  <- merge_nvfp4_lora    P/_triton_nvfp4_lora.py:515-595
+ *   lm_mx_merge     <- merge_mx_lora_      P/_triton_mx_lora.py:333-425
+ *   lm_bf16_merge   <- RegularAdapter.merge_lora_ (addmm_)
+ *                                          P/tensor_adapters.py:686-696
+ *   lm_q8_0_merge   <- (no reference counterpart: the reference routes GGUF
+ *                      only, P/gguf_adapter.py:160-284; requant follows the
+ *                      ggml Q8_0 recipe)
+ *   lm_gguf_dequant <- dequantize          P/gguf_dequant.py:303-331
+ *   lm_*_requant, lm_*_dequant           <- the portable dequantize_* /
+ *                      requantize_* shims (P/_torchao_int8.py:113-173,
+ *                      P/_torchao_float8.py:93-161, P/_torchao_nvfp4.py:106-197,
+ *                      P/_torchao_mx.py:143-207) as single fused kernels
+ *   lm_*_merge_stack <- the per-target loop of merge_lora()
+ *                      (P/merge.py:121-125) as one grouped launch
+ *
+ * Conventions
+ *  - All pointers are device pointers unless noted; tensors are row-major
+ *    and contiguous unless a leading dimension is given.  M = out rows,
+ *    N = logical in columns, rank = r.
+ *  - `stream` is a hipStream_t passed as void*.  No entry point
+ *    synchronizes or allocates device memory; scratch comes from the
+ *    caller's `workspace` (size from lm_workspace_size()).
+ *  - Return value: LM_OK or an lm_status; lm_last_error() returns a
+ *    thread-local message for the last failure on the calling thread.
+ *  - The deterministic path rounds to nearest even.  Stochastic rounding
+ *    draws u = k * 2^-16, k the 16-bit half-word (idx & 7) of
+ *    Philox4x32-10(counter = idx >> 3, key = seed), idx = row * N + col.
+ *  - merged = round_compute(fma(delta, strength, base)), delta the fp32
+ *    accumulation of B@A on bf16/fp16 MFMA.
+ */
+#ifndef PIPER_LORA_MERGE_H
+#define PIPER_LORA_MERGE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LM_ABI_VERSION 1
+
+/* element / storage dtypes */
+enum lm_dtype {
+  LM_F32 = 0,
+  LM_BF16 = 1,
+  LM_F16 = 2,
+  LM_E4M3 = 3, /* float8_e4m3fn */
+  LM_E5M2 = 4, /* float8_e5m2 */
+  LM_E2M1 = 5, /* packed fp4, even column in the low nibble */
+  LM_E8M0 = 6
+};
+
+/* rounding of terminal codes */
+enum lm_rounding_mode {
+  LM_ROUND_NEAREST = 0,
+  LM_ROUND_STOCHASTIC = 1
+};
+
+/* MX E8M0 scale calculation (P/_triton_mx_lora.py:23-26) */
+enum lm_mx_scaling { LM_MX_FLOOR = 0, LM_MX_RCEIL = 1, LM_MX_CEIL = 2, LM_MX_EVEN = 3 };
+
+/* GGUF quant types (ggml numbering) */
+enum lm_gguf_type { LM_GGUF_F32 = 0, LM_GGUF_F16 = 1, LM_GGUF_Q8_0 = 8, LM_GGUF_BF16 = 30 };
+
+enum lm_status {
+  LM_OK = 0,
+  LM_EINVAL = 1,       /* bad shape / dtype / pointer: maps to ValueError */
+  LM_EUNSUPPORTED = 2, /* valid but not implemented layout: ValueError */
+  LM_EWORKSPACE = 3,   /* workspace too small */
+  LM_EHIP = 4          /* HIP runtime failure: RuntimeError */
+};
+
+/* One LoRA update B@A scaled by `strength` (P/lora.py:595-626 stages B and A
+ * on the target device in the compute dtype). */
+typedef struct lm_lora {
+  const void* b; /* [M, rank], row stride ldb elements */
+  const void* a; /* [rank, N], row stride lda elements */
+  int64_t ldb;
+  int64_t lda;
+  int32_t rank;
+  int32_t dtype; /* LM_BF16 or LM_F16 (the compute dtype) */
+  float strength;
+  int32_t reserved;
+} lm_lora;
+
+/* Rounding request; `seed` is the uint64 from derive_seed()
+ * (P/seeding.py:10-36, P/lora.py:356-359). */
+typedef struct lm_rounding {
+  int32_t mode; /* lm_rounding_mode */
+  int32_t reserved;
+  uint64_t seed;
+} lm_rounding;
+
+int lm_version(void);
+const char* lm_last_error(void);
+
+/* Bytes of workspace any entry point below needs for one tensor of this
+ * shape and rank (stack entries: sum over items + lm_stack_workspace_extra). */
+size_t lm_workspace_size(int64_t M, int64_t N, int32_t rank);
+size_t lm_stack_workspace_extra(int32_t count);
+
+/* ---------------- INT8 (TorchAO Int8Tensor) ---------------------------
+ * q: int8 [M, N]; scale: [M*N/group] in scale_dtype (LM_F32/LM_BF16);
+ * zero_point: int8 [M*N/group] or NULL (symmetric).  group = N (per-row)
+ * or M*N (per-tensor).  Outputs may alias inputs (in-place merge). */
+int lm_int8_merge(const int8_t* q, const void* scale, const int8_t* zero_point, int8_t* q_out, void* scale_out,
+                  int8_t* zero_point_out, int64_t M, int64_t N, int64_t group, int32_t scale_dtype, int32_t asymmetric,
+                  int32_t reduce_range, const lm_lora* lora, const lm_rounding* rounding, void* workspace,
+                  size_t workspace_bytes, void* stream);
+int lm_int8_requant(const void* dense, int32_t dense_dtype, int8_t* q_out, void* scale_out, int8_t* zero_point_out,
+                    int64_t M, int64_t N, int64_t group, int32_t scale_dtype, int32_t asymmetric, int32_t reduce_range,
+                    const lm_rounding* rounding, void* workspace, size_t workspace_bytes, void* stream);
+/* dequantize (lora == NULL) or dequantize + merge without requant. */
+int lm_int8_dequant(const int8_t* q, const void* scale, const int8_t* zero_point, int64_t M, int64_t N, int64_t group,
+                    int32_t scale_dtype, const lm_lora* lora, void* out, int32_t out_dtype, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* ---------------- scaled FP8 (TorchAO Float8Tensor) -------------------
+ * q: fp8 [M, N] (fp8_dtype LM_E4M3/LM_E5M2); scale: fp32 [M*N/group];
+ * group = N (per-row) or M*N (per-tensor). */
+int lm_fp8_merge(const uint8_t* q, const float* scale, uint8_t* q_out, float* scale_out, int64_t M, int64_t N,
+                 int64_t group, int32_t fp8_dtype, const lm_lora* lora, const lm_rounding* rounding, void* workspace,
+                 size_t workspace_bytes, void* stream);
+int lm_fp8_requant(const void* dense, int32_t dense_dtype, uint8_t* q_out, float* scale_out, int64_t M, int64_t N,
+                   int64_t group, int32_t fp8_dtype, const lm_rounding* rounding, void* workspace,
+                   size_t workspace_bytes, void* stream);
+int lm_fp8_dequant(const uint8_t* q, const float* scale, int64_t M, int64_t N, int64_t group, int32_t fp8_dtype,
+                   const lm_lora* lora, void* out, int32_t out_dtype, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/* ---------------- NVFP4 (TorchAO NVFP4Tensor) -------------------------
+ * q: uint8 [M, N/2]; scale: e4m3 [M, N/16] or swizzled
+ * [ceil(M/128)*32, ceil(N/64)*16]; per_tensor_scale: fp32[1] or NULL
+ * (single-level).  scale_out is fully written (swizzle padding zeroed). */
+int lm_nvfp4_merge(const uint8_t* q, const uint8_t* scale, const float* per_tensor_scale, uint8_t* q_out,
+                   uint8_t* scale_out, float* per_tensor_scale_out, int64_t M, int64_t N, int32_t swizzled,
+                   const lm_lora* lora, const lm_rounding* rounding, void* workspace, size_t workspace_bytes,
+                   void* stream);
+int lm_nvfp4_requant(const void* dense, int32_t dense_dtype, uint8_t* q_out, uint8_t* scale_out,
+                     float* per_tensor_scale_out, int64_t M, int64_t N, int32_t swizzled, const lm_rounding* rounding,
+                     void* workspace, size_t workspace_bytes, void* stream);
+int lm_nvfp4_dequant(const uint8_t* q, const uint8_t* scale, const float* per_tensor_scale, int64_t M, int64_t N,
+                     int32_t swizzled, const lm_lora* lora, void* out, int32_t out_dtype, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* ---------------- MX (TorchAO MXTensor: MXFP4 / MXFP8) ----------------
+ * In place.  elem_dtype LM_E2M1 (q: uint8 [M, N/2]) or LM_E4M3/LM_E5M2
+ * (q: [M, N]); scale: e8m0 [M, N/32] or swizzled [ceil(M/128)*32,
+ * ceil(N/128)*16]; scaling = lm_mx_scaling. */
+int lm_mx_merge(uint8_t* q, uint8_t* scale, int64_t M, int64_t N, int32_t elem_dtype, int32_t scaling, int32_t swizzled,
+                const lm_lora* lora, const lm_rounding* rounding, void* workspace, size_t workspace_bytes,
+                void* stream);
+int lm_mx_requant(const void* dense, int32_t dense_dtype, uint8_t* q_out, uint8_t* scale_out, int64_t M, int64_t N,
+                  int32_t elem_dtype, int32_t scaling, int32_t swizzled, const lm_rounding* rounding, void* workspace,
+                  size_t workspace_bytes, void* stream);
+int lm_mx_dequant(const uint8_t* q, const uint8_t* scale, int64_t M, int64_t N, int32_t elem_dtype, int32_t swizzled,
+                  const lm_lora* lora, void* out, int32_t out_dtype, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* ---------------- GGUF Q8_0 ------------------------------------------
+ * packed: uint8 [M, N/32*34], blocks [fp16 d][32 x int8]. */
+int lm_q8_0_merge(const uint8_t* packed, uint8_t* packed_out, int64_t M, int64_t N, const lm_lora* lora,
+                  const lm_rounding* rounding, void* workspace, size_t workspace_bytes, void* stream);
+int lm_q8_0_requant(const void* dense, int32_t dense_dtype, uint8_t* packed_out, int64_t M, int64_t N,
+                    const lm_rounding* rounding, void* workspace, size_t workspace_bytes, void* stream);
+/* GGUF dequantize of `rows` rows of `cols` logical elements
+ * (P/gguf_dequant.py:303-331; out dtype LM_BF16/LM_F16/LM_F32). */
+int lm_gguf_dequant(const uint8_t* packed, int32_t quant_type, int64_t rows, int64_t cols, const lm_lora* lora,
+                    void* out, int32_t out_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------- plain bf16/fp16 weight (addmm_) ---------------------
+ * w: [M, N] row stride ldw, dtype = lora->dtype; w += strength * B@A. */
+int lm_dense_merge(void* w, int64_t M, int64_t N, int64_t ldw, const lm_lora* lora, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* ---------------- stacks: many targets, one grouped launch ------------
+ * `items` is a HOST array of `count` descriptors.  Each target gets its own
+ * seed (derive_seed(param_path, merge_index)). */
+typedef struct lm_stack_item {
+  const void* q;        /* packed codes in */
+  const void* scale;    /* scales in */
+  const void* aux;      /* int8: zero point or NULL; nvfp4: per_tensor_scale or NULL */
+  void* q_out;
+  void* scale_out;
+  void* aux_out;
+  int64_t M;
+  int64_t N;
+  lm_lora lora;
+  uint64_t seed;
+} lm_stack_item;
+
+/* INT8 per-row symmetric stack (scale_dtype LM_F32/LM_BF16). */
+int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, int32_t scale_dtype, int32_t rounding_mode,
+                        void* workspace, size_t workspace_bytes, void* stream);
+/* NVFP4 stack (two-level when aux != NULL). */
+int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, int32_t swizzled, int32_t rounding_mode,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PIPER_LORA_MERGE_H */

@@ -1,0 +1,642 @@
+/*
+ * lm_oracle.c -- CPU restatement of piper-offload's LoRA-merge hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP
+ * kernels: it is loaded by tests/, by __graft_entry__.smoke() and by the
+ * cpu_baseline leg of bench.py, never by the product path.
+ *
+ * Every function restates the arithmetic of the reference's fused Triton
+ * path (the only in-tree statement of TorchAO's rounding sequence); the
+ * citations below use the shorthand P/ = /root/reference/src/piper_offload/.
+ *
+ * Numeric conventions shared with the HIP kernels:
+ *   - the LoRA delta of one element is an fp32 sum over k = 0..r-1 in
+ *     ascending order, one fmaf per term (P/_triton_int8_lora.py:51-66 uses
+ *     tl.dot with fp32 accumulation; its order is hardware-defined, so this
+ *     is a canonical restatement -- see the tolerance contract in tests/);
+ *   - merged = round_cd(fmaf(delta, strength, base))
+ *     (P/_triton_int8_lora.py:89-93);
+ *   - stochastic rounding draws u = k * 2^-16 with k the 16-bit half-word
+ *     (idx & 7) of Philox4x32-10(ctr = (idx >> 3, 0, 0), key = seed), or the
+ *     Triton tl.rand stream (P/_triton_stochastic_quantization.py:19-22) in
+ *     compatibility mode.
+ *
+ * Build: oracle/Makefile (gcc -O2 -mfma -ffp-contract=off -fopenmp).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define EXPORT __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------ */
+/* dtype ids (must match include/lora_merge.h)                          */
+/* ------------------------------------------------------------------ */
+enum { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2, DT_E4M3 = 3, DT_E5M2 = 4, DT_E2M1 = 5, DT_E8M0 = 6, DT_I8 = 7, DT_U8 = 8 };
+enum { SR_OFF = 0, SR_PHILOX8 = 1, SR_TRITON = 2 };
+enum { MX_FLOOR = 0, MX_RCEIL = 1, MX_CEIL = 2, MX_EVEN = 3 };
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* fp32 -> bf16 round-to-nearest-even (NaN stays NaN). */
+static inline uint16_t bf16_bits(float x) {
+  uint32_t u = f2u(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+static inline float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+static inline float bf16r(float x) { return bf16_to_f32(bf16_bits(x)); }
+
+/* fp32 -> fp16 RNE with subnormals and overflow to inf. */
+static uint16_t f16_bits(float x) {
+  uint32_t u = f2u(x);
+  uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7e00u;
+  if (a >= 0x477ff000u) return sign | 0x7c00u; /* >= 65520 rounds to inf */
+  if (a < 0x38800000u) {                         /* below 2^-14: subnormal */
+    float q = fabsf(x) * 16777216.0f;            /* / 2^-24, exact scaling */
+    return sign | (uint16_t)nearbyintf(q);
+  }
+  uint32_t e = (a >> 23) - 127 + 15;
+  uint32_t m = a & 0x7fffffu;
+  uint32_t r = (e << 10) | (m >> 13);
+  uint32_t rem = m & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r += 1;
+  return sign | (uint16_t)r;
+}
+static float f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 31, m = h & 1023;
+  if (e == 0) { float v = ldexpf((float)m, -24); return (h & 0x8000u) ? -v : v; }
+  if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+  return u2f(sign | ((e - 15 + 127) << 23) | (m << 13));
+}
+static inline float f16r(float x) { return f16_to_f32(f16_bits(x)); }
+
+static inline float round_dt(int dt, float x) {
+  if (dt == DT_BF16) return bf16r(x);
+  if (dt == DT_F16) return f16r(x);
+  return x;
+}
+static inline float load_dt(int dt, const void* p, int64_t i) {
+  if (dt == DT_BF16) return bf16_to_f32(((const uint16_t*)p)[i]);
+  if (dt == DT_F16) return f16_to_f32(((const uint16_t*)p)[i]);
+  return ((const float*)p)[i];
+}
+static inline void store_dt(int dt, void* p, int64_t i, float v) {
+  if (dt == DT_BF16) ((uint16_t*)p)[i] = bf16_bits(v);
+  else if (dt == DT_F16) ((uint16_t*)p)[i] = f16_bits(v);
+  else ((float*)p)[i] = v;
+}
+
+/* ---- OCP 8-bit floats ------------------------------------------------ */
+/* decode e4m3fn: bias 7, 0x7f/0xff NaN, no inf. */
+static float e4m3_to_f32(uint8_t c) {
+  int s = c >> 7, e = (c >> 3) & 15, m = c & 7;
+  float v;
+  if (e == 15 && m == 7) v = NAN;
+  else if (e == 0) v = ldexpf((float)m, -9);
+  else v = ldexpf(1.0f + m / 8.0f, e - 7);
+  return s ? -v : v;
+}
+/* decode e5m2: bias 15, IEEE-like inf/NaN. */
+static float e5m2_to_f32(uint8_t c) {
+  int s = c >> 7, e = (c >> 2) & 31, m = c & 3;
+  float v;
+  if (e == 31) v = m ? NAN : INFINITY;
+  else if (e == 0) v = ldexpf((float)m, -16);
+  else v = ldexpf(1.0f + m / 4.0f, e - 15);
+  return s ? -v : v;
+}
+/* Generic RNE magnitude encode for a minifloat with mbits mantissa bits,
+ * exponent bias `bias`, smallest normal exponent 1-bias. Returns the code of
+ * |x| (no sign); caller guarantees |x| is within the finite range. */
+static uint8_t minifloat_mag_rne(float a, int mbits, int bias) {
+  if (a == 0.0f) return 0;
+  float min_normal = ldexpf(1.0f, 1 - bias);
+  int steps = 1 << mbits;
+  if (a < min_normal) {
+    float q = ldexpf(a, bias - 1 + mbits); /* a / subnormal step, exact */
+    return (uint8_t)nearbyintf(q);         /* == steps -> smallest normal */
+  }
+  int e2;
+  (void)frexpf(a, &e2);
+  int E = e2 - 1; /* a in [2^E, 2^(E+1)) */
+  float q = ldexpf(a, -E) * (float)steps - (float)steps;
+  int m = (int)nearbyintf(q);
+  int biased = E + bias;
+  if (m == steps) { biased += 1; m = 0; }
+  return (uint8_t)((biased << mbits) | m);
+}
+static uint8_t f32_to_e4m3(float x) { /* RNE, caller clamps to +-448 */
+  uint8_t sign = (uint8_t)((f2u(x) >> 24) & 0x80);
+  if (isnan(x)) return 0x7f | sign;
+  float a = fabsf(x);
+  if (a >= 464.0f) return 0x7f | sign;
+  return sign | minifloat_mag_rne(a, 3, 7);
+}
+static uint8_t f32_to_e5m2(float x) { /* RNE, caller clamps to +-57344 */
+  uint8_t sign = (uint8_t)((f2u(x) >> 24) & 0x80);
+  if (isnan(x)) return 0x7e | sign;
+  float a = fabsf(x);
+  if (a >= 61440.0f) return 0x7c | sign;
+  return sign | minifloat_mag_rne(a, 2, 15);
+}
+static inline float fp8_decode(int fmt, uint8_t c) { return fmt == DT_E4M3 ? e4m3_to_f32(c) : e5m2_to_f32(c); }
+static inline uint8_t fp8_encode(int fmt, float x) { return fmt == DT_E4M3 ? f32_to_e4m3(x) : f32_to_e5m2(x); }
+
+/* ---- E2M1 ------------------------------------------------------------ */
+static const float kE2M1[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+/* P/_triton_nvfp4_lora.py:24-52 */
+static inline float e2m1_to_f32(uint8_t c) { float v = kE2M1[c & 7]; return (c & 8) ? -v : v; }
+/* P/_triton_nvfp4_lora.py:55-85 (thresholds encode RNE with ties to even) */
+static inline uint8_t f32_to_e2m1(float x) {
+  float m = fabsf(x);
+  int c = m <= 0.25f ? 0 : m < 0.75f ? 1 : m <= 1.25f ? 2 : m < 1.75f ? 3 : m <= 2.5f ? 4 : m < 3.5f ? 5 : m <= 5.0f ? 6 : 7;
+  return (uint8_t)(c | ((f2u(x) >> 31) << 3));
+}
+
+/* ---- E8M0 (P/_triton_mx_lora.py:30-37) -------------------------------- */
+static inline float e8m0_to_f32(uint8_t c) {
+  if (c == 255) return NAN;
+  if (c == 0) return u2f(0x00400000u); /* 2^-127, an fp32 subnormal */
+  return u2f((uint32_t)c << 23);
+}
+
+/* ------------------------------------------------------------------ */
+/* Philox4x32 (Random123; triton/language/random.py philox_impl)         */
+/* ------------------------------------------------------------------ */
+static void philox4x32(uint32_t c[4], uint32_t k0, uint32_t k1, int rounds) {
+  for (int r = 0; r < rounds; ++r) {
+    uint32_t c0 = c[0], c2 = c[2];
+    uint64_t pb = (uint64_t)0xCD9E8D57u * c2, pa = (uint64_t)0xD2511F53u * c0;
+    c[0] = (uint32_t)(pb >> 32) ^ c[1] ^ k0;
+    c[2] = (uint32_t)(pa >> 32) ^ c[3] ^ k1;
+    c[1] = (uint32_t)pb;
+    c[3] = (uint32_t)pa;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+}
+EXPORT void lmo_philox4x32(const uint32_t* ctr, uint32_t k0, uint32_t k1, int rounds, uint32_t* out) {
+  uint32_t c[4] = {ctr[0], ctr[1], ctr[2], ctr[3]};
+  philox4x32(c, k0, k1, rounds);
+  memcpy(out, c, 16);
+}
+
+/* Uniform for the element at logical offset idx.
+ * SR_PHILOX8: one Philox call per 8 consecutive offsets, 16 bits each.
+ * SR_TRITON : triton tl.rand(seed, idx) (uint_to_uniform_float of word 0). */
+static inline float sr_uniform(int mode, uint64_t seed, uint64_t idx) {
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+  if (mode == SR_TRITON) {
+    uint32_t c[4] = {(uint32_t)idx, (uint32_t)(idx >> 32), 0, 0};
+    philox4x32(c, k0, k1, 10);
+    int32_t x = (int32_t)c[0];
+    if (x < 0) x = -x - 1;
+    return (float)x * (float)4.6566127342e-10;
+  }
+  uint64_t g = idx >> 3;
+  uint32_t c[4] = {(uint32_t)g, (uint32_t)(g >> 32), 0, 0};
+  philox4x32(c, k0, k1, 10);
+  int j = (int)(idx & 7);
+  uint32_t w = c[j >> 1];
+  uint32_t h = (j & 1) ? (w >> 16) : (w & 0xffffu);
+  return (float)h * (1.0f / 65536.0f);
+}
+EXPORT void lmo_uniforms(int mode, uint64_t seed, uint64_t start, int64_t n, float* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) out[i] = sr_uniform(mode, seed, start + (uint64_t)i);
+}
+
+/* ---- stochastic selections (P/_triton_stochastic_quantization.py) ---- */
+/* :25-40 */
+static inline int sr_int(float x, int det, float u, int qmin, int qmax) {
+  int interior = (x > (float)qmin) && (x < (float)qmax);
+  float safe = interior ? x : 0.0f;
+  float lower = floorf(safe);
+  float p = safe - lower;
+  float rounded = lower + ((u < p) ? 1.0f : 0.0f);
+  return (interior && p > 0.0f) ? (int)rounded : det;
+}
+/* :110-130 */
+static inline uint8_t sr_e2m1(float v, uint8_t det, float u) {
+  float mag = fabsf(v);
+  int nc = det & 7;
+  float nearest = kE2M1[nc];
+  int rd = nearest > mag;
+  int lo = rd ? nc - 1 : nc, hi = rd ? nc : nc + 1;
+  float lov = kE2M1[lo & 7], hiv = kE2M1[hi & 7];
+  float p = (hiv > lov) ? (mag - lov) / (hiv - lov) : 0.0f;
+  int mc = (u < p) ? hi : lo;
+  int sign = (int)((f2u(v) >> 28) & 8);
+  uint8_t chosen = (uint8_t)(mc | sign);
+  int interior = (mag > 0.0f) && (mag < 6.0f) && (p > 0.0f);
+  return interior ? chosen : det;
+}
+/* :133-177, returns the chosen 8-bit code */
+static inline uint8_t sr_fp8(int fmt, float v, float u, float limit) {
+  float mag = fabsf(v);
+  uint8_t det = fp8_encode(fmt, mag);
+  float detv = fp8_decode(fmt, det);
+  int rd = detv > mag;
+  uint8_t lo = rd ? (uint8_t)(det - 1) : det, hi = rd ? det : (uint8_t)(det + 1);
+  float lov = fp8_decode(fmt, lo), hiv = fp8_decode(fmt, hi);
+  float p = (hiv > lov) ? (mag - lov) / (hiv - lov) : 0.0f;
+  uint8_t mb = (u < p) ? hi : lo;
+  uint8_t sign = (uint8_t)((f2u(v) >> 24) & 0x80);
+  int interior = (mag < limit) && (p > 0.0f);
+  return interior ? (uint8_t)(mb | sign) : (uint8_t)(det | sign);
+}
+
+/* ------------------------------------------------------------------ */
+/* LoRA delta and dense merge                                           */
+/* ------------------------------------------------------------------ */
+/* B [M, r] row stride ldb, A [r, N] row stride lda, both in factor dtype fdt. */
+static inline float lora_delta(const void* b, int64_t ldb, const void* a, int64_t lda, int fdt, int r, int64_t row,
+                               int64_t col) {
+  float acc = 0.0f;
+  for (int k = 0; k < r; ++k) acc = fmaf(load_dt(fdt, b, row * ldb + k), load_dt(fdt, a, (int64_t)k * lda + col), acc);
+  return acc;
+}
+
+/* merged = round_cd(fmaf(delta, strength, base)); keep_zero_update reproduces
+ * the NVFP4 rule merged = (update == 0 ? base : ...) (P/_triton_nvfp4_lora.py:183-186).
+ * base and out are bf16/fp16/fp32 arrays in dtype cd, [M, N] contiguous. */
+EXPORT void lmo_merge_dense(const void* base, void* out, int cd, int64_t M, int64_t N, const void* b, int64_t ldb,
+                            const void* a, int64_t lda, int fdt, int r, float strength, int keep_zero_update) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M; ++i)
+    for (int64_t j = 0; j < N; ++j) {
+      float bv = load_dt(cd, base, i * N + j);
+      float d = r > 0 ? lora_delta(b, ldb, a, lda, fdt, r, i, j) : 0.0f;
+      float m;
+      if (keep_zero_update && d * strength == 0.0f) m = bv;
+      else m = round_dt(cd, fmaf(d, strength, bv));
+      store_dt(cd, out, i * N + j, m);
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* INT8 (TorchAO Int8Tensor; P/_triton_int8_lora.py)                    */
+/* ------------------------------------------------------------------ */
+/* dequant: P/_triton_int8_lora.py:68-87.  group = elements per qparam
+ * (N for per-row, M*N per-tensor, a divisor of N per-group). */
+EXPORT void lmo_int8_dequant(const int8_t* q, const void* scale, int scale_dt, const int8_t* zp, int64_t M, int64_t N,
+                             int64_t group, int cd, void* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M; ++i)
+    for (int64_t j = 0; j < N; ++j) {
+      int64_t f = i * N + j, qi = f / group;
+      float z = zp ? (float)zp[qi] : 0.0f;
+      float base = round_dt(cd, (float)q[f] - z);
+      base = round_dt(cd, base * load_dt(scale_dt, scale, qi));
+      store_dt(cd, out, f, base);
+    }
+}
+
+/* requant of a dense tensor (values in dtype cd): P/_triton_int8_lora.py:98-236 */
+EXPORT void lmo_int8_requant(const void* dense, int cd, int64_t M, int64_t N, int64_t group, int scale_dt, int asymmetric,
+                             int reduce_range, int sr_mode, uint64_t seed, int8_t* q_out, void* scale_out,
+                             int8_t* zp_out) {
+  int qmin = reduce_range ? -64 : -128, qmax = reduce_range ? 63 : 127;
+  int64_t numel = M * N, nq = numel / group;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t g = 0; g < nq; ++g) {
+    float mn = 0.0f, mx = 0.0f;
+    for (int64_t f = g * group; f < (g + 1) * group; ++f) {
+      float v = load_dt(cd, dense, f);
+      mn = fminf(mn, v);
+      mx = fmaxf(mx, v);
+    }
+    mn = round_dt(cd, mn);
+    mx = round_dt(cd, mx);
+    float scale;
+    if (asymmetric) {
+      float range = round_dt(cd, mx - mn);
+      scale = range / (float)(qmax - qmin);
+    } else {
+      scale = fmaxf(-mn, mx) / ((float)(qmax - qmin) / 2.0f);
+    }
+    scale = round_dt(cd, scale);
+    scale = fmaxf(scale, 1.1920928955078125e-07f);
+    scale = round_dt(cd, scale);
+    int zp = 0;
+    if (asymmetric) {
+      float ratio = round_dt(cd, mn / scale);
+      zp = qmin - (int)nearbyintf(ratio);
+      zp = zp < qmin ? qmin : (zp > qmax ? qmax : zp);
+    }
+    store_dt(scale_dt, scale_out, g, scale);
+    if (zp_out) zp_out[g] = (int8_t)zp;
+    float s = load_dt(scale_dt, scale_out, g); /* quantize reads the stored qparam */
+    float inv = round_dt(scale_dt, 1.0f / s);
+    for (int64_t f = g * group; f < (g + 1) * group; ++f) {
+      float v = load_dt(cd, dense, f);
+      float scaled = round_dt(scale_dt, v * inv);
+      int qv = isnan(scaled) ? 0 : (int)nearbyintf(scaled);
+      qv += zp;
+      if (sr_mode != SR_OFF) {
+        float x = v / s + (float)zp;
+        qv = sr_int(x, qv, sr_uniform(sr_mode, seed, (uint64_t)f), qmin, qmax);
+      }
+      q_out[f] = (int8_t)(qv < qmin ? qmin : (qv > qmax ? qmax : qv));
+    }
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* Scaled FP8 (TorchAO Float8Tensor; P/_triton_float8_lora.py)          */
+/* ------------------------------------------------------------------ */
+/* dequant P/_triton_float8_lora.py:72-85; scale fp32 per group (N = per-row). */
+EXPORT void lmo_fp8_dequant(const uint8_t* q, int fmt, const float* scale, int64_t M, int64_t N, int64_t group, int cd,
+                            void* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t f = 0; f < M * N; ++f) store_dt(cd, out, f, round_dt(cd, fp8_decode(fmt, q[f]) * scale[f / group]));
+}
+/* requant: scale = round_cd(amax/limit), 0 -> 2^-23 (:249-271); quantize
+ * dense/scale clamped to +-limit, optional SR, RNE cast (:275-308). */
+EXPORT void lmo_fp8_requant(const void* dense, int cd, int64_t M, int64_t N, int64_t group, int fmt, int sr_mode,
+                            uint64_t seed, uint8_t* q_out, float* scale_out) {
+  float limit = fmt == DT_E4M3 ? 448.0f : 57344.0f;
+  int64_t nq = (M * N) / group;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t g = 0; g < nq; ++g) {
+    float amax = 0.0f;
+    for (int64_t f = g * group; f < (g + 1) * group; ++f) amax = fmaxf(amax, fabsf(load_dt(cd, dense, f)));
+    float scale = round_dt(cd, amax / limit);
+    if (scale == 0.0f) scale = 1.1920928955078125e-07f;
+    scale_out[g] = scale;
+    for (int64_t f = g * group; f < (g + 1) * group; ++f) {
+      float x = load_dt(cd, dense, f) / scale;
+      x = fminf(fmaxf(x, -limit), limit);
+      if (sr_mode != SR_OFF) q_out[f] = sr_fp8(fmt, x, sr_uniform(sr_mode, seed, (uint64_t)f), limit);
+      else q_out[f] = fp8_encode(fmt, x);
+    }
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* NVFP4 (TorchAO NVFP4Tensor; P/_triton_nvfp4_lora.py)                 */
+/* ------------------------------------------------------------------ */
+/* P/_triton_nvfp4_lora.py:88-104 */
+EXPORT int64_t lmo_blocked_scale_offset(int64_t row, int64_t scale_col, int64_t scale_cols, int swizzled) {
+  if (!swizzled) return row * scale_cols + scale_col;
+  int64_t ncb = (scale_cols + 3) / 4;
+  int64_t rb = row / 128, rib = row % 128, cb = scale_col / 4, cib = scale_col % 4;
+  return (rb * ncb + cb) * 512 + (rib % 32) * 16 + (rib / 32) * 4 + cib;
+}
+
+/* dequant P/_triton_nvfp4_lora.py:133-163. pts = per-tensor scale or NULL. */
+EXPORT void lmo_nvfp4_dequant(const uint8_t* q, const uint8_t* scale, const float* pts, int64_t M, int64_t N, int swizzled,
+                              int cd, void* out) {
+  int64_t sc = N / 16;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M; ++i)
+    for (int64_t j = 0; j < N; ++j) {
+      uint8_t byte = q[i * (N / 2) + j / 2];
+      uint8_t code = (j & 1) ? (byte >> 4) : (byte & 15);
+      float bs = e4m3_to_f32(scale[lmo_blocked_scale_offset(i, j / 16, sc, swizzled)]);
+      if (cd == DT_BF16) bs = bf16r(bs);
+      if (pts) {
+        bs = bs * pts[0];
+        if (cd == DT_BF16) bs = bf16r(bs);
+      }
+      float base = e2m1_to_f32(code) * bs;
+      if (cd == DT_BF16) base = bf16r(base);
+      store_dt(cd, out, i * N + j, base);
+    }
+}
+
+/* requant of merged dense (P/_triton_nvfp4_lora.py:251-367).
+ * two_level: recompute g' = max(amax/2688, 2^-23) into *pts_out.
+ * scale_out must be pre-zeroed by the caller for swizzled padding. */
+EXPORT void lmo_nvfp4_requant(const void* dense, int cd, int64_t M, int64_t N, int swizzled, int two_level, int sr_mode,
+                              uint64_t seed, uint8_t* q_out, uint8_t* scale_out, float* pts_out) {
+  int64_t sc = N / 16;
+  float g = 1.0f;
+  if (two_level) {
+    float amax = 0.0f;
+    for (int64_t f = 0; f < M * N; ++f) amax = fmaxf(amax, fabsf(load_dt(cd, dense, f)));
+    g = fmaxf(amax / 2688.0f, 1.1920928955078125e-07f);
+    *pts_out = g;
+  }
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M; ++i)
+    for (int64_t b = 0; b < sc; ++b) {
+      float v[16], bmax = 0.0f;
+      for (int t = 0; t < 16; ++t) {
+        v[t] = load_dt(cd, dense, i * N + b * 16 + t);
+        bmax = fmaxf(bmax, fabsf(v[t]));
+      }
+      float bscale = bmax / 6.0f;
+      float fs = two_level ? bscale / g : bscale;
+      fs = fminf(fmaxf(fs, 0.015625f), 448.0f);
+      uint8_t sc8 = f32_to_e4m3(fs);
+      fs = e4m3_to_f32(sc8);
+      scale_out[lmo_blocked_scale_offset(i, b, sc, swizzled)] = sc8;
+      float recip = two_level ? (1.0f / g) / fs : 0.0f;
+      uint8_t codes[16];
+      for (int t = 0; t < 16; ++t) {
+        float nrm = two_level ? v[t] * recip : v[t] / fs;
+        nrm = fminf(fmaxf(nrm, -6.0f), 6.0f);
+        uint8_t c = f32_to_e2m1(nrm);
+        if (sr_mode != SR_OFF) c = sr_e2m1(nrm, c, sr_uniform(sr_mode, seed, (uint64_t)(i * N + b * 16 + t)));
+        codes[t] = c;
+      }
+      for (int t = 0; t < 8; ++t) q_out[i * (N / 2) + b * 8 + t] = (uint8_t)(codes[2 * t] | (codes[2 * t + 1] << 4));
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* MX (TorchAO MXTensor; P/_triton_mx_lora.py)                          */
+/* ------------------------------------------------------------------ */
+static void mx_params(int fmt, int* emax, float* maxpos, int* mbits) {
+  if (fmt == DT_E4M3) { *emax = 8; *maxpos = 448.0f; *mbits = 3; }
+  else if (fmt == DT_E5M2) { *emax = 15; *maxpos = 57344.0f; *mbits = 2; }
+  else { *emax = 2; *maxpos = 6.0f; *mbits = 1; }
+}
+/* P/_triton_mx_lora.py:97-112 (scale tile 128 rows x 4 scale columns) */
+static inline int64_t mx_scale_offset(int64_t row, int64_t blk, int64_t nblk, int swizzled) {
+  return lmo_blocked_scale_offset(row, blk, nblk, swizzled);
+}
+/* exact ceil(log2(x)) for finite x > 0 */
+static int ceil_log2_exact(float x) {
+  int e;
+  float m = frexpf(x, &e); /* x = m * 2^e, m in [0.5, 1) */
+  return (m == 0.5f) ? e - 1 : e;
+}
+/* P/_triton_mx_lora.py:115-159; returns code, writes inverse scale */
+static uint8_t mx_scale(float max_abs, int mode, int emax, float maxpos, int mbits, float* inv) {
+  if (mode == MX_RCEIL) {
+    float descale = max_abs / maxpos;
+    float unb;
+    if (isnan(descale)) { *inv = NAN; return 255; }
+    if (descale == 0.0f) unb = -127.0f;
+    else if (isinf(descale)) unb = 127.0f;
+    else unb = (float)ceil_log2_exact(descale);
+    unb = fminf(fmaxf(unb, -127.0f), 127.0f);
+    uint8_t enc = (uint8_t)(unb + 127.0f);
+    *inv = enc == 0 ? 1.0f : ldexpf(1.0f, -(int)unb);
+    return enc;
+  }
+  uint32_t bits = f2u(max_abs);
+  if (mode == MX_EVEN) {
+    uint32_t bias = mbits == 3 ? 524288u : (mbits == 2 ? 1048576u : 2097152u);
+    bits = (bits + bias) & 0xff800000u;
+  }
+  int ex = (int)((bits >> 23) & 255) - 127;
+  if (mode == MX_CEIL) ex += (bits & 0x7fffffu) > 0;
+  int unb = ex - emax;
+  unb = unb < -127 ? -127 : (unb > 128 ? 128 : unb);
+  uint8_t enc = (uint8_t)(unb + 127);
+  if (isnan(max_abs)) enc = 255;
+  float scale = u2f((uint32_t)enc << 23);
+  scale = fmaxf(scale, 1.1754943508222875e-38f);
+  *inv = 1.0f / scale;
+  return enc;
+}
+/* dequant P/_triton_mx_lora.py:209-242 */
+EXPORT void lmo_mx_dequant(const uint8_t* q, const uint8_t* scale, int fmt, int64_t M, int64_t N, int swizzled, int cd,
+                           void* out) {
+  int64_t nblk = N / 32;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M; ++i)
+    for (int64_t j = 0; j < N; ++j) {
+      float lp;
+      if (fmt == DT_E2M1) {
+        uint8_t byte = q[i * (N / 2) + j / 2];
+        lp = e2m1_to_f32((j & 1) ? (byte >> 4) : (byte & 15));
+      } else {
+        lp = fp8_decode(fmt, q[i * N + j]);
+      }
+      float s = e8m0_to_f32(scale[mx_scale_offset(i, j / 32, nblk, swizzled)]);
+      float base = (cd == DT_BF16) ? bf16r(bf16r(lp) * bf16r(s)) : lp * s;
+      store_dt(cd, out, i * N + j, base);
+    }
+}
+/* requant P/_triton_mx_lora.py:248-295 (writes qdata + scale). */
+EXPORT void lmo_mx_requant(const void* dense, int cd, int64_t M, int64_t N, int fmt, int mode, int swizzled, int sr_mode,
+                           uint64_t seed, uint8_t* q_out, uint8_t* scale_out) {
+  int emax, mbits;
+  float maxpos;
+  mx_params(fmt, &emax, &maxpos, &mbits);
+  int64_t nblk = N / 32;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M; ++i)
+    for (int64_t b = 0; b < nblk; ++b) {
+      float v[32], amax = 0.0f;
+      for (int t = 0; t < 32; ++t) {
+        v[t] = load_dt(cd, dense, i * N + b * 32 + t);
+        amax = fmaxf(amax, fabsf(v[t]));
+      }
+      float inv;
+      uint8_t enc = mx_scale(amax, mode, emax, maxpos, mbits, &inv);
+      scale_out[mx_scale_offset(i, b, nblk, swizzled)] = enc;
+      uint8_t codes[32];
+      for (int t = 0; t < 32; ++t) {
+        float nrm = v[t] * inv;
+        nrm = fminf(fmaxf(nrm, -maxpos), maxpos);
+        uint64_t idx = (uint64_t)(i * N + b * 32 + t);
+        if (fmt == DT_E2M1) {
+          uint8_t c = f32_to_e2m1(nrm);
+          if (sr_mode != SR_OFF) c = sr_e2m1(nrm, c, sr_uniform(sr_mode, seed, idx));
+          codes[t] = c;
+        } else {
+          uint8_t c = (sr_mode != SR_OFF) ? sr_fp8(fmt, nrm, sr_uniform(sr_mode, seed, idx), maxpos) : fp8_encode(fmt, nrm);
+          q_out[i * N + b * 32 + t] = c;
+        }
+      }
+      if (fmt == DT_E2M1)
+        for (int t = 0; t < 16; ++t) q_out[i * (N / 2) + b * 16 + t] = (uint8_t)(codes[2 * t] | (codes[2 * t + 1] << 4));
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* GGUF Q8_0                                                            */
+/* ------------------------------------------------------------------ */
+/* dequant: P/gguf_dequant.py:57-61 with dtype bf16: out = bf16(bf16(d) * q) */
+EXPORT void lmo_q8_0_dequant(const uint8_t* packed, int64_t M, int64_t N, int cd, void* out) {
+  int64_t nb = N / 32, rowbytes = nb * 34;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M; ++i)
+    for (int64_t b = 0; b < nb; ++b) {
+      const uint8_t* blk = packed + i * rowbytes + b * 34;
+      uint16_t dh;
+      memcpy(&dh, blk, 2);
+      float d = round_dt(cd, f16_to_f32(dh));
+      for (int t = 0; t < 32; ++t) store_dt(cd, out, i * N + b * 32 + t, round_dt(cd, d * (float)(int8_t)blk[2 + t]));
+    }
+}
+/* requant: ggml quantize_row_q8_0_ref (MIT): d = amax/127, id = d ? 1/d : 0,
+ * q = roundf(x*id) (half away from zero), store fp16(d). SR (an extension: the
+ * reference routes GGUF only) selects floor/ceil of x*id with P(up) = frac. */
+EXPORT void lmo_q8_0_requant(const void* dense, int cd, int64_t M, int64_t N, int sr_mode, uint64_t seed,
+                             uint8_t* packed_out) {
+  int64_t nb = N / 32, rowbytes = nb * 34;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M; ++i)
+    for (int64_t b = 0; b < nb; ++b) {
+      float v[32], amax = 0.0f;
+      for (int t = 0; t < 32; ++t) {
+        v[t] = load_dt(cd, dense, i * N + b * 32 + t);
+        amax = fmaxf(amax, fabsf(v[t]));
+      }
+      float d = amax / 127.0f;
+      float id = d != 0.0f ? 1.0f / d : 0.0f;
+      uint8_t* blk = packed_out + i * rowbytes + b * 34;
+      uint16_t dh = f16_bits(d);
+      memcpy(blk, &dh, 2);
+      for (int t = 0; t < 32; ++t) {
+        float x = v[t] * id;
+        int qv = (int)roundf(x);
+        if (sr_mode != SR_OFF) qv = sr_int(x, qv, sr_uniform(sr_mode, seed, (uint64_t)(i * N + b * 32 + t)), -127, 127);
+        blk[2 + t] = (uint8_t)(int8_t)qv;
+      }
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* small codec entry points (for exhaustive tests)                      */
+/* ------------------------------------------------------------------ */
+EXPORT void lmo_f32_to_bf16(const float* x, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = bf16_bits(x[i]);
+}
+EXPORT void lmo_f32_to_f16(const float* x, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f16_bits(x[i]);
+}
+EXPORT void lmo_f16_to_f32(const uint16_t* x, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f16_to_f32(x[i]);
+}
+EXPORT void lmo_f32_to_fp8(int fmt, const float* x, uint8_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = fp8_encode(fmt, x[i]);
+}
+EXPORT void lmo_fp8_to_f32(int fmt, const uint8_t* x, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = fp8_decode(fmt, x[i]);
+}
+EXPORT void lmo_f32_to_e2m1(const float* x, uint8_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f32_to_e2m1(x[i]);
+}
+EXPORT void lmo_e8m0_to_f32(const uint8_t* x, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = e8m0_to_f32(x[i]);
+}
+EXPORT void lmo_mx_scale(const float* amax, int64_t n, int fmt, int mode, uint8_t* codes, float* inv) {
+  int emax, mbits;
+  float maxpos;
+  mx_params(fmt, &emax, &maxpos, &mbits);
+  for (int64_t i = 0; i < n; ++i) codes[i] = mx_scale(amax[i], mode, emax, maxpos, mbits, &inv[i]);
+}
+EXPORT void lmo_sr_int(const float* x, const int32_t* det, const float* u, int64_t n, int qmin, int qmax, int32_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = sr_int(x[i], det[i], u[i], qmin, qmax);
+}
+EXPORT void lmo_sr_e2m1(const float* x, const uint8_t* det, const float* u, int64_t n, uint8_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = sr_e2m1(x[i], det[i], u[i]);
+}
+EXPORT void lmo_sr_fp8(int fmt, const float* x, const float* u, int64_t n, float limit, uint8_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = sr_fp8(fmt, x[i], u[i], limit);
+}
+EXPORT int lmo_version(void) { return 1; }

@@ -1,0 +1,341 @@
+// lm_device.h -- gfx950 device building blocks for the LoRA-merge kernels.
+//
+// Numerics follow the reference's fused Triton path (P/ = the reference's
+// src/piper_offload/):
+//   * bf16 rounding uses v_cvt_pk_bf16_f32 (RNE);
+//   * fp8 e4m3fn / e5m2 encodes use v_cvt_pk_{fp8,bf8}_f32 (RNE, the values
+//     are clamped to the finite range first, P/_triton_float8_lora.py:295-299);
+//   * e2m1 encodes use v_cvt_scalef32_pk_fp4_f32 with scale 1.0, which is
+//     round-to-nearest-even and therefore identical to the threshold chain of
+//     P/_triton_nvfp4_lora.py:55-85;
+//   * the per-element quotient v / s (INT8 stochastic rounding, FP8 and
+//     single-level NVFP4 quantization) is the IEEE-correct quotient computed
+//     as q0 = v*r, e = fma(-q0, s, v), q1 = fma(e, r, q0) with r = RN(1/s);
+//     this equals RN(v/s) for all bf16 and fp16 operands whose magnitudes
+//     and quotient lie in [2^-100, 2^100] (exhaustively checked on the CPU),
+//     the sign of a zero quotient is restored with copysign.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define DEV __device__ __forceinline__
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef _Float16 v4f16 __attribute__((ext_vector_type(4)));
+typedef float v4f32 __attribute__((ext_vector_type(4)));
+
+namespace lm {
+
+enum : int { F32 = 0, BF16 = 1, F16 = 2, E4M3 = 3, E5M2 = 4, E2M1 = 5, E8M0 = 6 };
+enum : int { MX_FLOOR = 0, MX_RCEIL = 1, MX_CEIL = 2, MX_EVEN = 3 };
+
+constexpr float kEps = 1.1920928955078125e-07f;  // torch.finfo(float32).eps
+
+DEV uint32_t f2u(float x) { return __float_as_uint(x); }
+DEV float u2f(uint32_t x) { return __uint_as_float(x); }
+
+DEV uint16_t bf16_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+DEV float bf16_val(uint32_t h) { return u2f(h << 16); }
+DEV float bf16r(float x) { return bf16_val(bf16_bits(x)); }
+DEV uint16_t f16_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+DEV float f16_val(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+DEV float f16r(float x) { return f16_val(f16_bits(x)); }
+
+template <int DT>
+DEV float round_dt(float x) {
+  if constexpr (DT == BF16) return bf16r(x);
+  else if constexpr (DT == F16) return f16r(x);
+  else return x;
+}
+template <int DT>
+DEV uint16_t bits_dt(float x) {
+  if constexpr (DT == F16) return f16_bits(x);
+  else return bf16_bits(x);
+}
+template <int DT>
+DEV float val_dt(uint32_t h) {
+  if constexpr (DT == F16) return f16_val(h);
+  else return bf16_val(h);
+}
+// load one element of a runtime-dtype scalar array (f32 / bf16 / f16)
+DEV float load_scalar(const void* p, int64_t i, int dt) {
+  if (dt == BF16) return bf16_val(((const uint16_t*)p)[i]);
+  if (dt == F16) return f16_val(((const uint16_t*)p)[i]);
+  return ((const float*)p)[i];
+}
+DEV void store_scalar(void* p, int64_t i, int dt, float v) {
+  if (dt == BF16) ((uint16_t*)p)[i] = bf16_bits(v);
+  else if (dt == F16) ((uint16_t*)p)[i] = f16_bits(v);
+  else ((float*)p)[i] = v;
+}
+DEV float round_runtime(float x, int dt) {
+  if (dt == BF16) return bf16r(x);
+  if (dt == F16) return f16r(x);
+  return x;
+}
+
+// RN(v / s) given r = RN(1/s); see header comment for the validity domain.
+DEV float div_rn(float v, float s, float r) {
+  float q0 = v * r;
+  float e = __builtin_fmaf(-q0, s, v);
+  float q1 = __builtin_fmaf(e, r, q0);
+  return __builtin_copysignf(q1, q0);
+}
+
+// ---- 8-bit floats -----------------------------------------------------
+template <int FMT>
+DEV float fp8_decode(uint32_t word, int byte) {
+  if constexpr (FMT == E4M3) {
+    switch (byte) {
+      case 0: return __builtin_amdgcn_cvt_f32_fp8(word, 0);
+      case 1: return __builtin_amdgcn_cvt_f32_fp8(word, 1);
+      case 2: return __builtin_amdgcn_cvt_f32_fp8(word, 2);
+      default: return __builtin_amdgcn_cvt_f32_fp8(word, 3);
+    }
+  } else {
+    switch (byte) {
+      case 0: return __builtin_amdgcn_cvt_f32_bf8(word, 0);
+      case 1: return __builtin_amdgcn_cvt_f32_bf8(word, 1);
+      case 2: return __builtin_amdgcn_cvt_f32_bf8(word, 2);
+      default: return __builtin_amdgcn_cvt_f32_bf8(word, 3);
+    }
+  }
+}
+// pack 4 values (already clamped to the finite range) to 4 fp8 codes, RNE
+template <int FMT>
+DEV uint32_t fp8_pack4(float a, float b, float c, float d) {
+  if constexpr (FMT == E4M3) {
+    uint32_t w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  } else {
+    uint32_t w = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
+    return __builtin_amdgcn_cvt_pk_bf8_f32(c, d, w, true);
+  }
+}
+template <int FMT>
+DEV uint32_t fp8_encode1(float a) {
+  if constexpr (FMT == E4M3) return __builtin_amdgcn_cvt_pk_fp8_f32(a, a, 0, false) & 0xffu;
+  else return __builtin_amdgcn_cvt_pk_bf8_f32(a, a, 0, false) & 0xffu;
+}
+template <int FMT>
+DEV float fp8_value(uint32_t code) {  // decode one code held in the low byte
+  return fp8_decode<FMT>(code, 0);
+}
+
+// ---- e2m1 ---------------------------------------------------------------
+DEV float e2m1_mag(uint32_t m) {  // m in 0..7 -> 0,0.5,1,1.5,2,3,4,6
+  uint32_t bits = m == 0 ? 0u : (m == 1 ? 0x3f000000u : ((((m >> 1) + 126u) << 23) | ((m & 1u) << 22)));
+  return u2f(bits);
+}
+DEV float e2m1_value(uint32_t code) {
+  float v = e2m1_mag(code & 7u);
+  return (code & 8u) ? -v : v;
+}
+// two values -> two e2m1 codes in the low byte (first value in the low nibble)
+DEV uint32_t e2m1_pack2(float a, float b) {
+  return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, a, b, 1.0f, 0) & 0xffu;
+}
+
+// ---- e8m0 (P/_triton_mx_lora.py:30-37) -------------------------------
+DEV float e8m0_value(uint32_t c) {
+  if (c == 255u) return __builtin_nanf("");
+  if (c == 0u) return u2f(0x00400000u);
+  return u2f(c << 23);
+}
+
+// ---- Philox4x32-10 (Random123; triton.language.random.philox_impl) -----
+DEV void philox10(uint64_t ctr, uint64_t seed, uint32_t (&c)[4]) {
+  c[0] = (uint32_t)ctr;
+  c[1] = (uint32_t)(ctr >> 32);
+  c[2] = 0;
+  c[3] = 0;
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    uint32_t c0 = c[0], c2 = c[2];
+    uint32_t hb = __umulhi(0xCD9E8D57u, c2), ha = __umulhi(0xD2511F53u, c0);
+    uint32_t lb = 0xCD9E8D57u * c2, la = 0xD2511F53u * c0;
+    c[0] = hb ^ c[1] ^ k0;
+    c[2] = ha ^ c[3] ^ k1;
+    c[1] = lb;
+    c[3] = la;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+}
+// 16-bit uniform integers h for offsets idx0 .. idx0+SPAN-1 (u = h * 2^-16)
+template <int SPAN>
+DEV void sr_bits(uint64_t seed, uint64_t idx0, uint32_t (&h)[SPAN]) {
+  if ((idx0 & 7u) == 0) {
+#pragma unroll
+    for (int gi = 0; gi < SPAN / 8; ++gi) {
+      uint32_t c[4];
+      philox10((idx0 >> 3) + gi, seed, c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[gi * 8 + j] = (j & 1) ? (c[j >> 1] >> 16) : (c[j >> 1] & 0xffffu);
+    }
+  } else {
+    for (int j = 0; j < SPAN; ++j) {
+      uint64_t idx = idx0 + j;
+      uint32_t c[4];
+      philox10(idx >> 3, seed, c);
+      int jj = (int)(idx & 7);
+      h[j] = (jj & 1) ? (c[jj >> 1] >> 16) : (c[jj >> 1] & 0xffffu);
+    }
+  }
+}
+// u < p with u = h * 2^-16 (exact: both sides scaled by 2^16)
+DEV bool sr_up(uint32_t h, float p) { return (float)h < p * 65536.0f; }
+
+// ---- stochastic selections (P/_triton_stochastic_quantization.py) --------
+// :25-40
+DEV int sr_int(float x, int det, uint32_t h, float qmin, float qmax) {
+  bool interior = (x > qmin) && (x < qmax);
+  float safe = interior ? x : 0.0f;
+  float lower = __builtin_floorf(safe);
+  float p = safe - lower;
+  float rounded = lower + (sr_up(h, p) ? 1.0f : 0.0f);
+  return (interior && p > 0.0f) ? (int)rounded : det;
+}
+// :110-130 ; det = RTN code (sign in bit 3)
+DEV uint32_t sr_e2m1(float v, uint32_t det, uint32_t h) {
+  float mag = __builtin_fabsf(v);
+  uint32_t nc = det & 7u;
+  float nearest = e2m1_mag(nc);
+  bool rd = nearest > mag;
+  uint32_t lo = rd ? nc - 1 : nc, hi = rd ? nc : nc + 1;
+  float lov = e2m1_mag(lo & 7u), hiv = e2m1_mag(hi & 7u);
+  float p = (hiv > lov) ? (mag - lov) / (hiv - lov) : 0.0f;
+  uint32_t mc = sr_up(h, p) ? hi : lo;
+  uint32_t sign = (f2u(v) >> 28) & 8u;
+  bool interior = (mag > 0.0f) && (mag < 6.0f) && (p > 0.0f);
+  return interior ? ((mc | sign) & 15u) : det;
+}
+// :133-177 ; returns the chosen code
+template <int FMT>
+DEV uint32_t sr_fp8(float v, uint32_t h, float limit) {
+  float mag = __builtin_fabsf(v);
+  uint32_t det = fp8_encode1<FMT>(mag);
+  float detv = fp8_value<FMT>(det);
+  bool rd = detv > mag;
+  uint32_t lo = rd ? ((det - 1u) & 0xffu) : det, hi = rd ? det : ((det + 1u) & 0xffu);
+  float lov = fp8_value<FMT>(lo), hiv = fp8_value<FMT>(hi);
+  float p = (hiv > lov) ? (mag - lov) / (hiv - lov) : 0.0f;
+  uint32_t mb = sr_up(h, p) ? hi : lo;
+  uint32_t sign = (f2u(v) >> 24) & 0x80u;
+  bool interior = (mag < limit) && (p > 0.0f);
+  return interior ? (mb | sign) : (det | sign);
+}
+
+// ---- blocked (swizzled) scale offsets: P/_triton_nvfp4_lora.py:88-104,
+//      P/_triton_mx_lora.py:97-112 --------------------------------------
+DEV int64_t blocked_offset(int64_t row, int64_t scol, int64_t scols, bool swz) {
+  if (!swz) return row * scols + scol;
+  int64_t ncb = (scols + 3) >> 2;
+  int64_t rb = row >> 7, rib = row & 127, cb = scol >> 2, cib = scol & 3;
+  return (rb * ncb + cb) * 512 + (rib & 31) * 16 + (rib >> 5) * 4 + cib;
+}
+
+// ---- MX scale (P/_triton_mx_lora.py:115-159) -----------------------------
+DEV uint32_t mx_scale(float max_abs, int mode, int emax, float maxpos, int mbits, float& inv) {
+  if (mode == MX_RCEIL) {
+    float descale = max_abs / maxpos;
+    if (descale != descale) {
+      inv = __builtin_nanf("");
+      return 255u;
+    }
+    int unb;
+    if (descale == 0.0f) unb = -127;
+    else if (__builtin_isinf(descale)) unb = 127;
+    else {
+      int e;
+      float m = __builtin_frexpf(descale, &e);
+      unb = (m == 0.5f) ? e - 1 : e;  // exact ceil(log2(descale))
+    }
+    unb = unb < -127 ? -127 : (unb > 127 ? 127 : unb);
+    uint32_t enc = (uint32_t)(unb + 127);
+    inv = enc == 0 ? 1.0f : __builtin_ldexpf(1.0f, -unb);
+    return enc;
+  }
+  uint32_t bits = f2u(max_abs);
+  if (mode == MX_EVEN) {
+    uint32_t bias = mbits == 3 ? 524288u : (mbits == 2 ? 1048576u : 2097152u);
+    bits = (bits + bias) & 0xff800000u;
+  }
+  int ex = (int)((bits >> 23) & 255u) - 127;
+  if (mode == MX_CEIL) ex += (bits & 0x7fffffu) > 0 ? 1 : 0;
+  int unb = ex - emax;
+  unb = unb < -127 ? -127 : (unb > 128 ? 128 : unb);
+  uint32_t enc = (uint32_t)(unb + 127);
+  if (max_abs != max_abs) enc = 255u;
+  float scale = u2f(enc << 23);
+  scale = __builtin_fmaxf(scale, 1.1754943508222875e-38f);
+  inv = 1.0f / scale;
+  return enc;
+}
+
+// ---- MFMA tile engine ---------------------------------------------------
+// Layout of the prepared factors (written by the prep kernel):
+//   At[col][g][kc][i] = A[kc*16 + 4g + i][col]   (zero for k >= rank)
+//   Bp[row][g][kc][i] = B[row][kc*16 + 4g + i]
+// A wavefront owns 16 weight rows; lane l holds row (l & 15) and, inside a
+// macro tile of 4*SPAN columns, the SPAN consecutive columns starting at
+// SPAN*(l >> 4).  The MFMA computes D^T (positions x rows): position p of
+// MFMA t maps to column SPAN*(p >> 2) + 4t + (p & 3), so the four fp32
+// results of MFMA t in lane l are columns SPAN*(l>>4) + 4t + 0..3.
+template <int NKC, bool F16>
+DEV v4f32 mfma_chain(const v4i16 (&a)[NKC], const v4i16 (&b)[NKC]) {
+  v4f32 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int kc = 0; kc < NKC; ++kc) {
+    if constexpr (F16)
+      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4f16, a[kc]), __builtin_bit_cast(v4f16, b[kc]),
+                                                  acc, 0, 0, 0);
+    else
+      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a[kc], b[kc], acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+template <int NKC>
+DEV void load_kchunks(const uint16_t* __restrict__ p, v4i16 (&out)[NKC]) {
+  if constexpr (NKC == 1) {
+    uint2 w = *(const uint2*)p;
+    out[0] = __builtin_bit_cast(v4i16, w);
+  } else {
+#pragma unroll
+    for (int h = 0; h < NKC / 2; ++h) {
+      uint4 w = *(const uint4*)(p + 8 * h);
+      uint2 lo = make_uint2(w.x, w.y), hi = make_uint2(w.z, w.w);
+      out[2 * h] = __builtin_bit_cast(v4i16, lo);
+      out[2 * h + 1] = __builtin_bit_cast(v4i16, hi);
+    }
+  }
+}
+
+// delta for the lane's SPAN columns of the macro tile starting at mt_col0
+template <int SPAN, int NKC, bool F16>
+DEV void tile_delta(const uint16_t* __restrict__ at, int64_t mt_col0, int lane, const v4i16 (&bop)[NKC],
+                    float (&d)[SPAN]) {
+  constexpr int T = SPAN / 4;
+  constexpr int RPAD = NKC * 16;
+  const int p = lane & 15, g = lane >> 4;
+  const int64_t colbase = mt_col0 + SPAN * (p >> 2) + (p & 3);
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    v4i16 aop[NKC];
+    load_kchunks<NKC>(at + (colbase + 4 * t) * RPAD + g * (NKC * 4), aop);
+    v4f32 acc = mfma_chain<NKC, F16>(aop, bop);
+    d[4 * t + 0] = acc[0];
+    d[4 * t + 1] = acc[1];
+    d[4 * t + 2] = acc[2];
+    d[4 * t + 3] = acc[3];
+  }
+}
+
+template <int NKC>
+DEV void load_bop(const uint16_t* __restrict__ bp, int64_t row, int lane, v4i16 (&bop)[NKC]) {
+  load_kchunks<NKC>(bp + row * (NKC * 16) + (lane >> 4) * (NKC * 4), bop);
+}
+
+}  // namespace lm

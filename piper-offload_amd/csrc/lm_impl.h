@@ -1,0 +1,1146 @@
+#pragma once
+// lm_impl.h -- MI355X (gfx950) kernels and C ABI for piper-offload's
+// LoRA-merge hot path.  See include/lora_merge.h for the entry points and
+// the reference functions each one replaces (P/ = src/piper_offload/).
+//
+// Kernel families
+//   k_prep      : stages B and A into the MFMA-ready layouts Bp / At and
+//                 clears the reduction slots (one launch per call or stack).
+//   k_rows      : per-row qparam formats (INT8 per-row, scaled FP8 per-row).
+//                 One workgroup owns 16 full rows; its waves split the
+//                 columns, keep merged bf16 values of up to CACHE macro tiles
+//                 in registers, reduce the row amax/min through LDS, then
+//                 quantize (recomputing tiles that did not fit the cache).
+//   k_blocks    : block-local formats (NVFP4 block 16, MX block 32, GGUF
+//                 Q8_0 block 32), dense bf16 weights, dequantize-to-dense,
+//                 and the two passes of per-tensor / two-level formats.
+// Every element's delta comes from the same MFMA chain (tile_delta), so a
+// fused merge and the dense merge of the same inputs see identical values.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/lora_merge.h"
+#include "lm_device.h"
+
+using namespace lm;
+
+// ---------------------------------------------------------------------------
+// error plumbing (thread-local message, defined in lm_common.hip)
+// ---------------------------------------------------------------------------
+int lm_fail_v(int code, const char* fmt, va_list ap);
+static inline int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+static inline int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  int rc = lm_fail_v(code, fmt, ap);
+  va_end(ap);
+  return rc;
+}
+#define HIP_TRY(expr)                                                                        \
+  do {                                                                                       \
+    hipError_t e_ = (expr);                                                                  \
+    if (e_ != hipSuccess) return fail(LM_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+#define LAUNCH_CHECK() HIP_TRY(hipGetLastError())
+
+// ---------------------------------------------------------------------------
+// workspace layout (per tensor): At | Bp | reduction slots
+// ---------------------------------------------------------------------------
+static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+static inline int rpad_of(int rank) { return rank <= 0 ? 0 : (rank <= 16 ? 16 : (rank <= 32 ? 32 : 64)); }
+static inline int64_t npad_of(int64_t N) { return (N + 127) / 128 * 128; }
+static inline int64_t mpad_of(int64_t M) { return (M + 15) / 16 * 16; }
+
+struct WsLayout {
+  size_t at_off, bp_off, red_off, total;
+};
+static WsLayout ws_layout(int64_t M, int64_t N, int rank) {
+  WsLayout w;
+  int rp = rpad_of(rank);
+  w.at_off = 0;
+  w.bp_off = align256((size_t)npad_of(N) * rp * 2);
+  w.red_off = w.bp_off + align256((size_t)mpad_of(M) * rp * 2);
+  w.total = w.red_off + 256;
+  return w;
+}
+
+// ---------------------------------------------------------------------------
+// prep: factors -> MFMA-ready layouts, clear reduction slots
+// ---------------------------------------------------------------------------
+struct PrepItem {
+  const uint16_t* b;
+  const uint16_t* a;
+  int64_t ldb, lda;
+  int64_t M, N;
+  int rank, rpad;
+  uint16_t* at;
+  uint16_t* bp;
+  uint32_t* red;
+  int64_t work_begin;  // prefix of per-item work units
+};
+
+__device__ __forceinline__ void prep_unit(const PrepItem& it, int64_t u) {
+  // units: [0, Npad*rpad/4) for At, then [.., + Mpad*rpad/4) for Bp, then 1 for red
+  const int64_t npad = (it.N + 127) / 128 * 128, mpad = (it.M + 15) / 16 * 16;
+  const int64_t n_at = npad * it.rpad / 4, n_bp = mpad * it.rpad / 4;
+  const int nkc = it.rpad / 16;
+  if (u < n_at) {
+    // At[col][g][kc][i]: unit = (col, g, kc)
+    int64_t col = u / (it.rpad / 4);
+    int rem = (int)(u % (it.rpad / 4));
+    int g = rem / nkc, kc = rem % nkc;
+    uint16_t v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int k = kc * 16 + 4 * g + i;
+      v[i] = (k < it.rank && col < it.N) ? it.a[(int64_t)k * it.lda + col] : (uint16_t)0;
+    }
+    uint2 w = make_uint2((uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16));
+    *(uint2*)(it.at + col * it.rpad + (g * nkc + kc) * 4) = w;
+    return;
+  }
+  u -= n_at;
+  if (u < n_bp) {
+    int64_t row = u / (it.rpad / 4);
+    int rem = (int)(u % (it.rpad / 4));
+    int g = rem / nkc, kc = rem % nkc;
+    uint16_t v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int k = kc * 16 + 4 * g + i;
+      v[i] = (k < it.rank && row < it.M) ? it.b[row * it.ldb + k] : (uint16_t)0;
+    }
+    uint2 w = make_uint2((uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16));
+    *(uint2*)(it.bp + row * it.rpad + (g * nkc + kc) * 4) = w;
+    return;
+  }
+  u -= n_bp;
+  if (u == 0 && it.red) {
+    for (int i = 0; i < 64; ++i) it.red[i] = 0u;
+  }
+}
+
+static inline int64_t prep_units(const PrepItem& it) {
+  const int64_t npad = (it.N + 127) / 128 * 128, mpad = (it.M + 15) / 16 * 16;
+  return npad * it.rpad / 4 + mpad * it.rpad / 4 + 1;
+}
+
+static __global__ __launch_bounds__(256) void k_prep1(PrepItem it, int64_t total) {
+  for (int64_t u = blockIdx.x * 256ll + threadIdx.x; u < total; u += (int64_t)gridDim.x * 256) prep_unit(it, u);
+}
+static __global__ __launch_bounds__(256) void k_prep_many(const PrepItem* __restrict__ items, int count, int64_t total) {
+  for (int64_t u = blockIdx.x * 256ll + threadIdx.x; u < total; u += (int64_t)gridDim.x * 256) {
+    int lo = 0, hi = count - 1;
+    while (lo < hi) {
+      int mid = (lo + hi + 1) >> 1;
+      if (items[mid].work_begin <= u) lo = mid;
+      else hi = mid - 1;
+    }
+    prep_unit(items[lo], u - items[lo].work_begin);
+  }
+}
+
+int launch_prep(const PrepItem& it, hipStream_t st);
+
+// ---------------------------------------------------------------------------
+// shared argument blocks
+// ---------------------------------------------------------------------------
+enum RowKind : int { K_INT8 = 0, K_E4M3 = 1, K_E5M2 = 2 };
+
+struct RowArgs {
+  const void* q;         // int8 / fp8 codes [M, N]
+  const void* scale;     // per-row (or per-tensor) scale, storage dtype scale_dt
+  const int8_t* zp;      // int8 zero point or null
+  const uint16_t* dense; // requant-only input (compute dtype)
+  void* q_out;
+  void* scale_out;
+  int8_t* zp_out;
+  const uint16_t* at;
+  const uint16_t* bp;
+  int64_t M, N;
+  float strength;
+  int qmin, qmax;
+  uint64_t seed;
+};
+
+template <int KIND>
+struct FmtLimit;
+template <>
+struct FmtLimit<K_E4M3> {
+  static constexpr float v = 448.0f;
+  static constexpr int fmt = E4M3;
+};
+template <>
+struct FmtLimit<K_E5M2> {
+  static constexpr float v = 57344.0f;
+  static constexpr int fmt = E5M2;
+};
+
+// per-row quantization parameters
+struct RowQP {
+  float s, inv, rcp, zp;
+};
+
+// INT8 qparams (P/_triton_int8_lora.py:123-186) -- computed by one thread
+template <int CD, int SDT, bool ASYM>
+__device__ RowQP int8_qparams(float mn, float mx, int qmin, int qmax, float& stored_scale, int& zp_out) {
+  mn = round_dt<CD>(mn);
+  mx = round_dt<CD>(mx);
+  float scale;
+  if constexpr (ASYM) {
+    float range = round_dt<CD>(mx - mn);
+    scale = range / (float)(qmax - qmin);
+  } else {
+    scale = __builtin_fmaxf(-mn, mx) / ((float)(qmax - qmin) / 2.0f);
+  }
+  scale = round_dt<CD>(scale);
+  scale = __builtin_fmaxf(scale, kEps);
+  scale = round_dt<CD>(scale);
+  int zp = 0;
+  if constexpr (ASYM) {
+    float ratio = round_dt<CD>(mn / scale);
+    zp = qmin - (int)__builtin_rintf(ratio);
+    zp = zp < qmin ? qmin : (zp > qmax ? qmax : zp);
+  }
+  stored_scale = scale;
+  zp_out = zp;
+  RowQP qp;
+  qp.s = round_dt<SDT>(scale);  // the quantize step reads the stored qparam
+  qp.inv = round_dt<SDT>(1.0f / qp.s);
+  qp.rcp = 1.0f / qp.s;
+  qp.zp = (float)zp;
+  return qp;
+}
+
+// FP8 qparams (P/_triton_float8_lora.py:249-271)
+template <int CD, int KIND>
+__device__ RowQP fp8_qparams(float amax, float& stored_scale) {
+  float scale = round_dt<CD>(amax / FmtLimit<KIND>::v);
+  if (scale == 0.0f) scale = kEps;
+  stored_scale = scale;
+  RowQP qp;
+  qp.s = scale;
+  qp.inv = 0.0f;
+  qp.rcp = 1.0f / scale;
+  qp.zp = 0.0f;
+  return qp;
+}
+
+// ---- row-format tile: load 16 codes (or dense values) and merge -------------
+template <int KIND, int CD, int SDT, int NKC, bool FROM_DENSE, bool HAS_LORA>
+__device__ __forceinline__ void row_merged_tile(const RowArgs& a, int64_t row, bool rok, int64_t c0, int lane,
+                                                int64_t mt_col0, const v4i16 (&bop)[NKC], float s_in, float z_in,
+                                                float (&m)[16]) {
+  const int64_t N = a.N;
+  const bool full = rok && (c0 + 16 <= N) && ((N & 15) == 0);
+  if constexpr (FROM_DENSE) {
+    if (full) {
+      const uint4* p = (const uint4*)(a.dense + row * N + c0);
+      uint4 w0 = p[0], w1 = p[1];
+      uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j) m[j] = val_dt<CD>((j & 1) ? (w[j >> 1] >> 16) : (w[j >> 1] & 0xffffu));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) m[j] = (rok && c0 + j < N) ? val_dt<CD>(a.dense[row * N + c0 + j]) : 0.0f;
+    }
+    return;
+  } else {
+    uint32_t w[4];
+    if (full) {
+      uint4 v = *(const uint4*)((const uint8_t*)a.q + row * N + c0);
+      w[0] = v.x;
+      w[1] = v.y;
+      w[2] = v.z;
+      w[3] = v.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          int64_t c = c0 + 4 * i + b;
+          if (rok && c < N) x |= (uint32_t)((const uint8_t*)a.q)[row * N + c] << (8 * b);
+        }
+        w[i] = x;
+      }
+    }
+    float d[16];
+    if constexpr (HAS_LORA) tile_delta<16, NKC, CD == F16>(a.at, mt_col0, lane, bop, d);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      float base;
+      if constexpr (KIND == K_INT8) {
+        int qv = (int)(int8_t)(w[j >> 2] >> (8 * (j & 3)));
+        base = round_dt<CD>(((float)qv - z_in) * s_in);
+      } else {
+        base = round_dt<CD>(fp8_decode<FmtLimit<KIND>::fmt>(w[j >> 2], j & 3) * s_in);
+      }
+      float v = base;
+      if constexpr (HAS_LORA) v = round_dt<CD>(__builtin_fmaf(d[j], a.strength, base));
+      const bool valid = rok && (c0 + j < N);
+      m[j] = valid ? v : 0.0f;
+    }
+  }
+}
+
+template <int KIND, int SDT, bool SR>
+__device__ __forceinline__ void row_quant_store(const RowArgs& a, int64_t row, bool rok, int64_t c0, const RowQP& qp,
+                                                const float (&m)[16]) {
+  const int64_t N = a.N;
+  if (!rok || c0 >= N) return;
+  const bool full = (c0 + 16 <= N) && ((N & 15) == 0);
+  uint32_t h[16];
+  if constexpr (SR) sr_bits<16>(a.seed, (uint64_t)(row * N + c0), h);
+  uint32_t w[4];
+  if constexpr (KIND == K_INT8) {
+    const float qmin = (float)a.qmin, qmax = (float)a.qmax;
+    int codes[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      float x = round_dt<SDT>(m[j] * qp.inv);
+      int q = (int)__builtin_rintf(x) + (int)qp.zp;
+      if constexpr (SR) {
+        float xs = div_rn(m[j], qp.s, qp.rcp) + qp.zp;
+        q = sr_int(xs, q, h[j], qmin, qmax);
+      }
+      q = q < a.qmin ? a.qmin : (q > a.qmax ? a.qmax : q);
+      codes[j] = q;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (uint32_t)(codes[4 * i] & 0xff) | ((uint32_t)(codes[4 * i + 1] & 0xff) << 8) |
+             ((uint32_t)(codes[4 * i + 2] & 0xff) << 16) | ((uint32_t)(codes[4 * i + 3] & 0xff) << 24);
+  } else {
+    constexpr float L = FmtLimit<KIND>::v;
+    constexpr int F = FmtLimit<KIND>::fmt;
+    float x[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) x[j] = __builtin_fminf(__builtin_fmaxf(div_rn(m[j], qp.s, qp.rcp), -L), L);
+    if constexpr (SR) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = sr_fp8<F>(x[4 * i], h[4 * i], L) | (sr_fp8<F>(x[4 * i + 1], h[4 * i + 1], L) << 8) |
+               (sr_fp8<F>(x[4 * i + 2], h[4 * i + 2], L) << 16) | (sr_fp8<F>(x[4 * i + 3], h[4 * i + 3], L) << 24);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = fp8_pack4<F>(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+    }
+  }
+  uint8_t* dst = (uint8_t*)a.q_out + row * N + c0;
+  if (full) {
+    *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    for (int j = 0; j < 16 && c0 + j < N; ++j) dst[j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+  }
+}
+
+// ---- k_rows: per-row formats ------------------------------------------------
+template <int KIND, int CD, int SDT, bool ASYM, bool SR, int NKC, bool FROM_DENSE, int NW, int CACHE>
+__device__ __forceinline__ void rows_body(const RowArgs& a, int64_t row0, int scale_dt) {
+  __shared__ float sh_mx[NW][16];
+  __shared__ float sh_mn[NW][16];
+  __shared__ float sh_qp[4][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15, g = lane >> 4;
+  const int64_t row = row0 + rl;
+  const bool rok = row < a.M;
+  const int64_t N = a.N;
+  const int ntiles = (int)((N + 63) >> 6);
+
+  v4i16 bop[NKC];
+  float s_in = 0.0f, z_in = 0.0f;
+  if constexpr (!FROM_DENSE) {
+    load_bop<NKC>(a.bp, row, lane, bop);
+    if (rok) {
+      s_in = load_scalar(a.scale, row, scale_dt);
+      if (KIND == K_INT8 && a.zp) z_in = (float)a.zp[row];
+    }
+  }
+
+  uint32_t cache[CACHE][8];
+  float vmx = 0.0f, vmn = 0.0f;
+  auto account = [&](const float (&m)[16]) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if constexpr (KIND == K_INT8) {
+        vmx = __builtin_fmaxf(vmx, m[j]);
+        vmn = __builtin_fminf(vmn, m[j]);
+      } else {
+        vmx = __builtin_fmaxf(vmx, __builtin_fabsf(m[j]));
+      }
+    }
+  };
+  // pass 1: merge, cache, reduce
+#pragma unroll
+  for (int i = 0; i < CACHE; ++i) {
+    const int mt = wave + i * NW;
+    if (mt < ntiles) {
+      float m[16];
+      row_merged_tile<KIND, CD, SDT, NKC, FROM_DENSE, !FROM_DENSE>(a, row, rok, (int64_t)mt * 64 + 16 * g, lane,
+                                                                    (int64_t)mt * 64, bop, s_in, z_in, m);
+      account(m);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) cache[i][k] = (uint32_t)bits_dt<CD>(m[2 * k]) | ((uint32_t)bits_dt<CD>(m[2 * k + 1]) << 16);
+    }
+  }
+  for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW) {
+    float m[16];
+    row_merged_tile<KIND, CD, SDT, NKC, FROM_DENSE, !FROM_DENSE>(a, row, rok, (int64_t)mt * 64 + 16 * g, lane,
+                                                                  (int64_t)mt * 64, bop, s_in, z_in, m);
+    account(m);
+  }
+  vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, 16));
+  vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, 32));
+  if constexpr (KIND == K_INT8) {
+    vmn = __builtin_fminf(vmn, __shfl_xor(vmn, 16));
+    vmn = __builtin_fminf(vmn, __shfl_xor(vmn, 32));
+  }
+  if (g == 0) {
+    sh_mx[wave][rl] = vmx;
+    sh_mn[wave][rl] = vmn;
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int t = threadIdx.x;
+    float mx = 0.0f, mn = 0.0f;
+    for (int w = 0; w < NW; ++w) {
+      mx = __builtin_fmaxf(mx, sh_mx[w][t]);
+      mn = __builtin_fminf(mn, sh_mn[w][t]);
+    }
+    const int64_t r = row0 + t;
+    RowQP qp;
+    float stored;
+    if constexpr (KIND == K_INT8) {
+      int zp;
+      qp = int8_qparams<CD, SDT, ASYM>(mn, mx, a.qmin, a.qmax, stored, zp);
+      if (r < a.M) {
+        store_scalar(a.scale_out, r, SDT, stored);
+        if (a.zp_out) a.zp_out[r] = (int8_t)zp;
+      }
+    } else {
+      qp = fp8_qparams<CD, KIND>(mx, stored);
+      if (r < a.M) ((float*)a.scale_out)[r] = stored;
+    }
+    sh_qp[0][t] = qp.s;
+    sh_qp[1][t] = qp.inv;
+    sh_qp[2][t] = qp.rcp;
+    sh_qp[3][t] = qp.zp;
+  }
+  __syncthreads();
+  RowQP qp;
+  qp.s = sh_qp[0][rl];
+  qp.inv = sh_qp[1][rl];
+  qp.rcp = sh_qp[2][rl];
+  qp.zp = sh_qp[3][rl];
+  // pass 2: quantize cached tiles, recompute the rest
+#pragma unroll
+  for (int i = 0; i < CACHE; ++i) {
+    const int mt = wave + i * NW;
+    if (mt < ntiles) {
+      float m[16];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        m[2 * k] = val_dt<CD>(cache[i][k] & 0xffffu);
+        m[2 * k + 1] = val_dt<CD>(cache[i][k] >> 16);
+      }
+      row_quant_store<KIND, SDT, SR>(a, row, rok, (int64_t)mt * 64 + 16 * g, qp, m);
+    }
+  }
+  for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW) {
+    float m[16];
+    row_merged_tile<KIND, CD, SDT, NKC, FROM_DENSE, !FROM_DENSE>(a, row, rok, (int64_t)mt * 64 + 16 * g, lane,
+                                                                  (int64_t)mt * 64, bop, s_in, z_in, m);
+    row_quant_store<KIND, SDT, SR>(a, row, rok, (int64_t)mt * 64 + 16 * g, qp, m);
+  }
+}
+
+template <int KIND, int CD, int SDT, bool ASYM, bool SR, int NKC, bool FROM_DENSE, int NW, int CACHE>
+__global__ __launch_bounds__(NW * 64) void k_rows(RowArgs a, int scale_dt) {
+  rows_body<KIND, CD, SDT, ASYM, SR, NKC, FROM_DENSE, NW, CACHE>(a, (int64_t)blockIdx.x * 16, scale_dt);
+}
+
+// stack: items[] in device memory, tile_begin[] = prefix of row tiles
+struct RowStackItem {
+  RowArgs a;
+  int64_t tile_begin;
+};
+template <int KIND, int CD, int SDT, bool SR, int NKC, int NW, int CACHE>
+__global__ __launch_bounds__(NW * 64) void k_rows_stack(const RowStackItem* __restrict__ items, int count,
+                                                        int scale_dt) {
+  int lo = 0, hi = count - 1;
+  const int64_t t = blockIdx.x;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (items[mid].tile_begin <= t) lo = mid;
+    else hi = mid - 1;
+  }
+  const RowArgs a = items[lo].a;
+  rows_body<KIND, CD, SDT, false, SR, NKC, false, NW, CACHE>(a, (t - items[lo].tile_begin) * 16, scale_dt);
+}
+
+// ---------------------------------------------------------------------------
+// k_blocks: block-local formats, dense weights, dequant, per-tensor passes
+// ---------------------------------------------------------------------------
+enum BlkFmt : int {
+  B_NVFP4 = 0,
+  B_MXFP4 = 1,
+  B_MXE4M3 = 2,
+  B_MXE5M2 = 3,
+  B_Q8_0 = 4,
+  B_DENSE = 5,   // plain bf16/fp16 weight (addmm_)
+  B_INT8 = 6,    // per-tensor / per-row INT8 (dequant, per-tensor passes)
+  B_E4M3 = 7,    // per-tensor / per-row FP8
+  B_E5M2 = 8,
+};
+enum BlkPass : int {
+  P_FULL = 0,     // merge + requant in one pass (block-local formats)
+  P_AMAX = 1,     // reduce max|merged| (and max(-min)) into red[]
+  P_QUANT = 2,    // quantize with the global qparams derived from red[]
+  P_TODENSE = 3,  // write merged (or dequantized) values to a dense output
+};
+
+struct BlkArgs {
+  const void* q;
+  const void* scale;
+  const void* aux;        // nvfp4: per-tensor scale in (float*); int8: zero point (int8*)
+  const uint16_t* dense;  // requant-only input
+  void* q_out;
+  void* scale_out;
+  void* aux_out;          // nvfp4: per-tensor scale out; int8: zero point out
+  void* out;              // P_TODENSE output
+  const uint16_t* at;
+  const uint16_t* bp;
+  uint32_t* red;
+  int64_t M, N, ld;       // ld: row stride of dense weights (B_DENSE)
+  float strength;
+  uint64_t seed;
+  int swizzled;
+  int mx_mode;
+  int out_dt;
+  int scale_dt;
+  int qmin, qmax;
+  int asym;
+  int64_t group;          // INT8/FP8 qparam group (N or M*N)
+  int tpw;                // macro tiles per wave
+};
+
+template <int F>
+struct BlkTraits {
+  static constexpr int SPAN = (F == B_MXFP4 || F == B_MXE4M3 || F == B_MXE5M2 || F == B_Q8_0) ? 32 : 16;
+};
+
+__device__ __forceinline__ float warp_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// load the lane's SPAN base (dequantized) values; returns false if row invalid
+template <int F, int CD>
+__device__ __forceinline__ void blk_load_base(const BlkArgs& a, int64_t row, bool rok, int64_t c0, float gscale,
+                                              float (&base)[BlkTraits<F>::SPAN], float& aux_val) {
+  constexpr int SPAN = BlkTraits<F>::SPAN;
+  const int64_t N = a.N;
+  if (!rok || c0 >= N) {
+#pragma unroll
+    for (int j = 0; j < SPAN; ++j) base[j] = 0.0f;
+    return;
+  }
+  if constexpr (F == B_NVFP4) {
+    uint2 w = *(const uint2*)((const uint8_t*)a.q + row * (N / 2) + c0 / 2);
+    uint32_t sc = ((const uint8_t*)a.scale)[blocked_offset(row, c0 / 16, N / 16, a.swizzled)];
+    float bs = round_dt<CD>(fp8_value<E4M3>(sc));
+    if (a.aux) bs = round_dt<CD>(bs * gscale);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      uint32_t word = j < 8 ? w.x : w.y;
+      uint32_t code = (word >> (4 * (j & 7))) & 15u;
+      base[j] = round_dt<CD>(e2m1_value(code) * bs);
+    }
+  } else if constexpr (F == B_MXFP4 || F == B_MXE4M3 || F == B_MXE5M2) {
+    uint32_t sc = ((const uint8_t*)a.scale)[blocked_offset(row, c0 / 32, N / 32, a.swizzled)];
+    float s = e8m0_value(sc);
+    float sr = round_dt<CD>(s);
+    if constexpr (F == B_MXFP4) {
+      uint4 w = *(const uint4*)((const uint8_t*)a.q + row * (N / 2) + c0 / 2);
+      uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        uint32_t code = (ws[j >> 3] >> (4 * (j & 7))) & 15u;
+        base[j] = round_dt<CD>(e2m1_value(code) * sr);
+      }
+    } else {
+      const uint4* p = (const uint4*)((const uint8_t*)a.q + row * N + c0);
+      uint4 w0 = p[0], w1 = p[1];
+      uint32_t ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        float lp = fp8_decode<F == B_MXE4M3 ? E4M3 : E5M2>(ws[j >> 2], j & 3);
+        base[j] = round_dt<CD>(lp * sr);
+      }
+    }
+  } else if constexpr (F == B_Q8_0) {
+    const int64_t ofs = row * (N / 32 * 34) + (c0 / 32) * 34;
+    const uint8_t* p8 = (const uint8_t*)a.q + (ofs & ~(int64_t)3);
+    const int sh = (int)(ofs & 3);
+    u32x4_a4 v0 = *(const u32x4_a4*)p8, v1 = *(const u32x4_a4*)(p8 + 16);
+    // sh == 0 needs only bytes 32..33 of the window: never read past the block
+    uint32_t v8 = sh ? *(const uint32_t*)(p8 + 32) : (uint32_t)*(const uint16_t*)(p8 + 32);
+    uint32_t win[9] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3], v8};
+    uint32_t blk[9];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) blk[k] = __builtin_amdgcn_alignbyte(win[k + 1], win[k], sh);
+    blk[8] = win[8] >> (8 * sh);
+    // blk bytes: [d lo][d hi][q0..q31]
+    float d = round_dt<CD>(f16_val(blk[0] & 0xffffu));
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      int bi = j + 2;
+      int qv = (int)(int8_t)(blk[bi >> 2] >> (8 * (bi & 3)));
+      base[j] = round_dt<CD>(d * (float)qv);
+    }
+  } else if constexpr (F == B_DENSE) {
+    const uint16_t* p = (const uint16_t*)a.q + row * a.ld + c0;
+    if (c0 + 16 <= N && (a.ld & 7) == 0) {
+      uint4 w0 = ((const uint4*)p)[0], w1 = ((const uint4*)p)[1];
+      uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j) base[j] = val_dt<CD>((j & 1) ? (w[j >> 1] >> 16) : (w[j >> 1] & 0xffffu));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) base[j] = (c0 + j < N) ? val_dt<CD>(p[j]) : 0.0f;
+    }
+  } else {  // B_INT8 / B_E4M3 / B_E5M2 with per-row or per-tensor scale
+    const int64_t qi = (a.group == N) ? row : 0;
+    const float s = load_scalar(a.scale, qi, a.scale_dt);
+    float z = 0.0f;
+    if constexpr (F == B_INT8) z = a.aux ? (float)((const int8_t*)a.aux)[qi] : 0.0f;
+    const uint8_t* p = (const uint8_t*)a.q + row * N + c0;
+    const bool full = (c0 + 16 <= N) && ((N & 15) == 0);
+    uint32_t w[4];
+    if (full) {
+      uint4 v = *(const uint4*)p;
+      w[0] = v.x;
+      w[1] = v.y;
+      w[2] = v.z;
+      w[3] = v.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t x = 0;
+        for (int b = 0; b < 4; ++b)
+          if (c0 + 4 * i + b < N) x |= (uint32_t)p[4 * i + b] << (8 * b);
+        w[i] = x;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      float v;
+      if constexpr (F == B_INT8) v = round_dt<CD>(((float)(int)(int8_t)(w[j >> 2] >> (8 * (j & 3))) - z) * s);
+      else v = round_dt<CD>(fp8_decode<F == B_E4M3 ? E4M3 : E5M2>(w[j >> 2], j & 3) * s);
+      base[j] = (c0 + j < N) ? v : 0.0f;
+    }
+  }
+  (void)aux_val;
+}
+
+// quantize + store one lane's block (block-local formats, or INT8/FP8 with
+// global qparams in P_QUANT)
+template <int F, int CD, bool SR>
+__device__ __forceinline__ void blk_store(const BlkArgs& a, int64_t row, int64_t c0, const float (&m)[BlkTraits<F>::SPAN],
+                                          float gscale, const RowQP& gqp) {
+  constexpr int SPAN = BlkTraits<F>::SPAN;
+  const int64_t N = a.N;
+  uint32_t h[SPAN];
+  if constexpr (SR) sr_bits<SPAN>(a.seed, (uint64_t)(row * N + c0), h);
+  if constexpr (F == B_NVFP4) {
+    float bmax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) bmax = __builtin_fmaxf(bmax, __builtin_fabsf(m[j]));
+    const bool two = a.aux != nullptr;
+    float bscale = bmax / 6.0f;
+    float fs = two ? bscale / gscale : bscale;
+    fs = __builtin_fminf(__builtin_fmaxf(fs, 0.015625f), 448.0f);
+    uint32_t sc8 = fp8_encode1<E4M3>(fs);
+    fs = fp8_value<E4M3>(sc8);
+    ((uint8_t*)a.scale_out)[blocked_offset(row, c0 / 16, N / 16, a.swizzled)] = (uint8_t)sc8;
+    float recip = two ? (1.0f / gscale) / fs : 0.0f;
+    float rfs = 1.0f / fs;
+    float x[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      float nrm = two ? m[j] * recip : div_rn(m[j], fs, rfs);
+      x[j] = __builtin_fminf(__builtin_fmaxf(nrm, -6.0f), 6.0f);
+    }
+    uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      uint32_t byte = e2m1_pack2(x[2 * t], x[2 * t + 1]);
+      if constexpr (SR) {
+        uint32_t c0c = sr_e2m1(x[2 * t], byte & 15u, h[2 * t]);
+        uint32_t c1c = sr_e2m1(x[2 * t + 1], byte >> 4, h[2 * t + 1]);
+        byte = c0c | (c1c << 4);
+      }
+      packed[t >> 2] |= byte << (8 * (t & 3));
+    }
+    *(uint2*)((uint8_t*)a.q_out + row * (N / 2) + c0 / 2) = make_uint2(packed[0], packed[1]);
+  } else if constexpr (F == B_MXFP4 || F == B_MXE4M3 || F == B_MXE5M2) {
+    constexpr int emax = F == B_MXFP4 ? 2 : (F == B_MXE4M3 ? 8 : 15);
+    constexpr float maxpos = F == B_MXFP4 ? 6.0f : (F == B_MXE4M3 ? 448.0f : 57344.0f);
+    constexpr int mbits = F == B_MXFP4 ? 1 : (F == B_MXE4M3 ? 3 : 2);
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(m[j]));
+    float inv;
+    uint32_t enc = mx_scale(amax, a.mx_mode, emax, maxpos, mbits, inv);
+    ((uint8_t*)a.scale_out)[blocked_offset(row, c0 / 32, N / 32, a.swizzled)] = (uint8_t)enc;
+    float x[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) x[j] = __builtin_fminf(__builtin_fmaxf(m[j] * inv, -maxpos), maxpos);
+    if constexpr (F == B_MXFP4) {
+      uint32_t packed[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        uint32_t byte = e2m1_pack2(x[2 * t], x[2 * t + 1]);
+        if constexpr (SR) {
+          uint32_t c0c = sr_e2m1(x[2 * t], byte & 15u, h[2 * t]);
+          uint32_t c1c = sr_e2m1(x[2 * t + 1], byte >> 4, h[2 * t + 1]);
+          byte = c0c | (c1c << 4);
+        }
+        packed[t >> 2] |= byte << (8 * (t & 3));
+      }
+      *(uint4*)((uint8_t*)a.q_out + row * (N / 2) + c0 / 2) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    } else {
+      constexpr int FF = F == B_MXE4M3 ? E4M3 : E5M2;
+      uint32_t w[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (SR)
+          w[i] = sr_fp8<FF>(x[4 * i], h[4 * i], maxpos) | (sr_fp8<FF>(x[4 * i + 1], h[4 * i + 1], maxpos) << 8) |
+                 (sr_fp8<FF>(x[4 * i + 2], h[4 * i + 2], maxpos) << 16) |
+                 (sr_fp8<FF>(x[4 * i + 3], h[4 * i + 3], maxpos) << 24);
+        else
+          w[i] = fp8_pack4<FF>(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+      }
+      uint4* dst = (uint4*)((uint8_t*)a.q_out + row * N + c0);
+      dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+      dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    }
+  } else if constexpr (F == B_Q8_0) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(m[j]));
+    float d = amax / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t blk[9];
+    blk[0] = (uint32_t)f16_bits(d);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      float x = m[j] * id;
+      int q = (int)__builtin_roundf(x);
+      if constexpr (SR) q = sr_int(x, q, h[j], -127.0f, 127.0f);
+      int bi = j + 2;
+      if ((bi & 3) == 0) blk[bi >> 2] = 0u;
+      blk[bi >> 2] |= ((uint32_t)q & 0xffu) << (8 * (bi & 3));
+    }
+    const int64_t ofs = row * (N / 32 * 34) + (c0 / 32) * 34;
+    uint8_t* base = (uint8_t*)a.q_out + ofs;
+    if ((ofs & 3) == 0) {
+      u32x4_a4 v0 = {blk[0], blk[1], blk[2], blk[3]}, v1 = {blk[4], blk[5], blk[6], blk[7]};
+      *(u32x4_a4*)base = v0;
+      *(u32x4_a4*)(base + 16) = v1;
+      *(uint16_t*)(base + 32) = (uint16_t)blk[8];
+    } else {  // ofs % 4 == 2: a short first, then 8 aligned dwords
+      *(uint16_t*)base = (uint16_t)blk[0];
+      uint32_t sh[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) sh[k] = __builtin_amdgcn_alignbyte(blk[k + 1], blk[k], 2);
+      u32x4_a4 v0 = {sh[0], sh[1], sh[2], sh[3]}, v1 = {sh[4], sh[5], sh[6], sh[7]};
+      *(u32x4_a4*)(base + 2) = v0;
+      *(u32x4_a4*)(base + 18) = v1;
+    }
+  } else if constexpr (F == B_DENSE) {
+    uint16_t* p = (uint16_t*)a.q_out + row * a.ld + c0;
+    if (c0 + 16 <= N && (a.ld & 7) == 0) {
+      uint32_t w[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) w[k] = (uint32_t)bits_dt<CD>(m[2 * k]) | ((uint32_t)bits_dt<CD>(m[2 * k + 1]) << 16);
+      ((uint4*)p)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+      ((uint4*)p)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    } else {
+      for (int j = 0; j < 16 && c0 + j < N; ++j) p[j] = bits_dt<CD>(m[j]);
+    }
+  } else {  // per-tensor INT8 / FP8 quantize with global qparams
+    RowArgs ra;
+    ra.q_out = a.q_out;
+    ra.N = N;
+    ra.qmin = a.qmin;
+    ra.qmax = a.qmax;
+    ra.seed = a.seed;
+    constexpr int KIND = F == B_INT8 ? K_INT8 : (F == B_E4M3 ? K_E4M3 : K_E5M2);
+    float mm[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mm[j] = m[j];
+    if (a.scale_dt == BF16) row_quant_store<KIND, BF16, SR>(ra, row, true, c0, gqp, mm);
+    else row_quant_store<KIND, F32, SR>(ra, row, true, c0, gqp, mm);
+  }
+}
+
+// global qparams for per-tensor INT8/FP8 from red[0] = max, red[1] = max(-min)
+template <int F, int CD>
+__device__ RowQP tensor_qparams(const BlkArgs& a, float& stored, int& zp) {
+  const float mx = u2f(a.red[0]), mn = -u2f(a.red[1]);
+  if constexpr (F == B_INT8) {
+    if (a.scale_dt == BF16) {
+      return a.asym ? int8_qparams<CD, BF16, true>(mn, mx, a.qmin, a.qmax, stored, zp)
+                    : int8_qparams<CD, BF16, false>(mn, mx, a.qmin, a.qmax, stored, zp);
+    }
+    return a.asym ? int8_qparams<CD, F32, true>(mn, mx, a.qmin, a.qmax, stored, zp)
+                  : int8_qparams<CD, F32, false>(mn, mx, a.qmin, a.qmax, stored, zp);
+  } else {
+    zp = 0;
+    return fp8_qparams<CD, F == B_E4M3 ? K_E4M3 : K_E5M2>(mx, stored);
+  }
+}
+
+template <int F, int CD, int NKC, bool SR, bool FROM_DENSE, int PASS, bool HAS_LORA>
+__global__ __launch_bounds__(256) void k_blocks(BlkArgs a) {
+  constexpr int SPAN = BlkTraits<F>::SPAN;
+  constexpr int MTW = 4 * SPAN;
+  __shared__ float sh_red[2][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15, g = lane >> 4;
+  const int64_t M = a.M, N = a.N;
+  const int ntiles = (int)((N + MTW - 1) / MTW);
+  const int tpw = a.tpw;
+  const int groups_per_rt = (ntiles + tpw - 1) / tpw;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t rt = unit / groups_per_rt;
+  const int grp = (int)(unit % groups_per_rt);
+  const int64_t row = rt * 16 + rl;
+  const bool active = rt * 16 < M;  // whole wave uniform
+  const bool rok = active && row < M;
+
+  float gscale = 1.0f;
+  if constexpr (F == B_NVFP4) {
+    if (a.aux) {
+      if constexpr (PASS == P_QUANT) {
+        gscale = __builtin_fmaxf(u2f(a.red[0]) / 2688.0f, kEps);
+      } else {
+        gscale = *(const float*)a.aux;
+      }
+    }
+  }
+  RowQP gqp = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (PASS == P_QUANT && (F == B_INT8 || F == B_E4M3 || F == B_E5M2)) {
+    float stored;
+    int zp;
+    gqp = tensor_qparams<F, CD>(a, stored, zp);
+  }
+  // the per-tensor global scale used by dequant stays the INPUT per-tensor scale
+  float gin = 1.0f;
+  if constexpr (F == B_NVFP4) gin = a.aux ? *(const float*)a.aux : 1.0f;
+
+  v4i16 bop[NKC];
+  if constexpr (HAS_LORA && !FROM_DENSE) load_bop<NKC>(a.bp, active ? row : 0, lane, bop);
+
+  float vmx = 0.0f, vmn = 0.0f;
+  if (active) {
+    for (int k = 0; k < tpw; ++k) {
+      const int mt = grp * tpw + k;
+      if (mt >= ntiles) break;
+      const int64_t mt_col0 = (int64_t)mt * MTW;
+      const int64_t c0 = mt_col0 + SPAN * g;
+      float m[SPAN];
+      if constexpr (FROM_DENSE) {
+#pragma unroll
+        for (int j = 0; j < SPAN; ++j) m[j] = (rok && c0 + j < N) ? val_dt<CD>(a.dense[row * N + c0 + j]) : 0.0f;
+      } else {
+        float base[SPAN];
+        float auxv = 0.0f;
+        blk_load_base<F, CD>(a, row, rok, c0, gin, base, auxv);
+        if constexpr (HAS_LORA) {
+          float d[SPAN];
+          tile_delta<SPAN, NKC, CD == F16>(a.at, mt_col0, lane, bop, d);
+#pragma unroll
+          for (int j = 0; j < SPAN; ++j) {
+            float v;
+            if constexpr (F == B_NVFP4) {
+              float upd = d[j] * a.strength;
+              v = (upd == 0.0f) ? base[j] : round_dt<CD>(__builtin_fmaf(d[j], a.strength, base[j]));
+            } else {
+              v = round_dt<CD>(__builtin_fmaf(d[j], a.strength, base[j]));
+            }
+            m[j] = (rok && c0 + j < N) ? v : 0.0f;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < SPAN; ++j) m[j] = base[j];
+        }
+      }
+      if constexpr (PASS == P_AMAX) {
+#pragma unroll
+        for (int j = 0; j < SPAN; ++j) {
+          if constexpr (F == B_INT8) {
+            vmx = __builtin_fmaxf(vmx, m[j]);
+            vmn = __builtin_fminf(vmn, m[j]);
+          } else {
+            vmx = __builtin_fmaxf(vmx, __builtin_fabsf(m[j]));
+          }
+        }
+      } else if constexpr (PASS == P_TODENSE) {
+        if (rok) {
+          for (int j = 0; j < SPAN && c0 + j < N; ++j) store_scalar(a.out, row * N + c0 + j, a.out_dt, m[j]);
+        }
+      } else {
+        if (rok && c0 < N) blk_store<F, CD, SR>(a, row, c0, m, gscale, gqp);
+      }
+    }
+  }
+  if constexpr (PASS == P_AMAX) {
+    vmx = warp_max(vmx);
+    float nmn = warp_max(-vmn);
+    if (lane == 0) {
+      sh_red[0][wave] = vmx;
+      sh_red[1][wave] = nmn;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float x = __builtin_fmaxf(__builtin_fmaxf(sh_red[0][0], sh_red[0][1]), __builtin_fmaxf(sh_red[0][2], sh_red[0][3]));
+      float y = __builtin_fmaxf(__builtin_fmaxf(sh_red[1][0], sh_red[1][1]), __builtin_fmaxf(sh_red[1][2], sh_red[1][3]));
+      atomicMax(&a.red[0], f2u(x));  // non-negative floats order like their bits
+      atomicMax(&a.red[1], f2u(y + 0.0f));
+    }
+  }
+}
+
+// zero the padding entries of a swizzled 128x4 scale layout
+static __global__ __launch_bounds__(256) void k_zero_swizzle_pad(uint8_t* scale, int64_t M, int64_t scols, int64_t total) {
+  const int64_t ncb = (scols + 3) / 4;
+  for (int64_t o = blockIdx.x * 256ll + threadIdx.x; o < total; o += (int64_t)gridDim.x * 256) {
+    int64_t tile = o / 512, w = o % 512;
+    int64_t row_lane = w / 16, rem = w % 16, rgrp = rem / 4, cib = rem % 4;
+    int64_t rb = tile / ncb, cb = tile % ncb;
+    int64_t row = rb * 128 + rgrp * 32 + row_lane, scol = cb * 4 + cib;
+    if (row >= M || scol >= scols) scale[o] = 0;
+  }
+}
+
+// writes the per-tensor outputs once every workgroup of the quantize pass has
+// consumed the inputs (the outputs may alias them)
+template <int F, int CD>
+__global__ void k_finalize(BlkArgs a) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  if constexpr (F == B_NVFP4) {
+    if (a.aux_out) *(float*)a.aux_out = __builtin_fmaxf(u2f(a.red[0]) / 2688.0f, kEps);
+  } else {
+    float stored;
+    int zp;
+    (void)tensor_qparams<F, CD>(a, stored, zp);
+    store_scalar(a.scale_out, 0, F == B_INT8 ? a.scale_dt : F32, stored);
+    if (F == B_INT8 && a.aux_out) *(int8_t*)a.aux_out = (int8_t)zp;
+  }
+}
+template <int F>
+static int run_finalize(const BlkArgs& a, int cd, hipStream_t st) {
+  if (cd == LM_F16) hipLaunchKernelGGL((k_finalize<F, F16>), dim3(1), dim3(64), 0, st, a);
+  else hipLaunchKernelGGL((k_finalize<F, BF16>), dim3(1), dim3(64), 0, st, a);
+  return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+// ---------------------------------------------------------------------------
+// host helpers
+// ---------------------------------------------------------------------------
+struct Ctx {
+  hipStream_t st;
+  uint16_t* at = nullptr;
+  uint16_t* bp = nullptr;
+  uint32_t* red = nullptr;
+  int nkc = 0;
+};
+
+static inline int check_lora(const lm_lora* l, int64_t M, int64_t N) {
+  if (!l) return LM_OK;
+  if (!l->b || !l->a) return fail(LM_EINVAL, "LoRA factor pointers must be non-null");
+  if (l->rank <= 0) return fail(LM_EINVAL, "LoRA rank must be positive, got %d", l->rank);
+  if (l->rank > 64) return fail(LM_EUNSUPPORTED, "LoRA rank %d exceeds the supported maximum 64", l->rank);
+  if (l->dtype != LM_BF16 && l->dtype != LM_F16)
+    return fail(LM_EUNSUPPORTED, "LoRA factors must be bfloat16 or float16, got dtype id %d", l->dtype);
+  if (l->ldb < l->rank || l->lda < N) return fail(LM_EINVAL, "LoRA factor leading dimensions are too small");
+  (void)M;
+  return LM_OK;
+}
+
+static inline int setup(Ctx& c, int64_t M, int64_t N, const lm_lora* l, void* ws, size_t wsb, void* stream) {
+  c.st = (hipStream_t)stream;
+  const int rank = l ? l->rank : 0;
+  WsLayout w = ws_layout(M, N, rank);
+  if (!ws) return fail(LM_EWORKSPACE, "workspace pointer is null (need %zu bytes)", w.total);
+  if (wsb < w.total) return fail(LM_EWORKSPACE, "workspace too small: %zu < %zu bytes", wsb, w.total);
+  if (((uintptr_t)ws & 255) != 0) return fail(LM_EINVAL, "workspace must be 256-byte aligned");
+  uint8_t* base = (uint8_t*)ws;
+  c.at = (uint16_t*)(base + w.at_off);
+  c.bp = (uint16_t*)(base + w.bp_off);
+  c.red = (uint32_t*)(base + w.red_off);
+  c.nkc = rpad_of(rank) / 16;
+  PrepItem it;
+  it.b = l ? (const uint16_t*)l->b : nullptr;
+  it.a = l ? (const uint16_t*)l->a : nullptr;
+  it.ldb = l ? l->ldb : 0;
+  it.lda = l ? l->lda : 0;
+  it.M = M;
+  it.N = N;
+  it.rank = rank;
+  it.rpad = rpad_of(rank);
+  it.at = c.at;
+  it.bp = c.bp;
+  it.red = c.red;
+  it.work_begin = 0;
+  return launch_prep(it, c.st);
+}
+
+static inline int check_rounding(const lm_rounding* r) {
+  if (!r) return LM_OK;
+  if (r->mode != LM_ROUND_NEAREST && r->mode != LM_ROUND_STOCHASTIC)
+    return fail(LM_EINVAL, "unknown rounding mode %d", r->mode);
+  return LM_OK;
+}
+static inline bool is_sr(const lm_rounding* r) { return r && r->mode == LM_ROUND_STOCHASTIC; }
+static inline uint64_t seed_of(const lm_rounding* r) { return r ? r->seed : 0; }
+
+// dispatch helpers: NKC in {1,2,4}
+#define NKC_SWITCH(nkc, ...)                                             \
+  switch (nkc) {                                                         \
+    case 1: { constexpr int NKC_ = 1; __VA_ARGS__; } break;              \
+    case 2: { constexpr int NKC_ = 2; __VA_ARGS__; } break;              \
+    case 4: { constexpr int NKC_ = 4; __VA_ARGS__; } break;              \
+    default: return fail(LM_EUNSUPPORTED, "unsupported rank padding");   \
+  }
+
+// ranks are padded to 16, 32 or 64 (rpad_of), so nkc is 1, 2 or 4
+static inline int nkc_bucket(int nkc) { return nkc; }
+
+static inline unsigned blocks_for(int64_t M, int64_t N, int mtw, int tpw) {
+  int64_t ntiles = (N + mtw - 1) / mtw;
+  int64_t groups = (ntiles + tpw - 1) / tpw;
+  int64_t units = (M + 15) / 16 * groups;
+  return (unsigned)((units + 3) / 4);
+}
+
+template <int F, int NKC, bool SR, bool FROM_DENSE, int PASS, bool HAS_LORA>
+static int run_blocks_cd(const BlkArgs& a, int cd, hipStream_t st) {
+  constexpr int SPAN = BlkTraits<F>::SPAN;
+  unsigned nb = blocks_for(a.M, a.N, 4 * SPAN, a.tpw);
+  if (nb == 0) return LM_OK;
+  if (cd == LM_F16)
+    hipLaunchKernelGGL((k_blocks<F, F16, NKC, SR, FROM_DENSE, PASS, HAS_LORA>), dim3(nb), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((k_blocks<F, BF16, NKC, SR, FROM_DENSE, PASS, HAS_LORA>), dim3(nb), dim3(256), 0, st, a);
+  LAUNCH_CHECK();
+  return LM_OK;
+}
+
+// run a block kernel for the given pass with optional LoRA / SR
+template <int F, int PASS>
+static int run_blocks(const BlkArgs& a, int cd, int nkc, bool sr, bool from_dense, hipStream_t st) {
+  if (from_dense) {
+    if (sr) return run_blocks_cd<F, 1, true, true, PASS, false>(a, cd, st);
+    return run_blocks_cd<F, 1, false, true, PASS, false>(a, cd, st);
+  }
+  if (nkc == 0) {
+    if (sr) return run_blocks_cd<F, 1, true, false, PASS, false>(a, cd, st);
+    return run_blocks_cd<F, 1, false, false, PASS, false>(a, cd, st);
+  }
+  if (sr) {
+    NKC_SWITCH(nkc_bucket(nkc), return (run_blocks_cd<F, NKC_, true, false, PASS, true>(a, cd, st)));
+  } else {
+    NKC_SWITCH(nkc_bucket(nkc), return (run_blocks_cd<F, NKC_, false, false, PASS, true>(a, cd, st)));
+  }
+  return LM_OK;
+}
+
+static BlkArgs blk_args_base(const Ctx& c, int64_t M, int64_t N, const lm_lora* l, const lm_rounding* r) {
+  BlkArgs a;
+  memset(&a, 0, sizeof a);
+  a.at = c.at;
+  a.bp = c.bp;
+  a.red = c.red;
+  a.M = M;
+  a.N = N;
+  a.ld = N;
+  a.strength = l ? l->strength : 0.0f;
+  a.seed = seed_of(r);
+  a.tpw = 4;
+  a.group = N;
+  return a;
+}
+
+// ---------------------------------------------------------------------------
+// per-row kernels dispatch
+// ---------------------------------------------------------------------------
+// NW waves per workgroup, CACHE macro tiles of 64 columns cached per wave.
+static constexpr int ROW_NW = 8;
+static constexpr int ROW_CACHE = 8;
+
+template <int KIND, int CD, int SDT, bool ASYM, bool SR, bool FROM_DENSE>
+static int run_rows_nkc(const RowArgs& a, int nkc, int scale_dt, hipStream_t st) {
+  dim3 grid((unsigned)((a.M + 15) / 16)), block(ROW_NW * 64);
+  if (FROM_DENSE || nkc == 0) {
+    hipLaunchKernelGGL((k_rows<KIND, CD, SDT, ASYM, SR, 1, FROM_DENSE, ROW_NW, ROW_CACHE>), grid, block, 0, st, a,
+                       scale_dt);
+  } else {
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_rows<KIND, CD, SDT, ASYM, SR, NKC_, FROM_DENSE, ROW_NW, ROW_CACHE>),
+                                                   grid, block, 0, st, a, scale_dt));
+  }
+  LAUNCH_CHECK();
+  return LM_OK;
+}
+
+template <int KIND, bool FROM_DENSE>
+static int run_rows(const RowArgs& a, int cd, int sdt, bool asym, bool sr, int nkc, hipStream_t st) {
+#define RR(CD_, SDT_, AS_, SR_) return run_rows_nkc<KIND, CD_, SDT_, AS_, SR_, FROM_DENSE>(a, nkc, sdt, st)
+  if (KIND != K_INT8) {
+    asym = false;
+    sdt = LM_F32;
+  }
+  if (cd == LM_F16) {
+    if (sdt == LM_BF16) {
+      if (asym) { if (sr) RR(F16, BF16, true, true); else RR(F16, BF16, true, false); }
+      else { if (sr) RR(F16, BF16, false, true); else RR(F16, BF16, false, false); }
+    } else {
+      if (asym) { if (sr) RR(F16, F32, true, true); else RR(F16, F32, true, false); }
+      else { if (sr) RR(F16, F32, false, true); else RR(F16, F32, false, false); }
+    }
+  } else {
+    if (sdt == LM_BF16) {
+      if (asym) { if (sr) RR(BF16, BF16, true, true); else RR(BF16, BF16, true, false); }
+      else { if (sr) RR(BF16, BF16, false, true); else RR(BF16, BF16, false, false); }
+    } else {
+      if (asym) { if (sr) RR(BF16, F32, true, true); else RR(BF16, F32, true, false); }
+      else { if (sr) RR(BF16, F32, false, true); else RR(BF16, F32, false, false); }
+    }
+  }
+#undef RR
+}
+
+static inline int check_nvfp4(int64_t M, int64_t N) {
+  if (M <= 0 || N <= 0) return fail(LM_EINVAL, "NVFP4 merge requires a non-empty weight");
+  if (N % 16 != 0) return fail(LM_EINVAL, "NVFP4 requires columns divisible by 16, got %lld", (long long)N);
+  return LM_OK;
+}
+static inline int zero_swizzle_pad(uint8_t* scale, int64_t M, int64_t scols, hipStream_t st) {
+  int64_t total = (M + 127) / 128 * 512 * ((scols + 3) / 4);
+  if ((M % 128) == 0 && (scols % 4) == 0) return LM_OK;
+  int64_t nb = (total + 255) / 256;
+  if (nb > 4096) nb = 4096;
+  hipLaunchKernelGGL(k_zero_swizzle_pad, dim3((unsigned)nb), dim3(256), 0, st, scale, M, scols, total);
+  LAUNCH_CHECK();
+  return LM_OK;
+}
+

@@ -1,0 +1,57 @@
+// lm_q8.hip -- GGUF Q8_0 merge / requant and GGUF dequant entry points.
+#include "lm_impl.h"
+
+// ---------------------------------------------------------------------------
+// GGUF Q8_0
+// ---------------------------------------------------------------------------
+static int check_q8(int64_t M, int64_t N) {
+  if (M <= 0 || N <= 0) return fail(LM_EINVAL, "Q8_0 merge requires a non-empty weight");
+  if (N % 32 != 0) return fail(LM_EINVAL, "Q8_0 requires logical columns divisible by 32, got %lld", (long long)N);
+  return LM_OK;
+}
+extern "C" int lm_q8_0_merge(const uint8_t* packed, uint8_t* packed_out, int64_t M, int64_t N, const lm_lora* lora,
+                             const lm_rounding* rounding, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if (!packed || !packed_out) return fail(LM_EINVAL, "Q8_0 pointers must be non-null");
+  if (!lora) return fail(LM_EINVAL, "lm_q8_0_merge requires LoRA factors");
+  if ((rc = check_q8(M, N))) return rc;
+  if ((rc = check_lora(lora, M, N))) return rc;
+  if ((rc = check_rounding(rounding))) return rc;
+  Ctx c;
+  if ((rc = setup(c, M, N, lora, workspace, workspace_bytes, stream))) return rc;
+  BlkArgs a = blk_args_base(c, M, N, lora, rounding);
+  a.q = packed;
+  a.q_out = packed_out;
+  return run_blocks<B_Q8_0, P_FULL>(a, lora->dtype, c.nkc, is_sr(rounding), false, c.st);
+}
+extern "C" int lm_q8_0_requant(const void* dense, int32_t dense_dtype, uint8_t* packed_out, int64_t M, int64_t N,
+                               const lm_rounding* rounding, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if (!dense || !packed_out) return fail(LM_EINVAL, "Q8_0 requant pointers must be non-null");
+  if ((rc = check_q8(M, N))) return rc;
+  if ((rc = check_rounding(rounding))) return rc;
+  Ctx c;
+  if ((rc = setup(c, M, N, nullptr, workspace, workspace_bytes, stream))) return rc;
+  BlkArgs a = blk_args_base(c, M, N, nullptr, rounding);
+  a.dense = (const uint16_t*)dense;
+  a.q_out = packed_out;
+  return run_blocks<B_Q8_0, P_FULL>(a, dense_dtype, 0, is_sr(rounding), true, c.st);
+}
+extern "C" int lm_gguf_dequant(const uint8_t* packed, int32_t quant_type, int64_t rows, int64_t cols, const lm_lora* lora,
+                               void* out, int32_t out_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if (!packed || !out) return fail(LM_EINVAL, "GGUF dequant pointers must be non-null");
+  if (quant_type != LM_GGUF_Q8_0)
+    return fail(LM_EUNSUPPORTED, "GGUF quant type %d has no HIP dequant kernel yet (Q8_0 only)", quant_type);
+  if ((rc = check_q8(rows, cols))) return rc;
+  if ((rc = check_lora(lora, rows, cols))) return rc;
+  Ctx c;
+  if ((rc = setup(c, rows, cols, lora, workspace, workspace_bytes, stream))) return rc;
+  BlkArgs a = blk_args_base(c, rows, cols, lora, nullptr);
+  a.q = packed;
+  a.out = out;
+  a.out_dt = out_dtype;
+  const int cd = lora ? lora->dtype : LM_BF16;
+  return run_blocks<B_Q8_0, P_TODENSE>(a, cd, c.nkc, false, false, c.st);
+}
+

@@ -1,0 +1,191 @@
+// lm_stack.hip -- grouped multi-target (stack) entry points.
+#include "lm_impl.h"
+
+// ---------------------------------------------------------------------------
+// stacks
+// ---------------------------------------------------------------------------
+extern "C" size_t lm_stack_workspace_extra(int32_t count) {
+  return align256((size_t)count * sizeof(PrepItem)) + align256((size_t)count * sizeof(RowStackItem)) +
+         align256((size_t)count * sizeof(BlkArgs)) + 256;
+}
+
+static int stack_layout(const lm_stack_item* items, int32_t count, void* ws, size_t wsb, PrepItem* preps,
+                        size_t& cursor) {
+  uint8_t* base = (uint8_t*)ws;
+  for (int i = 0; i < count; ++i) {
+    const lm_stack_item& s = items[i];
+    int rc;
+    if ((rc = check_lora(&s.lora, s.M, s.N))) return rc;
+    WsLayout w = ws_layout(s.M, s.N, s.lora.rank);
+    if (cursor + w.total > wsb) return fail(LM_EWORKSPACE, "stack workspace too small at item %d", i);
+    PrepItem& p = preps[i];
+    p.b = (const uint16_t*)s.lora.b;
+    p.a = (const uint16_t*)s.lora.a;
+    p.ldb = s.lora.ldb;
+    p.lda = s.lora.lda;
+    p.M = s.M;
+    p.N = s.N;
+    p.rank = s.lora.rank;
+    p.rpad = rpad_of(s.lora.rank);
+    p.at = (uint16_t*)(base + cursor + w.at_off);
+    p.bp = (uint16_t*)(base + cursor + w.bp_off);
+    p.red = (uint32_t*)(base + cursor + w.red_off);
+    cursor += w.total;
+  }
+  return LM_OK;
+}
+
+static int stack_prep(PrepItem* preps, int32_t count, uint8_t* dev_items, hipStream_t st) {
+  int64_t total = 0;
+  for (int i = 0; i < count; ++i) {
+    preps[i].work_begin = total;
+    total += prep_units(preps[i]);
+  }
+  HIP_TRY(hipMemcpyAsync(dev_items, preps, sizeof(PrepItem) * count, hipMemcpyHostToDevice, st));
+  int64_t nb = (total + 255) / 256;
+  if (nb > 8192) nb = 8192;
+  hipLaunchKernelGGL(k_prep_many, dim3((unsigned)nb), dim3(256), 0, st, (const PrepItem*)dev_items, count, total);
+  LAUNCH_CHECK();
+  return LM_OK;
+}
+
+extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, int32_t scale_dtype, int32_t rounding_mode,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  if (count <= 0) return LM_OK;
+  if (!items || !workspace) return fail(LM_EINVAL, "stack items and workspace must be non-null");
+  if (scale_dtype != LM_F32 && scale_dtype != LM_BF16) return fail(LM_EUNSUPPORTED, "INT8 scales must be f32/bf16");
+  if (((uintptr_t)workspace & 255) != 0) return fail(LM_EINVAL, "workspace must be 256-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  const size_t extra = lm_stack_workspace_extra(count);
+  if (workspace_bytes < extra) return fail(LM_EWORKSPACE, "stack workspace too small");
+  uint8_t* base = (uint8_t*)workspace;
+  uint8_t* dev_prep = base;
+  uint8_t* dev_rows = base + align256((size_t)count * sizeof(PrepItem));
+  size_t cursor = extra;
+  // host staging (pageable; hipMemcpyAsync copies it before returning)
+  PrepItem* preps = (PrepItem*)calloc(count, sizeof(PrepItem));
+  RowStackItem* rows = (RowStackItem*)calloc(count, sizeof(RowStackItem));
+  if (!preps || !rows) {
+    free(preps);
+    free(rows);
+    return fail(LM_EINVAL, "host allocation failed");
+  }
+  int rc = stack_layout(items, count, workspace, workspace_bytes, preps, cursor);
+  int nkc_max = 0, cd = items[0].lora.dtype;
+  int64_t tiles = 0;
+  for (int i = 0; rc == LM_OK && i < count; ++i) {
+    const lm_stack_item& s = items[i];
+    if (s.lora.dtype != cd) rc = fail(LM_EUNSUPPORTED, "all stack items must share one factor dtype");
+    if (s.M <= 0 || s.N <= 0 || !s.q || !s.scale || !s.q_out || !s.scale_out)
+      rc = fail(LM_EINVAL, "stack item %d has an invalid shape or null pointer", i);
+    RowArgs& a = rows[i].a;
+    a.q = s.q;
+    a.scale = s.scale;
+    a.zp = nullptr;
+    a.q_out = s.q_out;
+    a.scale_out = s.scale_out;
+    a.at = preps[i].at;
+    a.bp = preps[i].bp;
+    a.M = s.M;
+    a.N = s.N;
+    a.strength = s.lora.strength;
+    a.qmin = -128;
+    a.qmax = 127;
+    a.seed = s.seed;
+    rows[i].tile_begin = tiles;
+    tiles += (s.M + 15) / 16;
+    int nkc = rpad_of(s.lora.rank) / 16;
+    nkc_max = nkc > nkc_max ? nkc : nkc_max;
+  }
+  if (rc == LM_OK) rc = stack_prep(preps, count, dev_prep, st);
+  if (rc == LM_OK) {
+    // every item uses the largest rank bucket: the prepared layouts are per item,
+    // so items with a smaller rank must have the same padding.  Re-check.
+    for (int i = 0; i < count; ++i)
+      if (nkc_bucket(rpad_of(items[i].lora.rank) / 16) != nkc_bucket(nkc_max))
+        rc = fail(LM_EUNSUPPORTED, "stack items must share one rank bucket (16/32/64)");
+  }
+  if (rc == LM_OK) {
+    hipError_t e = hipMemcpyAsync(dev_rows, rows, sizeof(RowStackItem) * count, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) rc = fail(LM_EHIP, "hipMemcpyAsync: %s", hipGetErrorString(e));
+  }
+  if (rc == LM_OK) {
+    const bool sr = rounding_mode == LM_ROUND_STOCHASTIC;
+    dim3 grid((unsigned)tiles), block(ROW_NW * 64);
+#define RS(CD_, SDT_, SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_stack<K_INT8, CD_, SDT_, SR_, NKC_, ROW_NW, ROW_CACHE>), grid, block, 0, st, (const RowStackItem*)dev_rows, count, scale_dtype))
+    if (cd == LM_F16) {
+      if (scale_dtype == LM_BF16) { if (sr) { RS(F16, BF16, true); } else { RS(F16, BF16, false); } }
+      else { if (sr) { RS(F16, F32, true); } else { RS(F16, F32, false); } }
+    } else {
+      if (scale_dtype == LM_BF16) { if (sr) { RS(BF16, BF16, true); } else { RS(BF16, BF16, false); } }
+      else { if (sr) { RS(BF16, F32, true); } else { RS(BF16, F32, false); } }
+    }
+#undef RS
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) rc = fail(LM_EHIP, "stack launch: %s", hipGetErrorString(e));
+  }
+  // the pageable host buffers must outlive the async copies: wait for them
+  if (rc == LM_OK) {
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) rc = fail(LM_EHIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+  }
+  free(preps);
+  free(rows);
+  return rc;
+}
+
+// NVFP4 stack: every item is processed by its own block-kernel launches after
+// one grouped prep (two-level items need their own amax pass).
+extern "C" int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, int32_t swizzled, int32_t rounding_mode,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  if (count <= 0) return LM_OK;
+  if (!items || !workspace) return fail(LM_EINVAL, "stack items and workspace must be non-null");
+  if (((uintptr_t)workspace & 255) != 0) return fail(LM_EINVAL, "workspace must be 256-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  const size_t extra = lm_stack_workspace_extra(count);
+  if (workspace_bytes < extra) return fail(LM_EWORKSPACE, "stack workspace too small");
+  uint8_t* base = (uint8_t*)workspace;
+  size_t cursor = extra;
+  PrepItem* preps = (PrepItem*)calloc(count, sizeof(PrepItem));
+  if (!preps) return fail(LM_EINVAL, "host allocation failed");
+  int rc = stack_layout(items, count, workspace, workspace_bytes, preps, cursor);
+  if (rc == LM_OK) rc = stack_prep(preps, count, base, st);
+  lm_rounding rnd;
+  rnd.mode = rounding_mode;
+  rnd.reserved = 0;
+  for (int i = 0; rc == LM_OK && i < count; ++i) {
+    const lm_stack_item& s = items[i];
+    if ((rc = check_nvfp4(s.M, s.N))) break;
+    rnd.seed = s.seed;
+    Ctx c;
+    c.st = st;
+    c.at = preps[i].at;
+    c.bp = preps[i].bp;
+    c.red = preps[i].red;
+    c.nkc = preps[i].rpad / 16;
+    const bool two = s.aux != nullptr;
+    BlkArgs a = blk_args_base(c, s.M, s.N, &s.lora, &rnd);
+    a.q = s.q;
+    a.scale = s.scale;
+    a.aux = s.aux;
+    a.q_out = s.q_out;
+    a.scale_out = s.scale_out;
+    a.aux_out = s.aux_out;
+    a.swizzled = swizzled;
+    const bool sr = rounding_mode == LM_ROUND_STOCHASTIC;
+    if (swizzled && (rc = zero_swizzle_pad((uint8_t*)s.scale_out, s.M, s.N / 16, st))) break;
+    if (two) {
+      if ((rc = run_blocks<B_NVFP4, P_AMAX>(a, s.lora.dtype, c.nkc, false, false, st))) break;
+      if ((rc = run_blocks<B_NVFP4, P_QUANT>(a, s.lora.dtype, c.nkc, sr, false, st))) break;
+      if (run_finalize<B_NVFP4>(a, s.lora.dtype, st)) rc = fail(LM_EHIP, "finalize launch failed");
+    } else {
+      rc = run_blocks<B_NVFP4, P_FULL>(a, s.lora.dtype, c.nkc, sr, false, st);
+    }
+  }
+  if (rc == LM_OK) {
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) rc = fail(LM_EHIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+  }
+  free(preps);
+  return rc;
+}

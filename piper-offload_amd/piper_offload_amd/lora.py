@@ -1,0 +1,345 @@
+"""LoRA resources and the per-weight merge transform.
+
+Mirrors the merge half of P/lora.py (P/ = the reference's src/piper_offload/):
+
+* :class:`LoRAFactor` / :class:`ScaledLoRAFactor` -- host-backed A/B (+bias)
+  factors, strength bound extrinsically (P/lora.py:116-245);
+* :class:`LoRA` -- pairs ``*.lora_A.weight`` / ``*.lora_B.weight`` (+
+  ``*.lora_B.bias``) keys of a flat state dict into pinned host factors
+  (P/lora.py:264-311, 940-1095);
+* :class:`LoRATransform` -- validates a target, stages B/A on the target
+  device in its compute dtype, packs several LoRAs along the rank with the
+  strength folded into A, derives the stochastic-rounding seed
+  ``derive_seed(target_key, merge_index)`` and calls the adapter's
+  ``merge_lora_`` (P/lora.py:314-724).
+
+Routed LoRA (forward hooks) and DTensor shard slicing are outside this
+build's hot path.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Mapping, Sequence
+from dataclasses import dataclass
+from types import MappingProxyType
+from typing import Any
+
+import torch
+from torch import nn
+
+from .registry import param_representation, select_adapter
+from .seeding import derive_seed
+
+__all__ = ["LoRA", "LoRAFactor", "LoRATransform", "ScaledLoRAFactor"]
+
+
+def _host_copy(t: torch.Tensor, dtype: torch.dtype | None, pin: bool) -> torch.Tensor:
+    t = t.detach().to("cpu")
+    if dtype is not None and t.dtype is not dtype:
+        t = t.to(dtype)
+    t = t.contiguous()
+    if pin and torch.cuda.is_available():
+        t = t.pin_memory()
+    return t
+
+
+@dataclass(slots=True, frozen=True)
+class LoRAFactor:
+    """Host tensors for one target: ``a`` (rank, in), ``b`` (out, rank), optional ``bias`` (out,)."""
+
+    a: torch.Tensor
+    b: torch.Tensor
+    bias: torch.Tensor | None = None
+
+    @property
+    def cache_bytes(self) -> int:
+        total = self.a.numel() * self.a.element_size() + self.b.numel() * self.b.element_size()
+        if self.bias is not None:
+            total += self.bias.numel() * self.bias.element_size()
+        return total
+
+    def scaled(self, strength: float) -> ScaledLoRAFactor:
+        return ScaledLoRAFactor(self.a, self.b, strength, self.bias)
+
+
+@dataclass(slots=True, frozen=True)
+class ScaledLoRAFactor:
+    """Host factors bound to an application ``strength``; contributes ``strength * (b @ a)``."""
+
+    a: torch.Tensor
+    b: torch.Tensor
+    strength: float
+    bias: torch.Tensor | None = None
+
+    def __post_init__(self) -> None:
+        if self.a.ndim != 2 or self.b.ndim != 2 or self.a.shape[0] != self.b.shape[1]:
+            raise ValueError(
+                f"LoRA factor shape mismatch: A shape is {tuple(self.a.shape)}, B shape is {tuple(self.b.shape)}."
+            )
+        if self.bias is not None and (self.bias.ndim != 1 or self.bias.shape[0] != self.b.shape[0]):
+            raise ValueError(
+                f"LoRA bias shape mismatch: bias shape is {tuple(self.bias.shape)}, B shape is "
+                f"{tuple(self.b.shape)}. Expected bias=(out_dim,)."
+            )
+
+    @classmethod
+    def from_tensors(cls, a: torch.Tensor, b: torch.Tensor, strength: float,
+                     bias: torch.Tensor | None = None) -> ScaledLoRAFactor:
+        return cls(_host_copy(a, None, True), _host_copy(b, None, True), strength,
+                   None if bias is None else _host_copy(bias, None, True))
+
+    @property
+    def rank(self) -> int:
+        return self.a.shape[0]
+
+    @property
+    def produced_shape(self) -> tuple[int, int]:
+        return (self.b.shape[0], self.a.shape[1])
+
+
+class LoRA:
+    """Reusable immutable host-backed LoRA resource (P/lora.py:224-311)."""
+
+    def __init__(self, targets: Mapping[str, LoRAFactor]) -> None:
+        self._targets = MappingProxyType(dict(targets))
+        self._cache_bytes = sum(f.cache_bytes for f in self._targets.values())
+
+    @classmethod
+    def from_state_dict(cls, state_dict: dict[str, torch.Tensor], *, dtype: torch.dtype | None = None,
+                        host_backing: str = "pinned") -> LoRA:
+        if host_backing not in ("pinned", "adopt"):
+            raise ValueError(f"host_backing must be 'pinned' or 'adopt', got {host_backing!r}")
+        if dtype is not None and not dtype.is_floating_point:
+            raise ValueError(f"LoRA dtype must be floating-point, got {dtype}.")
+        a_t, b_t, bias_t = _split_factor_tensors(state_dict)
+        if not a_t and not b_t:
+            raise ValueError("LoRA state_dict contains no factor pairs")
+        a_only, b_only = set(a_t) - set(b_t), set(b_t) - set(a_t)
+        if a_only or b_only:
+            raise ValueError(
+                f"Unpaired LoRA factors: A-only={sorted(a_only)}, B-only={sorted(b_only)}. Each target needs both "
+                ".lora_A.weight and .lora_B.weight."
+            )
+        bias_only = set(bias_t) - set(a_t)
+        if bias_only:
+            raise ValueError(f"Unpaired LoRA biases: {sorted(bias_only)}. Each .lora_B.bias must accompany a "
+                             "complete .lora_A.weight / .lora_B.weight pair.")
+        targets: dict[str, LoRAFactor] = {}
+        pin = host_backing == "pinned"
+        for base, a in a_t.items():
+            b, bias = b_t[base], bias_t.get(base)
+            _validate_factor_pair(f"{base}.weight", a, b, bias)
+            if host_backing == "adopt" and dtype is not None and (a.dtype is not dtype or b.dtype is not dtype):
+                raise ValueError("adopted LoRA host backing cannot convert factor dtype without copying.")
+            if pin:
+                targets[f"{base}.weight"] = LoRAFactor(_host_copy(a, dtype, True), _host_copy(b, dtype, True),
+                                                       None if bias is None else _host_copy(bias, dtype, True))
+            else:
+                targets[f"{base}.weight"] = LoRAFactor(a, b, bias)
+        return cls(targets)
+
+    @property
+    def targets(self) -> Mapping[str, LoRAFactor]:
+        return self._targets
+
+    @property
+    def cache_bytes(self) -> int:
+        return self._cache_bytes
+
+
+@dataclass(slots=True, frozen=True)
+class _WeightPlan:
+    adapter: Any
+    staging_shape: tuple[int, ...]
+    compute_dtype: torch.dtype
+
+
+class LoRATransform:
+    """LoRA factors applied to one base weight and optional base bias (P/lora.py:314-724)."""
+
+    __slots__ = ("_factors", "_merge_index", "_stochastic_rounding", "_target_key", "_weight_plan")
+
+    def __init__(self, factors: list[ScaledLoRAFactor], *, stochastic_rounding: bool = False,
+                 target_key: str = "") -> None:
+        if stochastic_rounding and not target_key:
+            raise ValueError("Stochastic LoRATransform requires a non-empty target_key.")
+        self._factors = factors
+        self._stochastic_rounding = stochastic_rounding
+        self._target_key = target_key
+        self._merge_index = 0
+        self._weight_plan: _WeightPlan | None = None
+
+    @property
+    def merge_index(self) -> int:
+        return self._merge_index
+
+    def _rounding_seed(self) -> int | None:
+        if not self._stochastic_rounding:
+            return None
+        return derive_seed(self._target_key, self._merge_index)
+
+    @property
+    def has_bias(self) -> bool:
+        return any(f.bias is not None for f in self._factors)
+
+    # -- validation -------------------------------------------------------
+    def validate_target(self, weight: nn.Parameter | torch.Tensor, bias: nn.Parameter | None = None) -> None:
+        self._weight_plan = None
+        plan = self._build_weight_plan(weight)
+        if self.has_bias:
+            if bias is None:
+                raise ValueError("LoRA transform contains a bias but no base bias target was provided.")
+            self.validate_bias_target(bias)
+        self._weight_plan = plan
+
+    def validate_weight_target(self, param: nn.Parameter | torch.Tensor) -> None:
+        self._weight_plan = None
+        self._weight_plan = self._build_weight_plan(param)
+
+    def _build_weight_plan(self, param: torch.Tensor) -> _WeightPlan:
+        data = param_representation(param)
+        try:
+            adapter = select_adapter(data)
+        except NotImplementedError as exc:
+            raise ValueError(
+                f"Tensor type {type(data).__name__} has no registered tensor adapter. "
+                "Merge requires a tensor adapter with LoRA merge support."
+            ) from exc
+        if not callable(getattr(adapter, "merge_lora_", None)):
+            raise ValueError(f"{type(adapter).__name__} does not support LoRA merge. Use routed LoRA for this tensor type.")
+        compute_dtype = adapter.compute_dtype(data)
+        if not compute_dtype.is_floating_point:
+            raise ValueError(f"LoRA merge requires a floating-point compute dtype, got {compute_dtype}.")
+        shape = tuple(adapter.logical_shape(data))
+        for f in self._factors:
+            if f.produced_shape != shape:
+                raise ValueError(f"LoRA factor shape mismatch: B@A produces {f.produced_shape}, target shape is {shape}.")
+        for f in self._factors:
+            if type(f.a) is not torch.Tensor or type(f.b) is not torch.Tensor or f.a.device.type != "cpu" \
+                    or f.b.device.type != "cpu":
+                raise ValueError("LoRA merge requires plain CPU torch.Tensor factors; wrapped factor "
+                                 "representations are unsupported.")
+        validate = getattr(adapter, "validate_lora_merge", None)
+        if callable(validate):
+            b, a, strength, prepared = self._stage(data, adapter, shape, compute_dtype)
+            hook = getattr(adapter, "validate_prepared_lora_merge", None) if prepared else validate
+            hook(data, b, a, strength, rounding_seed=self._rounding_seed())
+        return _WeightPlan(adapter, shape, compute_dtype)
+
+    def validate_bias_target(self, param: torch.Tensor) -> None:
+        if not self.has_bias:
+            raise ValueError("LoRA bias merge requires at least one bias")
+        target = param_representation(param)
+        if type(target) is not torch.Tensor:
+            raise ValueError(f"LoRA bias merge requires a plain dense base bias; got {type(target).__name__}.")
+        if not target.is_floating_point():
+            raise ValueError(f"LoRA bias merge requires a floating-point base bias; got {target.dtype}.")
+        if target.dim() != 1:
+            raise ValueError(f"LoRA bias merge requires a rank-one base bias; got shape {tuple(target.shape)}.")
+        for f in self._factors:
+            if f.bias is not None and tuple(f.bias.shape) != tuple(target.shape):
+                raise ValueError(f"LoRA bias shape mismatch: adapter bias shape is {tuple(f.bias.shape)}, "
+                                 f"base bias shape is {tuple(target.shape)}.")
+
+    # -- application ------------------------------------------------------
+    def apply(self, weight: nn.Parameter | torch.Tensor, bias: nn.Parameter | None = None) -> None:
+        if self.has_bias and bias is None:
+            raise ValueError("LoRA transform contains a bias but no base bias target was provided.")
+        self.apply_weight(weight)
+        if self.has_bias and bias is not None:
+            self.apply_bias(bias)
+
+    def apply_weight(self, param: nn.Parameter | torch.Tensor) -> None:
+        plan = self._weight_plan
+        if plan is None:
+            raise RuntimeError("LoRA weight target must be validated before application.")
+        data = param_representation(param)
+        seed = self._rounding_seed()
+        b, a, strength, prepared = self._stage(data, plan.adapter, plan.staging_shape, plan.compute_dtype)
+        if prepared:
+            plan.adapter.merge_prepared_lora_(data, b, a, strength, rounding_seed=seed)
+        else:
+            plan.adapter.merge_lora_(data, b, a, strength, rounding_seed=seed)
+        self._merge_index += 1
+
+    def apply_bias(self, param: torch.Tensor) -> None:
+        target = param_representation(param)
+        delta = torch.zeros_like(target)
+        for f in self._factors:
+            if f.bias is not None:
+                delta.add_(f.bias.to(device=target.device, dtype=target.dtype, non_blocking=True), alpha=f.strength)
+        target.add_(delta)
+
+    # -- staging (P/lora.py:595-724) ------------------------------------------
+    def staged_update(self, data: torch.Tensor, compute_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor, float]:
+        """Public form of the ordinary staging: (B, A, strength) on ``data``'s device."""
+        shape = (self._factors[0].b.shape[0], self._factors[0].a.shape[1])
+        return self._stage_single_or_packed(data, shape, compute_dtype)
+
+    def _stage(self, data: torch.Tensor, adapter: Any, shape: tuple[int, ...],  # noqa: ANN401
+               compute_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor, float, bool]:
+        stage = getattr(adapter, "stage_lora_factors", None)
+        if callable(stage):
+            prepared = stage(data, tuple((f.strength, f.a, f.b) for f in self._factors), logical_shape=shape,
+                             compute_dtype=compute_dtype)
+            if prepared is not None:
+                b, a, s = prepared
+                return b, a, s, True
+        b, a, s = self._stage_single_or_packed(data, shape, compute_dtype)
+        return b, a, s, False
+
+    def _stage_single_or_packed(self, data: torch.Tensor, shape: tuple[int, ...],
+                                compute_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor, float]:
+        device = data.device
+        if len(self._factors) == 1:
+            f = self._factors[0]
+            return (f.b.to(device=device, dtype=compute_dtype, non_blocking=True).contiguous(),
+                    f.a.to(device=device, dtype=compute_dtype, non_blocking=True).contiguous(), f.strength)
+        total = sum(f.a.shape[0] for f in self._factors)
+        a_packed = torch.empty((total, shape[1]), device=device, dtype=compute_dtype)
+        b_packed = torch.empty((shape[0], total), device=device, dtype=compute_dtype)
+        off = 0
+        for f in self._factors:
+            nxt = off + f.a.shape[0]
+            a_slice = a_packed[off:nxt]
+            a_slice.copy_(f.a, non_blocking=True)
+            b_packed[:, off:nxt].copy_(f.b, non_blocking=True)
+            if f.strength != 1.0:
+                a_slice.mul_(f.strength)
+            off = nxt
+        return b_packed, a_packed, 1.0
+
+
+def _split_factor_tensors(state_dict: dict[str, torch.Tensor]
+                          ) -> tuple[dict[str, torch.Tensor], dict[str, torch.Tensor], dict[str, torch.Tensor]]:
+    a_t: dict[str, torch.Tensor] = {}
+    b_t: dict[str, torch.Tensor] = {}
+    bias_t: dict[str, torch.Tensor] = {}
+    for key, t in state_dict.items():
+        if key.endswith(".lora_A.weight"):
+            a_t[key[: -len(".lora_A.weight")]] = t
+        elif key.endswith(".lora_B.weight"):
+            b_t[key[: -len(".lora_B.weight")]] = t
+        elif key.endswith(".lora_B.bias"):
+            bias_t[key[: -len(".lora_B.bias")]] = t
+    return a_t, b_t, bias_t
+
+
+def _validate_factor_pair(key: str, a: torch.Tensor, b: torch.Tensor, bias: torch.Tensor | None) -> None:
+    if not a.is_floating_point() or not b.is_floating_point():
+        raise ValueError(f"LoRA factors for {key!r}: must be floating-point; got A.dtype={a.dtype}, B.dtype={b.dtype}.")
+    if a.dim() != 2 or b.dim() != 2 or a.shape[0] != b.shape[1]:
+        raise ValueError(
+            f"LoRA factor shape mismatch for {key!r}: A.shape={tuple(a.shape)}, B.shape={tuple(b.shape)}. "
+            "Expected A=(rank, in_dim), B=(out_dim, rank) with A.shape[0] == B.shape[1]."
+        )
+    if bias is not None:
+        if not bias.is_floating_point():
+            raise ValueError(f"LoRA bias for {key!r} must be floating-point; got dtype={bias.dtype}.")
+        if bias.dim() != 1 or bias.shape[0] != b.shape[0]:
+            raise ValueError(f"LoRA bias shape mismatch for {key!r}: bias.shape={tuple(bias.shape)}, "
+                             f"B.shape={tuple(b.shape)}. Expected bias=(out_dim,) with bias.shape[0] == B.shape[0].")
+
+
+def factors_for(loras: Sequence[tuple[LoRA, float]], target_key: str) -> list[ScaledLoRAFactor]:
+    return [lora.targets[target_key].scaled(s) for lora, s in loras if target_key in lora.targets]

@@ -1,0 +1,97 @@
+"""Scaled FP8 (e4m3fn / e5m2) per-row and per-tensor merge vs the oracle (same contract as INT8)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import bf16_np, bf16_ulp_diff, fp8_initial, lora_factors, normal_bf16, u8_np
+
+pytestmark = pytest.mark.gpu
+
+K = pytest.importorskip("piper_offload_amd.kernels")
+from piper_offload_amd import Float8Adapter, Float8Weight, derive_seed  # noqa: E402
+
+DEV = "cuda"
+FMT = {torch.float8_e4m3fn: O.DT_E4M3, torch.float8_e5m2: O.DT_E5M2}
+
+
+@pytest.mark.parametrize("shape", [(24, 69), (64, 8192), (16, 1000)])
+@pytest.mark.parametrize("fp8", [torch.float8_e4m3fn, torch.float8_e5m2])
+@pytest.mark.parametrize("sr", [False, True])
+@pytest.mark.parametrize("per_tensor", [False, True])
+def test_fp8_requant_bit_exact(shape, fp8, sr, per_tensor):
+    dense = normal_bf16(shape, 0.02, 7)
+    dense[1] = 0
+    dense[2, :3] = torch.tensor([1e-30, -3.0, 0.5], dtype=torch.bfloat16)
+    dense[3, 0] = -0.0
+    block = shape if per_tensor else (1, shape[1])
+    group = shape[0] * shape[1] if per_tensor else shape[1]
+    seed = derive_seed("fp8.requant", shape[1]) if sr else None
+    q, s = K.requantize_float8(dense.to(DEV), block, fp8_dtype=fp8, rounding_seed=seed)
+    oq, os_ = O.fp8_requant(bf16_np(dense), group, fmt=FMT[fp8], sr_mode=O.SR_PHILOX8 if sr else O.SR_OFF,
+                            seed=seed or 0)
+    assert np.array_equal(u8_np(q), oq)
+    assert np.array_equal(s.cpu().numpy().reshape(-1), os_)
+
+
+@pytest.mark.parametrize("shape,rank,strength", [((64, 8192), 64, 1.0), ((24, 69), 5, 0.75), ((32, 1024), 16, 0.5)])
+@pytest.mark.parametrize("sr", [False, True])
+def test_fp8_fused_equals_requant_of_gpu_dense(shape, rank, strength, sr):
+    rows, cols = shape
+    w = normal_bf16(shape, 0.02, 0)
+    q, s = fp8_initial(w)
+    b, a = lora_factors(rows, cols, rank, 2)
+    qd, sd, bd, ad = q.to(DEV), s.to(DEV), b.to(DEV), a.to(DEV)
+    base = K.dequantize_float8(qd, sd, (1, cols))
+    obase = O.fp8_dequant(u8_np(q), s.numpy(), cols)
+    assert np.array_equal(bf16_np(base), obase)
+    dense = K.dequantize_float8(qd, sd, (1, cols), lora=(bd, ad, strength))
+    omerged = O.merge_dense(obase, bf16_np(b), bf16_np(a), strength)
+    diff = bf16_ulp_diff(bf16_np(dense), omerged)
+    assert diff.max() <= 1 and (diff > 0).mean() <= 1e-3
+    seed = derive_seed("fp8.fused", rows) if sr else None
+    oq, os_ = K.merge_float8_lora(qd, sd, (1, cols), bd, ad, strength, rounding_seed=seed)
+    rq, rs = O.fp8_requant(bf16_np(dense), cols, sr_mode=O.SR_PHILOX8 if sr else O.SR_OFF, seed=seed or 0)
+    assert np.array_equal(u8_np(oq), rq)
+    assert np.array_equal(os_.cpu().numpy().reshape(-1), rs)
+
+
+def test_fp8_per_tensor_and_adapter_in_place():
+    rows, cols, rank = 32, 512, 16
+    w = normal_bf16((rows, cols), 0.02, 1)
+    wf = w.float()
+    st = (wf.abs().max() / 448.0).reshape(1, 1)
+    q = (wf / st).clamp(-448, 448).to(torch.float8_e4m3fn)
+    b, a = lora_factors(rows, cols, rank, 3)
+    target = Float8Weight(q.clone().to(DEV), st.clone().to(DEV), (rows, cols), torch.bfloat16)
+    ptr = target.qdata.data_ptr()
+    Float8Adapter.merge_lora_(target, b.to(DEV), a.to(DEV), 1.0)
+    dense = K.dequantize_float8(q.to(DEV), st.to(DEV), (rows, cols), lora=(b.to(DEV), a.to(DEV), 1.0))
+    rq, rs = O.fp8_requant(bf16_np(dense), rows * cols)
+    assert target.qdata.data_ptr() == ptr
+    assert np.array_equal(u8_np(target.qdata), rq)
+    assert np.array_equal(target.scale.cpu().numpy().reshape(-1), rs)
+
+
+def test_fp8_sr_two_neighbours_and_unbiased():
+    rows, cols = 64, 4096
+    dense = torch.full((rows, cols), 0.3, dtype=torch.bfloat16)
+    dense[:, 0] = 448 * 0.3 / 0.3  # fixes the row scale at 1.0 (amax 448)
+    q, s = K.requantize_float8(dense.to(DEV), (1, cols), rounding_seed=derive_seed("fp8-unbiased", 0))
+    vals = q.float().cpu()[:, 1:]
+    x = float(torch.tensor(0.3, dtype=torch.bfloat16).float()) / float(s[0, 0])
+    neighbours = sorted({float(v) for v in vals.unique()})
+    assert len(neighbours) == 2 and min(neighbours) <= x <= max(neighbours)
+    assert float(vals.mean()) == pytest.approx(x, abs=1e-3)
+
+
+def test_fp8_negative_zero_keeps_sign_and_zero_rows_get_eps():
+    dense = torch.zeros(16, 64, dtype=torch.bfloat16)
+    dense[0, 0] = -0.0
+    dense[1, 1] = 1.0
+    q, s = K.requantize_float8(dense.to(DEV), (1, 64), rounding_seed=derive_seed("negzero", 0))
+    assert u8_np(q)[0, 0] == 0x80
+    assert float(s[0, 0]) == torch.finfo(torch.float32).eps
