@@ -1,0 +1,415 @@
+#!/usr/bin/env python3
+"""LoRA-merge throughput on one MI355X.
+
+Default workload (BASELINE.json metric "LoRA-merge GB/s & % of HBM peak; ms to
+merge 8B-shaped INT8 stack", config 5): the 224 projection weights of an
+8B-shaped model (32 layers x q/o [4096,4096], k/v [1024,4096], gate/up
+[14336,4096], down [4096,14336]) stored as per-row symmetric INT8 with fp32
+scales, a rank-16 bf16 LoRA on every projection (A ~ N(0, 1/16),
+B ~ N(0, 0.01), strength 1.0), stochastic requant with one Philox seed per
+target and merge index, derive_seed(param_path, step).  A step merges the
+whole stack once, in place, through the grouped HIP kernel.
+
+``value`` is algorithmic GB/s: per target 2*M*N (codes in + out) + 8*M
+(fp32 scales in + out) + 2*r*(M+N) (bf16 factors), over the step time.  The
+``roofline`` block uses the dominant kernel's own HIP-event time; the
+``cpu_baseline`` block times the CPU oracle (a C restatement of the same
+merge) on a bounded sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--workload int8_stack|nvfp4_stack|int8|fp8|q8_0|nvfp4|mxfp4]
+                    [--rounding stochastic|nearest] [--cpu-seconds S]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "piper-offload_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+METRIC = "LoRA-merge GB/s & % of HBM peak; ms to merge 8B-shaped INT8 stack"
+
+LAYER_SHAPES = (
+    ("self_attn.q_proj", 4096, 4096),
+    ("self_attn.k_proj", 1024, 4096),
+    ("self_attn.v_proj", 1024, 4096),
+    ("self_attn.o_proj", 4096, 4096),
+    ("mlp.gate_proj", 14336, 4096),
+    ("mlp.up_proj", 14336, 4096),
+    ("mlp.down_proj", 4096, 14336),
+)
+
+
+def _parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--workload", default="int8_stack",
+                   choices=["int8_stack", "nvfp4_stack", "int8", "fp8", "q8_0", "nvfp4", "mxfp4"])
+    p.add_argument("--rounding", default="stochastic", choices=["stochastic", "nearest"])
+    p.add_argument("--layers", type=int, default=32)
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-oracle baseline (0: skip)")
+    return p.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# synthetic workloads
+# ---------------------------------------------------------------------------
+def _gen(seed: int):  # noqa: ANN202
+    import torch
+
+    return torch.Generator(device="cuda").manual_seed(seed % (1 << 63))
+
+
+def _normal(shape, std, seed, dtype=None):  # noqa: ANN001, ANN202
+    import torch
+
+    t = torch.randn(shape, generator=_gen(seed), device="cuda", dtype=torch.float32).mul_(std)
+    return t.to(dtype or torch.bfloat16)
+
+
+def _int8_weight(path: str, rows: int, cols: int):  # noqa: ANN202
+    import torch
+
+    from piper_offload_amd import Int8Weight, derive_seed
+
+    w = _normal((rows, cols), 0.02, derive_seed(path, 0)).float()
+    scale = (w.abs().amax(dim=1, keepdim=True) / 127.0).clamp_min(torch.finfo(torch.float32).eps)
+    q = torch.round(w / scale).clamp_(-128, 127).to(torch.int8)
+    del w
+    return Int8Weight(q, scale, (1, cols), torch.bfloat16)
+
+
+def _nvfp4_weight(path: str, rows: int, cols: int):  # noqa: ANN202
+    from piper_offload_amd import NVFP4Weight, derive_seed
+    from piper_offload_amd.kernels import requantize_nvfp4
+
+    w = _normal((rows, cols), 0.02, derive_seed(path, 0))
+    q, s, pts = requantize_nvfp4(w, two_level=True, swizzled=False)
+    del w
+    return NVFP4Weight(q, s, pts.reshape(()), 16)
+
+
+def _factors(path: str, rows: int, cols: int, rank: int):  # noqa: ANN202
+    from piper_offload_amd import derive_seed
+
+    a = _normal((rank, cols), 1.0 / rank, derive_seed(path, 1))
+    b = _normal((rows, rank), 0.01, derive_seed(path, 2))
+    return b, a
+
+
+def _int8_bytes(rows: int, cols: int, rank: int) -> int:
+    return 2 * rows * cols + 8 * rows + 2 * rank * (rows + cols)
+
+
+def _nvfp4_bytes(rows: int, cols: int, rank: int) -> int:
+    return 2 * (rows * cols // 2 + rows * cols // 16) + 8 + 2 * rank * (rows + cols)
+
+
+class Workload:
+    """One merge 'step' plus its algorithmic byte count and dominant kernel family."""
+
+    name = ""
+    family = ""
+    config: dict = {}
+    bytes_per_step = 0
+
+    def step(self, index: int) -> None:
+        raise NotImplementedError
+
+
+class Int8Stack(Workload):
+    family = "rows_stack"
+
+    def __init__(self, layers: int, stochastic: bool) -> None:
+        from piper_offload_amd.stack import StackTarget
+
+        self.stochastic = stochastic
+        self.paths, self.targets = [], []
+        rank = 16
+        for i in range(layers):
+            for name, rows, cols in LAYER_SHAPES:
+                path = f"model.layers.{i}.{name}.weight"
+                w = _int8_weight(path, rows, cols)
+                b, a = _factors(path, rows, cols, rank)
+                self.paths.append(path)
+                self.targets.append(StackTarget(w, b, a, 1.0, 0))
+                self.bytes_per_step += _int8_bytes(rows, cols, rank)
+        n_el = sum(t.weight.qdata.numel() for t in self.targets)
+        self.name = "int8_stack"
+        self.config = {
+            "workload": f"{layers}-layer 8B-shaped INT8 stack merge ({len(self.targets)} targets: q/o [4096,4096], "
+                        "k/v [1024,4096], gate/up [14336,4096], down [4096,14336]); per-row symmetric int8 codes + "
+                        "fp32 scales from W~N(0,0.02) (absmax/127); rank-16 bf16 LoRA A~N(0,1/16) B~N(0,0.01), "
+                        f"strength 1.0; {'stochastic' if stochastic else 'round-to-nearest'} requant, seed "
+                        "derive_seed(param_path, step); one grouped launch per step",
+            "targets": len(self.targets), "rank": rank, "elements": n_el,
+            "rounding": "stochastic" if stochastic else "nearest",
+            "algorithmic_bytes_per_step": self.bytes_per_step,
+        }
+
+    def step(self, index: int) -> None:
+        from piper_offload_amd import derive_seed
+        from piper_offload_amd.stack import merge_int8_stack
+
+        for t, p in zip(self.targets, self.paths):
+            t.seed = derive_seed(p, index)
+        merge_int8_stack(self.targets, stochastic=self.stochastic)
+
+
+class Nvfp4Stack(Workload):
+    family = "blocks_quant"
+
+    def __init__(self, layers: int, stochastic: bool) -> None:
+        from piper_offload_amd.stack import StackTarget
+
+        self.stochastic = stochastic
+        self.paths, self.targets = [], []
+        rank = 16
+        for i in range(layers):
+            for name, rows, cols in LAYER_SHAPES:
+                path = f"model.layers.{i}.{name}.weight"
+                w = _nvfp4_weight(path, rows, cols)
+                b, a = _factors(path, rows, cols, rank)
+                self.paths.append(path)
+                self.targets.append(StackTarget(w, b, a, 1.0, 0))
+                self.bytes_per_step += _nvfp4_bytes(rows, cols, rank)
+        self.name = "nvfp4_stack"
+        self.config = {
+            "workload": f"{layers}-layer 8B-shaped NVFP4 stack merge (two-level: e2m1 codes, e4m3 block-16 scales, "
+                        "fp32 per-tensor scale); rank-16 bf16 LoRA, strength 1.0, "
+                        f"{'stochastic' if stochastic else 'round-to-nearest'} requant",
+            "targets": len(self.targets), "rank": rank,
+            "rounding": "stochastic" if stochastic else "nearest",
+            "algorithmic_bytes_per_step": self.bytes_per_step,
+        }
+
+    def step(self, index: int) -> None:
+        from piper_offload_amd import derive_seed
+        from piper_offload_amd.stack import merge_nvfp4_stack
+
+        for t, p in zip(self.targets, self.paths):
+            t.seed = derive_seed(p, index)
+        merge_nvfp4_stack(self.targets, stochastic=self.stochastic)
+
+
+class Single(Workload):
+    """One tensor of configs 2-4 (or NVFP4 / MXFP4 at the gate_proj shape)."""
+
+    def __init__(self, kind: str, stochastic: bool) -> None:
+        import torch
+
+        from piper_offload_amd import derive_seed
+        from piper_offload_amd import kernels as K
+
+        self.kind, self.stochastic = kind, stochastic
+        self.path = "bench.weight"
+        if kind == "int8":
+            rows, cols, rank, self.strength = 14336, 4096, 32, 0.5
+            w = _int8_weight(self.path, rows, cols)
+            self.q, self.s = w.qdata, w.scale
+            self.family = "rows"
+            self.bytes_per_step = _int8_bytes(rows, cols, rank)
+        elif kind == "fp8":
+            rows, cols, rank, self.strength = 8192, 8192, 64, 1.0
+            w = _normal((rows, cols), 0.02, derive_seed(self.path, 0)).float()
+            self.s = (w.abs().amax(dim=1, keepdim=True) / 448.0).clamp_min(torch.finfo(torch.float32).eps)
+            self.q = (w / self.s).clamp_(-448, 448).to(torch.float8_e4m3fn)
+            self.family = "rows"
+            self.bytes_per_step = 2 * rows * cols + 8 * rows + 2 * rank * (rows + cols)
+        elif kind == "q8_0":
+            rows, cols, rank, self.strength = 13824, 5120, 16, 1.0
+            self.q = K.requantize_q8_0(_normal((rows, cols), 0.02, derive_seed(self.path, 0)))
+            self.family = "blocks_full"
+            self.bytes_per_step = 2 * rows * (cols // 32 * 34) + 2 * rank * (rows + cols)
+        elif kind == "nvfp4":
+            rows, cols, rank, self.strength = 14336, 4096, 16, 1.0
+            self.w = _nvfp4_weight(self.path, rows, cols)
+            self.family = "blocks_quant"
+            self.bytes_per_step = _nvfp4_bytes(rows, cols, rank)
+        else:  # mxfp4
+            rows, cols, rank, self.strength = 14336, 4096, 16, 1.0
+            q, s = K.requantize_mx(_normal((rows, cols), 0.02, derive_seed(self.path, 0)), torch.float4_e2m1fn_x2)
+            self.q, self.s = q, s
+            self.family = "blocks_full"
+            self.bytes_per_step = 2 * (rows * cols // 2 + rows * cols // 32) + 2 * rank * (rows + cols)
+        self.b, self.a = _factors(self.path, rows, cols, rank)
+        self.name = kind
+        self.config = {"workload": f"{kind} merge [{rows},{cols}] rank {rank} strength {self.strength}, "
+                                   f"{'stochastic' if stochastic else 'round-to-nearest'} requant",
+                       "rank": rank, "rounding": "stochastic" if stochastic else "nearest",
+                       "algorithmic_bytes_per_step": self.bytes_per_step}
+
+    def step(self, index: int) -> None:
+        import torch
+
+        from piper_offload_amd import derive_seed
+        from piper_offload_amd import kernels as K
+
+        seed = derive_seed(self.path, index) if self.stochastic else None
+        if self.kind == "int8":
+            K.merge_int8_lora_into(self.q, self.s, None, (1, self.q.shape[1]), self.b, self.a, self.strength,
+                                   asymmetric=False, reduce_range=False, rounding_seed=seed, out_qdata=self.q,
+                                   out_scale=self.s, out_zero_point=None)
+        elif self.kind == "fp8":
+            K.merge_float8_lora_into(self.q, self.s, (1, self.q.shape[1]), self.b, self.a, self.strength,
+                                     rounding_seed=seed, out_qdata=self.q, out_scale=self.s)
+        elif self.kind == "q8_0":
+            K.merge_q8_0_lora(self.q, self.b, self.a, self.strength, rounding_seed=seed, out=self.q)
+        elif self.kind == "nvfp4":
+            w = self.w
+            K.merge_nvfp4_lora_into(w.qdata, w.scale, w.per_tensor_scale, 16, False, self.b, self.a, self.strength,
+                                    rounding_seed=seed, out_qdata=w.qdata, out_scale=w.scale,
+                                    out_per_tensor_scale=w.per_tensor_scale)
+        else:
+            K.merge_mx_lora_(self.q, self.s, torch.float4_e2m1fn_x2, 32, torch.bfloat16, self.b, self.a,
+                             self.strength, scaling_mode=0, swizzled=False, rounding_seed=seed)
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle (C restatement, OpenMP) on a bounded sample
+# ---------------------------------------------------------------------------
+def cpu_baseline(kind: str, stochastic: bool, budget_s: float) -> dict | None:
+    if budget_s <= 0:
+        return None
+    import numpy as np
+
+    cores = len(os.sched_getaffinity(0))
+    os.environ.setdefault("OMP_NUM_THREADS", str(cores))
+    import oracle as O
+
+    rng = np.random.default_rng(0)
+    if kind in ("int8_stack", "int8"):
+        cols, rank, strength = 4096, (16 if kind == "int8_stack" else 32), (1.0 if kind == "int8_stack" else 0.5)
+        def make(rows):  # noqa: ANN001, ANN202
+            w = (rng.standard_normal((rows, cols), dtype=np.float32) * 0.02)
+            s = np.maximum(np.abs(w).max(1) / 127.0, np.float32(1.1920929e-07)).astype(np.float32)
+            q = np.clip(np.round(w / s[:, None]), -128, 127).astype(np.int8)
+            a = O.f32_to_bf16(rng.standard_normal((rank, cols), dtype=np.float32) / rank)
+            b = O.f32_to_bf16(rng.standard_normal((rows, rank), dtype=np.float32) * 0.01)
+            return q, s, a, b
+        def run(data):  # noqa: ANN001, ANN202
+            q, s, a, b = data
+            base = O.int8_dequant(q, s, None, cols)
+            merged = O.merge_dense(base, b, a, strength)
+            O.int8_requant(merged, cols, sr_mode=O.SR_PHILOX8 if stochastic else O.SR_OFF, seed=12345)
+        def nbytes(rows):  # noqa: ANN001, ANN202
+            return _int8_bytes(rows, cols, rank)
+        shape_note = f"gate_proj-shaped rows x {cols} (rank {rank})"
+    else:
+        return None
+    rows = 64
+    t0 = time.perf_counter()
+    run(make(rows))
+    dt = time.perf_counter() - t0
+    # size the sample to about budget_s / 3 per repeat, median of 3
+    rows = int(max(64, min(14336, rows * (budget_s / 3.0) / max(dt, 1e-3)))) // 16 * 16
+    data = make(rows)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run(data)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    return {"value": round(nbytes(rows) / t / 1e9, 3), "unit": "GB/s", "cores": int(os.environ.get("OMP_NUM_THREADS", cores)),
+            "kind": "port",
+            "sample": f"oracle dequant + fp32 B@A + requant ({'SR' if stochastic else 'RTN'}) of {rows} {shape_note}, "
+                      f"median of 3 ({t:.2f} s each)"}
+
+
+def _traffic(name: str) -> int | None:
+    path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["hbm_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def main() -> int:
+    args = _parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the merge shards by weight and by row "
+              "with no exchange except one scalar max for two-level scales -- see DESIGN.md", file=sys.stderr)
+        return 2
+    import torch
+
+    from piper_offload_amd import _lib as L
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    L.lib()
+    stochastic = args.rounding == "stochastic"
+    print(f"[bench] building workload {args.workload} ...", file=sys.stderr, flush=True)
+    if args.workload == "int8_stack":
+        wl: Workload = Int8Stack(args.layers, stochastic)
+    elif args.workload == "nvfp4_stack":
+        wl = Nvfp4Stack(args.layers, stochastic)
+    else:
+        wl = Single(args.workload, stochastic)
+    torch.cuda.synchronize()
+    print(f"[bench] warmup {args.warmup} ...", file=sys.stderr, flush=True)
+    for i in range(args.warmup):
+        wl.step(i)
+    torch.cuda.synchronize()
+    L.timer_enable(True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(args.steps):
+        wl.step(args.warmup + i)
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = start.elapsed_time(stop)
+    kern_ms, launches = L.timer_read(wl.family)
+    L.timer_enable(False)
+    ms_per_step = ev_ms / args.steps
+    value = wl.bytes_per_step / (ms_per_step * 1e-3) / 1e9
+    print(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step (events), wall {wall / args.steps * 1e3:.3f} ms/step, "
+          f"{wl.family}: {launches} launches {kern_ms / max(launches, 1):.3f} ms avg", file=sys.stderr, flush=True)
+    per_launch_bytes = wl.bytes_per_step * args.steps / max(launches, 1)
+    achieved = per_launch_bytes / (kern_ms / max(launches, 1) * 1e-3) / 1e9 if launches else None
+    print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+    cpu = cpu_baseline(args.workload, stochastic, args.cpu_seconds)
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": wl.config,
+        "hbm_peak_fraction": round(value / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": wl.family,
+            "achieved": None if achieved is None else round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": None if achieved is None else round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": _traffic(wl.name),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -9,7 +9,7 @@
  *   lm_fp8_merge    <- merge_float8_lora   P/_triton_float8_lora.py:486-588
  *   lm_nvfp4_merge  <- merge_nvfp4_lora    P/_triton_nvfp4_lora.py:515-595
  *   lm_mx_merge     <- merge_mx_lora_      P/_triton_mx_lora.py:333-425
- *   lm_bf16_merge   <- RegularAdapter.merge_lora_ (addmm_)
+ *   lm_dense_merge  <- RegularAdapter.merge_lora_ (addmm_)
  *                                          P/tensor_adapters.py:686-696
  *   lm_q8_0_merge   <- (no reference counterpart: the reference routes GGUF
  *                      only, P/gguf_adapter.py:160-284; requant follows the
@@ -26,9 +26,11 @@
  *  - All pointers are device pointers unless noted; tensors are row-major
  *    and contiguous unless a leading dimension is given.  M = out rows,
  *    N = logical in columns, rank = r.
- *  - `stream` is a hipStream_t passed as void*.  No entry point
- *    synchronizes or allocates device memory; scratch comes from the
- *    caller's `workspace` (size from lm_workspace_size()).
+ *  - `stream` is a hipStream_t passed as void*.  No entry point allocates
+ *    device memory (scratch comes from the caller's `workspace`, sized by
+ *    lm_workspace_size()); single-tensor entry points are asynchronous on
+ *    `stream`, the *_stack entry points synchronize it once before returning
+ *    (their descriptor tables are staged from host memory).
  *  - Return value: LM_OK or an lm_status; lm_last_error() returns a
  *    thread-local message for the last failure on the calling thread.
  *  - The deterministic path rounds to nearest even.  Stochastic rounding
@@ -205,6 +207,16 @@ int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, int32_t scale
 /* NVFP4 stack (two-level when aux != NULL). */
 int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, int32_t swizzled, int32_t rounding_mode,
                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------- instrumentation -------------------------------------
+ * No reference counterpart.  When enabled, every entry point brackets its
+ * main kernel launches with hipEvents on the caller's stream, keyed by kernel
+ * family ("rows", "rows_stack", "blocks_full", "blocks_amax",
+ * "blocks_quant", "todense", "prep").  lm_timer_read synchronizes the
+ * recorded events and returns the summed milliseconds and launch count of one
+ * family.  Enabling (or re-enabling) clears the record. */
+int lm_timer_enable(int32_t enable);
+int lm_timer_read(const char* family, double* total_ms, int64_t* launches);
 
 #ifdef __cplusplus
 }

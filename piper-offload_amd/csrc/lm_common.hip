@@ -14,7 +14,80 @@ extern "C" int lm_version(void) { return LM_ABI_VERSION; }
 extern "C" const char* lm_last_error(void) { return g_err.c_str(); }
 extern "C" size_t lm_workspace_size(int64_t M, int64_t N, int32_t rank) { return ws_layout(M, N, rank).total; }
 
+// ---- kernel timer -----------------------------------------------------------
+#include <atomic>
+#include <map>
+#include <mutex>
+#include <vector>
+
+namespace {
+struct TimerRec {
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pairs;
+  hipEvent_t open = nullptr;
+};
+std::atomic<bool> g_timer_on{false};
+std::mutex g_timer_mu;
+std::map<std::string, TimerRec> g_timer;
+
+void timer_clear_locked() {
+  for (auto& kv : g_timer) {
+    for (auto& p : kv.second.pairs) {
+      (void)hipEventDestroy(p.first);
+      (void)hipEventDestroy(p.second);
+    }
+    if (kv.second.open) (void)hipEventDestroy(kv.second.open);
+  }
+  g_timer.clear();
+}
+}  // namespace
+
+bool lm_timer_on() { return g_timer_on.load(std::memory_order_relaxed); }
+
+void lm_timer_mark(const char* family, hipStream_t st, bool begin) {
+  std::lock_guard<std::mutex> lk(g_timer_mu);
+  TimerRec& r = g_timer[family];
+  hipEvent_t e;
+  if (hipEventCreate(&e) != hipSuccess) return;
+  (void)hipEventRecord(e, st);
+  if (begin) {
+    if (r.open) (void)hipEventDestroy(r.open);
+    r.open = e;
+  } else if (r.open) {
+    r.pairs.emplace_back(r.open, e);
+    r.open = nullptr;
+  } else {
+    (void)hipEventDestroy(e);
+  }
+}
+
+extern "C" int lm_timer_enable(int32_t enable) {
+  std::lock_guard<std::mutex> lk(g_timer_mu);
+  timer_clear_locked();
+  g_timer_on.store(enable != 0);
+  return LM_OK;
+}
+
+extern "C" int lm_timer_read(const char* family, double* total_ms, int64_t* launches) {
+  std::lock_guard<std::mutex> lk(g_timer_mu);
+  double ms = 0.0;
+  int64_t n = 0;
+  auto it = g_timer.find(family ? family : "");
+  if (it != g_timer.end()) {
+    for (auto& p : it->second.pairs) {
+      HIP_TRY(hipEventSynchronize(p.second));
+      float t = 0.0f;
+      HIP_TRY(hipEventElapsedTime(&t, p.first, p.second));
+      ms += t;
+      ++n;
+    }
+  }
+  if (total_ms) *total_ms = ms;
+  if (launches) *launches = n;
+  return LM_OK;
+}
+
 int launch_prep(const PrepItem& it, hipStream_t st) {
+  TimedLaunch timed("prep", st);
   int64_t total = prep_units(it);
   int64_t blocks = (total + 255) / 256;
   if (blocks > 4096) blocks = 4096;

@@ -147,6 +147,21 @@ static __global__ __launch_bounds__(256) void k_prep_many(const PrepItem* __rest
 
 int launch_prep(const PrepItem& it, hipStream_t st);
 
+// kernel timer (lm_timer_enable / lm_timer_read): bracket a launch on `st`
+bool lm_timer_on();
+void lm_timer_mark(const char* family, hipStream_t st, bool begin);
+struct TimedLaunch {
+  const char* family;
+  hipStream_t st;
+  bool on;
+  TimedLaunch(const char* f, hipStream_t s) : family(f), st(s), on(lm_timer_on()) {
+    if (on) lm_timer_mark(family, st, true);
+  }
+  ~TimedLaunch() {
+    if (on) lm_timer_mark(family, st, false);
+  }
+};
+
 // ---------------------------------------------------------------------------
 // shared argument blocks
 // ---------------------------------------------------------------------------
@@ -1038,6 +1053,9 @@ static int run_blocks_cd(const BlkArgs& a, int cd, hipStream_t st) {
   constexpr int SPAN = BlkTraits<F>::SPAN;
   unsigned nb = blocks_for(a.M, a.N, 4 * SPAN, a.tpw);
   if (nb == 0) return LM_OK;
+  TimedLaunch timed(PASS == P_FULL ? "blocks_full" : PASS == P_AMAX ? "blocks_amax" : PASS == P_QUANT ? "blocks_quant"
+                                                                                                    : "todense",
+                    st);
   if (cd == LM_F16)
     hipLaunchKernelGGL((k_blocks<F, F16, NKC, SR, FROM_DENSE, PASS, HAS_LORA>), dim3(nb), dim3(256), 0, st, a);
   else
@@ -1091,6 +1109,7 @@ static constexpr int ROW_CACHE = 8;
 template <int KIND, int CD, int SDT, bool ASYM, bool SR, bool FROM_DENSE>
 static int run_rows_nkc(const RowArgs& a, int nkc, int scale_dt, hipStream_t st) {
   dim3 grid((unsigned)((a.M + 15) / 16)), block(ROW_NW * 64);
+  TimedLaunch timed("rows", st);
   if (FROM_DENSE || nkc == 0) {
     hipLaunchKernelGGL((k_rows<KIND, CD, SDT, ASYM, SR, 1, FROM_DENSE, ROW_NW, ROW_CACHE>), grid, block, 0, st, a,
                        scale_dt);

@@ -44,6 +44,7 @@ static int stack_prep(PrepItem* preps, int32_t count, uint8_t* dev_items, hipStr
   HIP_TRY(hipMemcpyAsync(dev_items, preps, sizeof(PrepItem) * count, hipMemcpyHostToDevice, st));
   int64_t nb = (total + 255) / 256;
   if (nb > 8192) nb = 8192;
+  TimedLaunch timed("prep", st);
   hipLaunchKernelGGL(k_prep_many, dim3((unsigned)nb), dim3(256), 0, st, (const PrepItem*)dev_items, count, total);
   LAUNCH_CHECK();
   return LM_OK;
@@ -112,6 +113,7 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
   if (rc == LM_OK) {
     const bool sr = rounding_mode == LM_ROUND_STOCHASTIC;
     dim3 grid((unsigned)tiles), block(ROW_NW * 64);
+    TimedLaunch timed("rows_stack", st);
 #define RS(CD_, SDT_, SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_stack<K_INT8, CD_, SDT_, SR_, NKC_, ROW_NW, ROW_CACHE>), grid, block, 0, st, (const RowStackItem*)dev_rows, count, scale_dtype))
     if (cd == LM_F16) {
       if (scale_dtype == LM_BF16) { if (sr) { RS(F16, BF16, true); } else { RS(F16, BF16, false); } }

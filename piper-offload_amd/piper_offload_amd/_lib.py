@@ -82,6 +82,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lm_dense_merge": (_I32, [_P, _I64, _I64, _I64, _L, _P, _SZ, _P]),
     "lm_int8_merge_stack": (_I32, [ctypes.POINTER(StackItem), _I32, _I32, _I32, _P, _SZ, _P]),
     "lm_nvfp4_merge_stack": (_I32, [ctypes.POINTER(StackItem), _I32, _I32, _I32, _P, _SZ, _P]),
+    "lm_timer_enable": (_I32, [_I32]),
+    "lm_timer_read": (_I32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]),
 }
 
 _lock = threading.Lock()
@@ -121,6 +123,19 @@ def lib() -> ctypes.CDLL:
 
 def exported_symbols() -> list[str]:
     return list(_SIGNATURES)
+
+
+def timer_enable(enable: bool = True) -> None:
+    """Start (and clear) or stop the library's per-kernel-family HIP event timer."""
+    check(load_library().lm_timer_enable(int(enable)))
+
+
+def timer_read(family: str) -> tuple[float, int]:
+    """(summed milliseconds, launches) recorded for one kernel family; synchronizes its events."""
+    ms = ctypes.c_double(0.0)
+    n = ctypes.c_int64(0)
+    check(load_library().lm_timer_read(family.encode(), ctypes.byref(ms), ctypes.byref(n)))
+    return ms.value, n.value
 
 
 def check(rc: int) -> None:

@@ -80,7 +80,7 @@ class Int8Weight(PackedWeight):
         self.reduce_range = bool(reduce_range)
 
     @classmethod
-    def _logical(cls, qdata, scale, block_size, dtype_=torch.bfloat16, **_kw):  # noqa: ANN001, ANN206, ARG003
+    def _logical(cls, qdata, scale, block_size, dtype_=torch.bfloat16, *_a, **_kw):  # noqa: ANN001, ANN206, ARG003
         return tuple(qdata.shape), dtype_, qdata.device
 
 
@@ -98,7 +98,7 @@ class Float8Weight(PackedWeight):
         self.dtype_ = dtype_
 
     @classmethod
-    def _logical(cls, qdata, scale, block_size, dtype_=torch.bfloat16, **_kw):  # noqa: ANN001, ANN206, ARG003
+    def _logical(cls, qdata, scale, block_size, dtype_=torch.bfloat16, *_a, **_kw):  # noqa: ANN001, ANN206, ARG003
         return tuple(qdata.shape), dtype_, qdata.device
 
 
@@ -120,7 +120,7 @@ class NVFP4Weight(PackedWeight):
         self.is_swizzled_scales = bool(is_swizzled_scales)
 
     @classmethod
-    def _logical(cls, qdata, scale, per_tensor_scale=None, block_size=16, orig_dtype=torch.bfloat16, **_kw):  # noqa: ANN001, ANN206, ARG003
+    def _logical(cls, qdata, scale, per_tensor_scale=None, block_size=16, orig_dtype=torch.bfloat16, *_a, **_kw):  # noqa: ANN001, ANN206, ARG003
         return (qdata.shape[0], qdata.shape[1] * 2), orig_dtype, qdata.device
 
 
@@ -143,7 +143,7 @@ class MXWeight(PackedWeight):
         self.scaling_mode = scaling_mode
 
     @classmethod
-    def _logical(cls, qdata, scale, elem_dtype, block_size=32, orig_dtype=torch.bfloat16, **_kw):  # noqa: ANN001, ANN206, ARG003
+    def _logical(cls, qdata, scale, elem_dtype, block_size=32, orig_dtype=torch.bfloat16, *_a, **_kw):  # noqa: ANN001, ANN206, ARG003
         fp4 = getattr(torch, "float4_e2m1fn_x2", None)
         cols = qdata.shape[1] * 2 if elem_dtype is fp4 else qdata.shape[1]
         return (qdata.shape[0], cols), orig_dtype, qdata.device

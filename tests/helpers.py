@@ -70,3 +70,24 @@ def fp8_initial(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     scale = (wf.abs().amax(dim=1, keepdim=True) / 448.0).clamp_min(torch.finfo(torch.float32).eps)
     q = (wf / scale).clamp(-448, 448).to(torch.float8_e4m3fn)
     return q, scale
+
+
+MERGED_MISMATCH_FRACTION = 1e-3
+MERGED_ABS_REL = 2.0 ** -18
+
+
+def assert_merged_close(got: np.ndarray, ref: np.ndarray, base: np.ndarray) -> None:
+    """Tolerance contract for dense merged weights (bf16 bit patterns).
+
+    An element matches when it is within 1 bf16 ulp of the oracle, or within
+    2^-18 * (|base| + |oracle - base|) absolutely: when base and delta cancel,
+    the result is far smaller than its operands and a different fp32
+    summation order of B@A (the MFMA's) moves it by many of its own ulps.
+    At most 1e-3 of the elements may differ at all.
+    """
+    g, r, b = (O.bf16_to_f32(x).astype(np.float64) for x in (got, ref, base))
+    ulp = bf16_ulp_diff(got, ref)
+    tol = MERGED_ABS_REL * (np.abs(b) + np.abs(r - b))
+    bad = (ulp > 1) & (np.abs(g - r) > tol)
+    assert not bad.any(), f"{int(bad.sum())} merged values outside tolerance, first at {np.argwhere(bad)[0]}"
+    assert (ulp > 0).mean() <= MERGED_MISMATCH_FRACTION
