@@ -227,6 +227,39 @@ DEV uint32_t sr_fp8(float v, uint32_t h, float limit) {
   return interior ? (mb | sign) : (det | sign);
 }
 
+
+// ---- packed helpers for the fast paths -----------------------------------
+// two fp32 -> packed bf16 pair (RNE, v_cvt_pk_bf16_f32); low half = a
+DEV uint32_t pack_bf16x2(float a, float b) {
+  return (uint32_t)bf16_bits(a) | ((uint32_t)bf16_bits(b) << 16);
+}
+DEV float bf16_lo(uint32_t w) { return u2f(w << 16); }
+DEV float bf16_hi(uint32_t w) { return u2f(w & 0xffff0000u); }
+// per-halfword unsigned max (v_pk_max_u16)
+DEV uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+  us2 x = __builtin_bit_cast(us2, a), y = __builtin_bit_cast(us2, b);
+  us2 r = __builtin_elementwise_max(x, y);
+  return __builtin_bit_cast(uint32_t, r);
+}
+// low bytes of four 32-bit words -> one word (byte k from w_k)
+DEV uint32_t pack_low_bytes(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+  uint32_t lo = __builtin_amdgcn_perm(w1, w0, 0x0c0c0400u);
+  uint32_t hi = __builtin_amdgcn_perm(w3, w2, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+// Stochastic rounding of y >= 0 (or any sign) onto the integer grid with the
+// reference's rule  up <=> u < frac(y),  u = h * 2^-16  (h a 16-bit uniform):
+// with X = ceil(65536 * y),  result = floor((X + 65535 - h) / 65536).
+// y16 = 65536 * y must be exactly representable (|y| < 2^7 for fp32 inputs
+// of 24-bit precision keeps every step exact).  Equivalent to
+// lower + (u < frac) for all finite y; an integer y stays y.
+DEV int sr_grid(float y16, uint32_t h) {
+  int fneg = (int)__builtin_floorf(-y16);  // floor(-y16) = -ceil(y16)
+  return ((int)(65535u - h) - fneg) >> 16;
+}
+
 // ---- blocked (swizzled) scale offsets: P/_triton_nvfp4_lora.py:88-104,
 //      P/_triton_mx_lora.py:97-112 --------------------------------------
 DEV int64_t blocked_offset(int64_t row, int64_t scol, int64_t scols, bool swz) {

@@ -498,6 +498,199 @@ __global__ __launch_bounds__(NW * 64) void k_rows_stack(const RowStackItem* __re
   rows_body<KIND, CD, SDT, false, SR, NKC, false, NW, CACHE>(a, (t - items[lo].tile_begin) * 16, scale_dt);
 }
 
+
+// ---- fast per-row kernels -----------------------------------------------------
+// Specialization of rows_body for the production layouts: bf16 factors,
+// N % 64 == 0, INT8 symmetric with fp32 scales or scaled FP8 (fp32 scales).
+// Merged values stay packed bf16 (v_cvt_pk_bf16_f32) from pass 1 to pass 2,
+// the row amax is a packed 16-bit max over |bits|, round-to-nearest uses the
+// 1.5*2^23 magic add, and stochastic rounding uses sr_grid (an exact
+// reformulation of the reference's u < p selection).
+template <int KIND, int NKC>
+__device__ __forceinline__ void fast_merged_tile(const RowArgs& a, int64_t row, bool rok, int mt, int lane,
+                                                 const v4i16 (&bop)[NKC], float s_in, float base_off,
+                                                 uint32_t (&out)[8]) {
+  const int64_t N = a.N;
+  const int64_t c0 = (int64_t)mt * 64 + 16 * (lane >> 4);
+  uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+  if (rok) raw = *(const uint4*)((const uint8_t*)a.q + row * N + c0);
+  float d[16];
+  tile_delta<16, NKC, false>(a.at, (int64_t)mt * 64, lane, bop, d);
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t word = w[k >> 1];
+    const int b0 = (2 * k) & 3, b1 = (2 * k + 1) & 3;
+    float x0, x1;
+    if constexpr (KIND == K_INT8) {
+      // (u ^ 0x80) - 128 = signed byte: fma(u', s, -128 s) = RN(q * s) exactly
+      const uint32_t ws = word ^ 0x80808080u;
+      x0 = __builtin_fmaf((float)((ws >> (8 * b0)) & 0xffu), s_in, base_off);
+      x1 = __builtin_fmaf((float)((ws >> (8 * b1)) & 0xffu), s_in, base_off);
+    } else {
+      x0 = fp8_decode<FmtLimit<KIND>::fmt>(word, b0) * s_in;
+      x1 = fp8_decode<FmtLimit<KIND>::fmt>(word, b1) * s_in;
+    }
+    const uint32_t bb = pack_bf16x2(x0, x1);
+    const float m0 = __builtin_fmaf(d[2 * k], a.strength, bf16_lo(bb));
+    const float m1 = __builtin_fmaf(d[2 * k + 1], a.strength, bf16_hi(bb));
+    out[k] = pack_bf16x2(m0, m1);
+  }
+}
+
+template <int KIND, bool SR>
+__device__ __forceinline__ void fast_quant_store(const RowArgs& a, int64_t row, bool rok, int mt, int lane,
+                                                 const RowQP& qp, const uint32_t (&w)[8]) {
+  if (!rok) return;
+  const int64_t N = a.N;
+  const int64_t c0 = (int64_t)mt * 64 + 16 * (lane >> 4);
+  uint32_t h[16];
+  if constexpr (SR) sr_bits<16>(a.seed, (uint64_t)(row * N + c0), h);
+  uint32_t out[4];
+  if constexpr (KIND == K_INT8) {
+    const float qmin = (float)a.qmin, qmax = (float)a.qmax;
+    uint32_t y[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
+      if constexpr (SR) {
+        // 65536 * RN(m / s) with exact power-of-two scaling of the refinement
+        const float q0 = m * qp.inv;  // qp.inv = 65536 * RN(1/s)
+        const float e = __builtin_fmaf(-q0, qp.rcp, m);  // qp.rcp = s / 65536
+        const float y16 = __builtin_fmaf(e, qp.inv, q0);
+        int q = sr_grid(y16, h[j]);
+        q = q < a.qmin ? a.qmin : (q > a.qmax ? a.qmax : q);
+        y[j] = (uint32_t)q;
+      } else {
+        const float x = __builtin_amdgcn_fmed3f(m * qp.inv, qmin, qmax);
+        y[j] = f2u(x + 12582912.0f);  // low byte = rint(x) (two's complement)
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = pack_low_bytes(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+  } else {
+    constexpr float L = FmtLimit<KIND>::v;
+    constexpr int F = FmtLimit<KIND>::fmt;
+    float x[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
+      float v = __builtin_amdgcn_fmed3f(div_rn(m, qp.s, qp.rcp), -L, L);
+      if constexpr (SR) {
+        // grid spacing of the fp8 value: 2^(E - mbits), at least the subnormal step
+        constexpr int MB = F == E4M3 ? 3 : 2;
+        constexpr int MINE = F == E4M3 ? -9 : -16;
+        const float mag = __builtin_fabsf(v);
+        int e = (int)((f2u(mag) >> 23) & 255u) - 127 - MB;
+        e = e < MINE ? MINE : e;
+        const int q = sr_grid(__builtin_ldexpf(mag, 16 - e), h[j]);
+        v = __builtin_copysignf(__builtin_ldexpf((float)q, e), v);
+      }
+      x[j] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = fp8_pack4<F>(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+  }
+  *(uint4*)((uint8_t*)a.q_out + row * N + c0) = make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+template <int KIND, bool SR, int NKC, int NW, int CACHE>
+__device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
+  __shared__ float sh_mx[NW][16];
+  __shared__ float sh_qp[4][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
+  const int64_t row = row0 + rl;
+  const bool rok = row < a.M;
+  const int ntiles = (int)(a.N >> 6);
+  v4i16 bop[NKC];
+  load_bop<NKC>(a.bp, row, lane, bop);
+  float s_in = 0.0f, base_off = 0.0f;
+  if (rok) {
+    s_in = ((const float*)a.scale)[row];
+    base_off = -128.0f * s_in;
+  }
+  uint32_t cache[CACHE][8];
+  uint32_t pmax = 0u;
+#pragma unroll
+  for (int i = 0; i < CACHE; ++i) {
+    const int mt = wave + i * NW;
+    if (mt < ntiles) {
+      fast_merged_tile<KIND, NKC>(a, row, rok, mt, lane, bop, s_in, base_off, cache[i]);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) pmax = pk_max_u16(pmax, cache[i][k] & 0x7fff7fffu);
+    }
+  }
+  for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW) {
+    uint32_t t[8];
+    fast_merged_tile<KIND, NKC>(a, row, rok, mt, lane, bop, s_in, base_off, t);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) pmax = pk_max_u16(pmax, t[k] & 0x7fff7fffu);
+  }
+  float vmx = __builtin_fmaxf(bf16_lo(pmax), bf16_hi(pmax));
+  vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, 16));
+  vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, 32));
+  if ((lane >> 4) == 0) sh_mx[wave][rl] = vmx;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int t = threadIdx.x;
+    float mx = 0.0f;
+    for (int w = 0; w < NW; ++w) mx = __builtin_fmaxf(mx, sh_mx[w][t]);
+    const int64_t r = row0 + t;
+    float stored;
+    RowQP qp;
+    if constexpr (KIND == K_INT8) {
+      int zp;
+      qp = int8_qparams<BF16, F32, false>(-mx, mx, a.qmin, a.qmax, stored, zp);
+      if (r < a.M) ((float*)a.scale_out)[r] = stored;
+      if (r < a.M && a.zp_out) a.zp_out[r] = 0;
+      if constexpr (SR) {
+        qp.inv = qp.rcp * 65536.0f;  // 65536 * RN(1/s)
+        qp.rcp = qp.s * (1.0f / 65536.0f);
+      }
+    } else {
+      qp = fp8_qparams<BF16, KIND>(mx, stored);
+      if (r < a.M) ((float*)a.scale_out)[r] = stored;
+    }
+    sh_qp[0][t] = qp.s;
+    sh_qp[1][t] = qp.inv;
+    sh_qp[2][t] = qp.rcp;
+    sh_qp[3][t] = qp.zp;
+  }
+  __syncthreads();
+  RowQP qp;
+  qp.s = sh_qp[0][rl];
+  qp.inv = sh_qp[1][rl];
+  qp.rcp = sh_qp[2][rl];
+  qp.zp = sh_qp[3][rl];
+#pragma unroll
+  for (int i = 0; i < CACHE; ++i) {
+    const int mt = wave + i * NW;
+    if (mt < ntiles) fast_quant_store<KIND, SR>(a, row, rok, mt, lane, qp, cache[i]);
+  }
+  for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW) {
+    uint32_t t[8];
+    fast_merged_tile<KIND, NKC>(a, row, rok, mt, lane, bop, s_in, base_off, t);
+    fast_quant_store<KIND, SR>(a, row, rok, mt, lane, qp, t);
+  }
+}
+
+template <int KIND, bool SR, int NKC, int NW, int CACHE>
+__global__ __launch_bounds__(NW * 64) void k_rows_fast(RowArgs a) {
+  rows_fast_body<KIND, SR, NKC, NW, CACHE>(a, (int64_t)blockIdx.x * 16);
+}
+template <int KIND, bool SR, int NKC, int NW, int CACHE>
+__global__ __launch_bounds__(NW * 64) void k_rows_fast_stack(const RowStackItem* __restrict__ items, int count) {
+  int lo = 0, hi = count - 1;
+  const int64_t t = blockIdx.x;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (items[mid].tile_begin <= t) lo = mid;
+    else hi = mid - 1;
+  }
+  const RowArgs a = items[lo].a;
+  rows_fast_body<KIND, SR, NKC, NW, CACHE>(a, (t - items[lo].tile_begin) * 16);
+}
+
 // ---------------------------------------------------------------------------
 // k_blocks: block-local formats, dense weights, dequant, per-tensor passes
 // ---------------------------------------------------------------------------
@@ -1121,8 +1314,29 @@ static int run_rows_nkc(const RowArgs& a, int nkc, int scale_dt, hipStream_t st)
   return LM_OK;
 }
 
+// fast path eligibility: bf16 factors, N % 64 == 0, INT8 symmetric fp32 scales or FP8
+static inline bool rows_fast_ok(int kind, int cd, int sdt, bool asym, int nkc, int64_t N) {
+  return cd == LM_BF16 && nkc > 0 && (N % 64) == 0 && (kind != K_INT8 || (!asym && sdt == LM_F32));
+}
+
+template <int KIND, bool SR, int NKC>
+static int launch_rows_fast(const RowArgs& a, hipStream_t st) {
+  dim3 grid((unsigned)((a.M + 15) / 16)), block(ROW_NW * 64);
+  TimedLaunch timed("rows", st);
+  hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_CACHE>), grid, block, 0, st, a);
+  LAUNCH_CHECK();
+  return LM_OK;
+}
+
 template <int KIND, bool FROM_DENSE>
 static int run_rows(const RowArgs& a, int cd, int sdt, bool asym, bool sr, int nkc, hipStream_t st) {
+  if (!FROM_DENSE && rows_fast_ok(KIND, cd, sdt, asym, nkc, a.N)) {
+    if (sr) {
+      NKC_SWITCH(nkc_bucket(nkc), return (launch_rows_fast<KIND, true, NKC_>(a, st)));
+    } else {
+      NKC_SWITCH(nkc_bucket(nkc), return (launch_rows_fast<KIND, false, NKC_>(a, st)));
+    }
+  }
 #define RR(CD_, SDT_, AS_, SR_) return run_rows_nkc<KIND, CD_, SDT_, AS_, SR_, FROM_DENSE>(a, nkc, sdt, st)
   if (KIND != K_INT8) {
     asym = false;

@@ -114,6 +114,14 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
     const bool sr = rounding_mode == LM_ROUND_STOCHASTIC;
     dim3 grid((unsigned)tiles), block(ROW_NW * 64);
     TimedLaunch timed("rows_stack", st);
+    bool fast = true;
+    for (int i = 0; i < count; ++i)
+      fast = fast && rows_fast_ok(K_INT8, cd, scale_dtype, false, nkc_max, items[i].N);
+    if (fast) {
+#define RF(SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, ROW_CACHE>), grid, block, 0, st, (const RowStackItem*)dev_rows, count))
+      if (sr) { RF(true); } else { RF(false); }
+#undef RF
+    } else {
 #define RS(CD_, SDT_, SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_stack<K_INT8, CD_, SDT_, SR_, NKC_, ROW_NW, ROW_CACHE>), grid, block, 0, st, (const RowStackItem*)dev_rows, count, scale_dtype))
     if (cd == LM_F16) {
       if (scale_dtype == LM_BF16) { if (sr) { RS(F16, BF16, true); } else { RS(F16, BF16, false); } }
@@ -123,6 +131,7 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
       else { if (sr) { RS(BF16, F32, true); } else { RS(BF16, F32, false); } }
     }
 #undef RS
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "stack launch: %s", hipGetErrorString(e));
   }
