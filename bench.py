@@ -16,7 +16,7 @@ whole stack once, in place, through the grouped HIP kernel.
 ``cpu_baseline`` block times the CPU oracle (a C restatement of the same
 merge) on a bounded sample of the same workload.
 
-    python bench.py [--steps K] [--warmup W] [--workload int8_stack|nvfp4_stack|int8|fp8|q8_0|nvfp4|mxfp4]
+    python bench.py [--steps K] [--warmup W] [--workload int8_stack|nvfp4_stack|int8|fp8|q8_0|nvfp4|mxfp4|copy]
                     [--rounding stochastic|nearest] [--cpu-seconds S]
 """
 
@@ -52,7 +52,7 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="int8_stack",
-                   choices=["int8_stack", "nvfp4_stack", "int8", "fp8", "q8_0", "nvfp4", "mxfp4"])
+                   choices=["int8_stack", "nvfp4_stack", "int8", "fp8", "q8_0", "nvfp4", "mxfp4", "copy"])
     p.add_argument("--rounding", default="stochastic", choices=["stochastic", "nearest"])
     p.add_argument("--layers", type=int, default=32)
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-oracle baseline (0: skip)")
@@ -200,6 +200,29 @@ class Nvfp4Stack(Workload):
         merge_nvfp4_stack(self.targets, stochastic=self.stochastic)
 
 
+class Copy(Workload):
+    """Plain device copy (torch elementwise kernel, 1 GiB in + 1 GiB out): the achievable-HBM reference
+    and the byte-counter calibration for the rocprofv3 FETCH_SIZE / WRITE_SIZE traffic figures."""
+
+    family = ""
+
+    def __init__(self) -> None:
+        import torch
+
+        n = 1 << 28  # int32 elements = 1 GiB
+        self.src = torch.arange(n, device="cuda", dtype=torch.int32)
+        self.dst = torch.empty_like(self.src)
+        self.bytes_per_step = 2 * self.src.numel() * 4
+        self.name = "copy"
+        self.config = {"workload": "device copy 1 GiB -> 1 GiB (torch.bitwise_not on int32)",
+                       "algorithmic_bytes_per_step": self.bytes_per_step}
+
+    def step(self, index: int) -> None:
+        import torch
+
+        torch.bitwise_not(self.src, out=self.dst)
+
+
 class Single(Workload):
     """One tensor of configs 2-4 (or NVFP4 / MXFP4 at the gate_proj shape)."""
 
@@ -302,26 +325,23 @@ def cpu_baseline(kind: str, stochastic: bool, budget_s: float) -> dict | None:
             O.int8_requant(merged, cols, sr_mode=O.SR_PHILOX8 if stochastic else O.SR_OFF, seed=12345)
         def nbytes(rows):  # noqa: ANN001, ANN202
             return _int8_bytes(rows, cols, rank)
-        shape_note = f"gate_proj-shaped rows x {cols} (rank {rank})"
+        shape_note = f"{cols} gate_proj-shaped INT8 tensor (rank {rank})"
     else:
         return None
-    rows = 64
-    t0 = time.perf_counter()
-    run(make(rows))
-    dt = time.perf_counter() - t0
-    # size the sample to about budget_s / 3 per repeat, median of 3
-    rows = int(max(64, min(14336, rows * (budget_s / 3.0) / max(dt, 1e-3)))) // 16 * 16
+    # the sample is one full gate_proj-shaped tensor, merged repeatedly until
+    # the budget is spent (at least twice); throughput over every repeat
+    rows = 14336
     data = make(rows)
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
+    run(data)  # first touch of the buffers and the thread pool
+    reps, t0 = 0, time.perf_counter()
+    while reps < 2 or time.perf_counter() - t0 < budget_s:
         run(data)
-        times.append(time.perf_counter() - t0)
-    t = sorted(times)[1]
-    return {"value": round(nbytes(rows) / t / 1e9, 3), "unit": "GB/s", "cores": int(os.environ.get("OMP_NUM_THREADS", cores)),
-            "kind": "port",
-            "sample": f"oracle dequant + fp32 B@A + requant ({'SR' if stochastic else 'RTN'}) of {rows} {shape_note}, "
-                      f"median of 3 ({t:.2f} s each)"}
+        reps += 1
+    t = time.perf_counter() - t0
+    return {"value": round(nbytes(rows) * reps / t / 1e9, 3), "unit": "GB/s",
+            "cores": int(os.environ.get("OMP_NUM_THREADS", cores)), "kind": "port",
+            "sample": f"oracle dequant + fp32 B@A + requant ({'SR' if stochastic else 'RTN'}) of one {rows} x "
+                      f"{shape_note}, {reps} repeats in {t:.1f} s"}
 
 
 def _traffic(name: str) -> int | None:
@@ -351,6 +371,8 @@ def main() -> int:
     print(f"[bench] building workload {args.workload} ...", file=sys.stderr, flush=True)
     if args.workload == "int8_stack":
         wl: Workload = Int8Stack(args.layers, stochastic)
+    elif args.workload == "copy":
+        wl = Copy()
     elif args.workload == "nvfp4_stack":
         wl = Nvfp4Stack(args.layers, stochastic)
     else:
@@ -371,7 +393,7 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ev_ms = start.elapsed_time(stop)
-    kern_ms, launches = L.timer_read(wl.family)
+    kern_ms, launches = L.timer_read(wl.family) if wl.family else (ev_ms, args.steps)
     L.timer_enable(False)
     ms_per_step = ev_ms / args.steps
     value = wl.bytes_per_step / (ms_per_step * 1e-3) / 1e9

@@ -34,9 +34,18 @@ constexpr float kEps = 1.1920928955078125e-07f;  // torch.finfo(float32).eps
 DEV uint32_t f2u(float x) { return __float_as_uint(x); }
 DEV float u2f(uint32_t x) { return __uint_as_float(x); }
 
+typedef float v2f32 __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf16 __attribute__((ext_vector_type(2)));
+
 DEV uint16_t bf16_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
 DEV float bf16_val(uint32_t h) { return u2f(h << 16); }
-DEV float bf16r(float x) { return bf16_val(bf16_bits(x)); }
+// RNE bf16 of (a, b) packed low/high: one v_cvt_pk_bf16_f32
+DEV uint32_t pack_bf16x2(float a, float b) {
+  const v2f32 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, v2bf16));
+}
+// bf16-rounded x as an fp32 value: v_cvt_pk_bf16_f32 with x in the high half
+DEV float bf16r(float x) { return u2f(pack_bf16x2(0.0f, x)); }
 DEV uint16_t f16_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
 DEV float f16_val(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 DEV float f16r(float x) { return f16_val(f16_bits(x)); }
@@ -150,15 +159,16 @@ DEV void philox10(uint64_t ctr, uint64_t seed, uint32_t (&c)[4]) {
   c[2] = 0;
   c[3] = 0;
   uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+  // One round: both halves of each 32x32 product come from one v_mad_u64_u32
+  // and each output word is one v_bitop3_b32 (0x96 = a ^ b ^ c).
 #pragma unroll
   for (int r = 0; r < 10; ++r) {
-    uint32_t c0 = c[0], c2 = c[2];
-    uint32_t hb = __umulhi(0xCD9E8D57u, c2), ha = __umulhi(0xD2511F53u, c0);
-    uint32_t lb = 0xCD9E8D57u * c2, la = 0xD2511F53u * c0;
-    c[0] = hb ^ c[1] ^ k0;
-    c[2] = ha ^ c[3] ^ k1;
-    c[1] = lb;
-    c[3] = la;
+    const uint64_t pb = (uint64_t)c[2] * 0xCD9E8D57u;
+    const uint64_t pa = (uint64_t)c[0] * 0xD2511F53u;
+    c[0] = __builtin_amdgcn_bitop3_b32((uint32_t)(pb >> 32), c[1], k0, 0x96);
+    c[2] = __builtin_amdgcn_bitop3_b32((uint32_t)(pa >> 32), c[3], k1, 0x96);
+    c[1] = (uint32_t)pb;
+    c[3] = (uint32_t)pa;
     k0 += 0x9E3779B9u;
     k1 += 0xBB67AE85u;
   }
@@ -182,6 +192,18 @@ DEV void sr_bits(uint64_t seed, uint64_t idx0, uint32_t (&h)[SPAN]) {
       int jj = (int)(idx & 7);
       h[j] = (jj & 1) ? (c[jj >> 1] >> 16) : (c[jj >> 1] & 0xffffu);
     }
+  }
+}
+// The SPAN/2 Philox output words covering offsets idx0 .. idx0+SPAN-1 when idx0 % 8 == 0:
+// word k holds h for offsets idx0+2k (low half) and idx0+2k+1 (high half).
+template <int SPAN>
+DEV void sr_words_aligned(uint64_t seed, uint64_t idx0, uint32_t (&w)[SPAN / 2]) {
+#pragma unroll
+  for (int gi = 0; gi < SPAN / 8; ++gi) {
+    uint32_t c[4];
+    philox10((idx0 >> 3) + gi, seed, c);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[gi * 4 + k] = c[k];
   }
 }
 // u < p with u = h * 2^-16 (exact: both sides scaled by 2^16)
@@ -230,9 +252,6 @@ DEV uint32_t sr_fp8(float v, uint32_t h, float limit) {
 
 // ---- packed helpers for the fast paths -----------------------------------
 // two fp32 -> packed bf16 pair (RNE, v_cvt_pk_bf16_f32); low half = a
-DEV uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)bf16_bits(a) | ((uint32_t)bf16_bits(b) << 16);
-}
 DEV float bf16_lo(uint32_t w) { return u2f(w << 16); }
 DEV float bf16_hi(uint32_t w) { return u2f(w & 0xffff0000u); }
 // per-halfword unsigned max (v_pk_max_u16)
@@ -246,6 +265,12 @@ DEV uint32_t pk_max_u16(uint32_t a, uint32_t b) {
 DEV uint32_t pack_low_bytes(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
   uint32_t lo = __builtin_amdgcn_perm(w1, w0, 0x0c0c0400u);
   uint32_t hi = __builtin_amdgcn_perm(w3, w2, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+// byte 2 of four 32-bit words -> one word (byte k from w_k)
+DEV uint32_t pack_byte2s(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+  uint32_t lo = __builtin_amdgcn_perm(w1, w0, 0x0c0c0602u);
+  uint32_t hi = __builtin_amdgcn_perm(w3, w2, 0x0c0c0602u);
   return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 

@@ -506,17 +506,40 @@ __global__ __launch_bounds__(NW * 64) void k_rows_stack(const RowStackItem* __re
 // the row amax is a packed 16-bit max over |bits|, round-to-nearest uses the
 // 1.5*2^23 magic add, and stochastic rounding uses sr_grid (an exact
 // reformulation of the reference's u < p selection).
+// Global inputs of one 64-column macro tile for one lane: 16 codes of its row
+// and the 4 A^T operands of its MFMAs.  Loading is split from the arithmetic
+// so that a wave can have several tiles' loads in flight.
+template <int NKC>
+struct FastTileIn {
+  uint4 raw;
+  v4i16 aop[4][NKC];
+};
+
+template <int NKC>
+__device__ __forceinline__ void fast_load_tile(const RowArgs& a, int64_t rowc, int mt, int lane,
+                                               FastTileIn<NKC>& t) {
+  constexpr int RPAD = NKC * 16;
+  const int p = lane & 15, g = lane >> 4;
+  t.raw = *(const uint4*)((const uint8_t*)a.q + rowc * a.N + (int64_t)mt * 64 + 16 * g);
+  const int64_t colbase = (int64_t)mt * 64 + 16 * (p >> 2) + (p & 3);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) load_kchunks<NKC>(a.at + (colbase + 4 * k) * RPAD + g * (NKC * 4), t.aop[k]);
+}
+
 template <int KIND, int NKC>
-__device__ __forceinline__ void fast_merged_tile(const RowArgs& a, int64_t row, bool rok, int mt, int lane,
+__device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const FastTileIn<NKC>& in,
                                                  const v4i16 (&bop)[NKC], float s_in, float base_off,
                                                  uint32_t (&out)[8]) {
-  const int64_t N = a.N;
-  const int64_t c0 = (int64_t)mt * 64 + 16 * (lane >> 4);
-  uint4 raw = make_uint4(0u, 0u, 0u, 0u);
-  if (rok) raw = *(const uint4*)((const uint8_t*)a.q + row * N + c0);
   float d[16];
-  tile_delta<16, NKC, false>(a.at, (int64_t)mt * 64, lane, bop, d);
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const v4f32 acc = mfma_chain<NKC, false>(in.aop[k], bop);
+    d[4 * k + 0] = acc[0];
+    d[4 * k + 1] = acc[1];
+    d[4 * k + 2] = acc[2];
+    d[4 * k + 3] = acc[3];
+  }
+  const uint32_t w[4] = {in.raw.x, in.raw.y, in.raw.z, in.raw.w};
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const uint32_t word = w[k >> 1];
@@ -531,9 +554,8 @@ __device__ __forceinline__ void fast_merged_tile(const RowArgs& a, int64_t row, 
       x0 = fp8_decode<FmtLimit<KIND>::fmt>(word, b0) * s_in;
       x1 = fp8_decode<FmtLimit<KIND>::fmt>(word, b1) * s_in;
     }
-    const uint32_t bb = pack_bf16x2(x0, x1);
-    const float m0 = __builtin_fmaf(d[2 * k], a.strength, bf16_lo(bb));
-    const float m1 = __builtin_fmaf(d[2 * k + 1], a.strength, bf16_hi(bb));
+    const float m0 = __builtin_fmaf(d[2 * k], a.strength, bf16r(x0));
+    const float m1 = __builtin_fmaf(d[2 * k + 1], a.strength, bf16r(x1));
     out[k] = pack_bf16x2(m0, m1);
   }
 }
@@ -544,30 +566,43 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, int64_t row, 
   if (!rok) return;
   const int64_t N = a.N;
   const int64_t c0 = (int64_t)mt * 64 + 16 * (lane >> 4);
-  uint32_t h[16];
-  if constexpr (SR) sr_bits<16>(a.seed, (uint64_t)(row * N + c0), h);
+  // N % 64 == 0 and c0 % 16 == 0: the lane's 16 offsets start a Philox block
+  uint32_t rw[8];
+  if constexpr (SR) sr_words_aligned<16>(a.seed, (uint64_t)(row * N + c0), rw);
   uint32_t out[4];
   if constexpr (KIND == K_INT8) {
-    const float qmin = (float)a.qmin, qmax = (float)a.qmax;
     uint32_t y[16];
+    if constexpr (SR) {
+      // Stochastic rounding of y = RN(m / s): q = floor(y) + [h * 2^-16 < frac(y)].
+      // With Y = 65536 y (exact) and T = ceil(Y), q = (T + 65535 - h) >> 16.
+      // Y is first clamped to [qmin, qmax] * 65536, which yields the bound for
+      // exactly the inputs the reference keeps at their (clamped) RTN code.
+      // The code byte is bit 16..23 of T + 65535 - h, picked by v_perm.
+      const float lo16 = (float)a.qmin * 65536.0f, hi16 = (float)a.qmax * 65536.0f;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
-      if constexpr (SR) {
-        // 65536 * RN(m / s) with exact power-of-two scaling of the refinement
+      for (int j = 0; j < 16; ++j) {
+        const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
         const float q0 = m * qp.inv;  // qp.inv = 65536 * RN(1/s)
         const float e = __builtin_fmaf(-q0, qp.rcp, m);  // qp.rcp = s / 65536
-        const float y16 = __builtin_fmaf(e, qp.inv, q0);
-        int q = sr_grid(y16, h[j]);
-        q = q < a.qmin ? a.qmin : (q > a.qmax ? a.qmax : q);
-        y[j] = (uint32_t)q;
-      } else {
+        const float y16 = __builtin_amdgcn_fmed3f(__builtin_fmaf(e, qp.inv, q0), lo16, hi16);
+        const int tneg = (int)__builtin_floorf(-y16);  // -ceil(Y)
+        const uint32_t nw = ~rw[j >> 1];                 // 65535 - h in each half
+        const uint32_t nh = (j & 1) ? (nw >> 16) : (nw & 0xffffu);
+        y[j] = nh - (uint32_t)tneg;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[i] = pack_byte2s(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+    } else {
+      const float qmin = (float)a.qmin, qmax = (float)a.qmax;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
         const float x = __builtin_amdgcn_fmed3f(m * qp.inv, qmin, qmax);
         y[j] = f2u(x + 12582912.0f);  // low byte = rint(x) (two's complement)
       }
-    }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = pack_low_bytes(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+      for (int i = 0; i < 4; ++i) out[i] = pack_low_bytes(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+    }
   } else {
     constexpr float L = FmtLimit<KIND>::v;
     constexpr int F = FmtLimit<KIND>::fmt;
@@ -580,10 +615,11 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, int64_t row, 
         // grid spacing of the fp8 value: 2^(E - mbits), at least the subnormal step
         constexpr int MB = F == E4M3 ? 3 : 2;
         constexpr int MINE = F == E4M3 ? -9 : -16;
+        const uint32_t h = (j & 1) ? (rw[j >> 1] >> 16) : (rw[j >> 1] & 0xffffu);
         const float mag = __builtin_fabsf(v);
         int e = (int)((f2u(mag) >> 23) & 255u) - 127 - MB;
         e = e < MINE ? MINE : e;
-        const int q = sr_grid(__builtin_ldexpf(mag, 16 - e), h[j]);
+        const int q = sr_grid(__builtin_ldexpf(mag, 16 - e), h);
         v = __builtin_copysignf(__builtin_ldexpf((float)q, e), v);
       }
       x[j] = v;
@@ -594,13 +630,23 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, int64_t row, 
   *(uint4*)((uint8_t*)a.q_out + row * N + c0) = make_uint4(out[0], out[1], out[2], out[3]);
 }
 
-template <int KIND, bool SR, int NKC, int NW, int CACHE>
+// Tiles whose loads a wave keeps in flight ahead of the arithmetic.  One
+// FastTileIn holds 12, 20 or 36 VGPRs for NKC 1, 2, 4; rank 16 with 4 tiles in
+// flight stays under 128 VGPRs (two 512-thread workgroups per CU), which
+// measured faster on the 8B stack than 2 or 8 tiles.
+template <int NKC>
+constexpr int fast_prefetch() { return NKC == 1 ? 4 : 2; }
+
+template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC>()>
 __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   __shared__ float sh_mx[NW][16];
   __shared__ float sh_qp[4][16];
+  constexpr int PF = PF_ < CACHE ? PF_ : CACHE;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int64_t row = row0 + rl;
   const bool rok = row < a.M;
+  // rows past M load row M-1 (valid memory); their results are never stored
+  const int64_t rowc = rok ? row : a.M - 1;
   const int ntiles = (int)(a.N >> 6);
   v4i16 bop[NKC];
   load_bop<NKC>(a.bp, row, lane, bop);
@@ -611,20 +657,45 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   }
   uint32_t cache[CACHE][8];
   uint32_t pmax = 0u;
+  if (wave + (CACHE - 1) * NW < ntiles) {
+    // every cache slot holds a tile: branch-free, PF tiles of loads in flight
+    FastTileIn<NKC> in[CACHE];
 #pragma unroll
-  for (int i = 0; i < CACHE; ++i) {
-    const int mt = wave + i * NW;
-    if (mt < ntiles) {
-      fast_merged_tile<KIND, NKC>(a, row, rok, mt, lane, bop, s_in, base_off, cache[i]);
+    for (int i = 0; i < PF; ++i) fast_load_tile<NKC>(a, rowc, wave + i * NW, lane, in[i]);
+#pragma unroll
+    for (int i = 0; i < CACHE; ++i) {
+      if (i + PF < CACHE) fast_load_tile<NKC>(a, rowc, wave + (i + PF) * NW, lane, in[i + PF]);
+      fast_merged_tile<KIND, NKC>(a, in[i], bop, s_in, base_off, cache[i]);
 #pragma unroll
       for (int k = 0; k < 8; ++k) pmax = pk_max_u16(pmax, cache[i][k] & 0x7fff7fffu);
     }
-  }
-  for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW) {
-    uint32_t t[8];
-    fast_merged_tile<KIND, NKC>(a, row, rok, mt, lane, bop, s_in, base_off, t);
+  } else {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) pmax = pk_max_u16(pmax, t[k] & 0x7fff7fffu);
+    for (int i = 0; i < CACHE; ++i) {
+      const int mt = wave + i * NW;
+      if (mt < ntiles) {
+        FastTileIn<NKC> in;
+        fast_load_tile<NKC>(a, rowc, mt, lane, in);
+        fast_merged_tile<KIND, NKC>(a, in, bop, s_in, base_off, cache[i]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) pmax = pk_max_u16(pmax, cache[i][k] & 0x7fff7fffu);
+      }
+    }
+  }
+  // tiles beyond the cache: one tile of loads ahead (the last prefetch
+  // re-reads the final tile instead of branching)
+  if (wave + CACHE * NW < ntiles) {
+    FastTileIn<NKC> cur;
+    fast_load_tile<NKC>(a, rowc, wave + CACHE * NW, lane, cur);
+    for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW) {
+      FastTileIn<NKC> nxt;
+      fast_load_tile<NKC>(a, rowc, mt + NW < ntiles ? mt + NW : mt, lane, nxt);
+      uint32_t t[8];
+      fast_merged_tile<KIND, NKC>(a, cur, bop, s_in, base_off, t);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) pmax = pk_max_u16(pmax, t[k] & 0x7fff7fffu);
+      cur = nxt;
+    }
   }
   float vmx = __builtin_fmaxf(bf16_lo(pmax), bf16_hi(pmax));
   vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, 16));
@@ -667,10 +738,17 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
     const int mt = wave + i * NW;
     if (mt < ntiles) fast_quant_store<KIND, SR>(a, row, rok, mt, lane, qp, cache[i]);
   }
-  for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW) {
-    uint32_t t[8];
-    fast_merged_tile<KIND, NKC>(a, row, rok, mt, lane, bop, s_in, base_off, t);
-    fast_quant_store<KIND, SR>(a, row, rok, mt, lane, qp, t);
+  if (wave + CACHE * NW < ntiles) {
+    FastTileIn<NKC> cur;
+    fast_load_tile<NKC>(a, rowc, wave + CACHE * NW, lane, cur);
+    for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW) {
+      FastTileIn<NKC> nxt;
+      fast_load_tile<NKC>(a, rowc, mt + NW < ntiles ? mt + NW : mt, lane, nxt);
+      uint32_t t[8];
+      fast_merged_tile<KIND, NKC>(a, cur, bop, s_in, base_off, t);
+      fast_quant_store<KIND, SR>(a, row, rok, mt, lane, qp, t);
+      cur = nxt;
+    }
   }
 }
 
@@ -678,7 +756,7 @@ template <int KIND, bool SR, int NKC, int NW, int CACHE>
 __global__ __launch_bounds__(NW * 64) void k_rows_fast(RowArgs a) {
   rows_fast_body<KIND, SR, NKC, NW, CACHE>(a, (int64_t)blockIdx.x * 16);
 }
-template <int KIND, bool SR, int NKC, int NW, int CACHE>
+template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC>()>
 __global__ __launch_bounds__(NW * 64) void k_rows_fast_stack(const RowStackItem* __restrict__ items, int count) {
   int lo = 0, hi = count - 1;
   const int64_t t = blockIdx.x;
@@ -688,7 +766,7 @@ __global__ __launch_bounds__(NW * 64) void k_rows_fast_stack(const RowStackItem*
     else hi = mid - 1;
   }
   const RowArgs a = items[lo].a;
-  rows_fast_body<KIND, SR, NKC, NW, CACHE>(a, (t - items[lo].tile_begin) * 16);
+  rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_>(a, (t - items[lo].tile_begin) * 16);
 }
 
 // ---------------------------------------------------------------------------
