@@ -165,7 +165,7 @@ class Int8Stack(Workload):
 
 
 class Nvfp4Stack(Workload):
-    family = "blocks_quant"
+    family = "nvfp4"  # amax pass + quant pass of the two-level merge
 
     def __init__(self, layers: int, stochastic: bool) -> None:
         from piper_offload_amd.stack import StackTarget
@@ -255,7 +255,7 @@ class Single(Workload):
         elif kind == "nvfp4":
             rows, cols, rank, self.strength = 14336, 4096, 16, 1.0
             self.w = _nvfp4_weight(self.path, rows, cols)
-            self.family = "blocks_quant"
+            self.family = "nvfp4"
             self.bytes_per_step = _nvfp4_bytes(rows, cols, rank)
         else:  # mxfp4
             rows, cols, rank, self.strength = 14336, 4096, 16, 1.0
@@ -399,8 +399,9 @@ def main() -> int:
     value = wl.bytes_per_step / (ms_per_step * 1e-3) / 1e9
     print(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step (events), wall {wall / args.steps * 1e3:.3f} ms/step, "
           f"{wl.family}: {launches} launches {kern_ms / max(launches, 1):.3f} ms avg", file=sys.stderr, flush=True)
-    per_launch_bytes = wl.bytes_per_step * args.steps / max(launches, 1)
-    achieved = per_launch_bytes / (kern_ms / max(launches, 1) * 1e-3) / 1e9 if launches else None
+    # the dominant kernel family's time per step (one launch, or the amax +
+    # quant launches of a two-level NVFP4 merge) against the step's bytes
+    achieved = wl.bytes_per_step * args.steps / (kern_ms * 1e-3) / 1e9 if launches else None
     print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
     cpu = cpu_baseline(args.workload, stochastic, args.cpu_seconds)
     out = {

@@ -1,5 +1,5 @@
 // lm_nvfp4.hip -- NVFP4 (TorchAO NVFP4Tensor) entry points.
-#include "lm_impl.h"
+#include "lm_nvfp4_fast.h"
 
 // ---------------------------------------------------------------------------
 // NVFP4
@@ -27,6 +27,24 @@ static int nvfp4_common(const uint8_t* q, const uint8_t* scale, const float* pts
   a.aux_out = pts_out;
   a.swizzled = swz;
   if (swz && (rc = zero_swizzle_pad(scale_out, M, N / 16, c.st))) return rc;
+  if (lora && !dense && nv_fast_ok(cd, c.nkc, N)) {
+    NvArgs na;
+    na.q = q;
+    na.scale = scale;
+    na.gin = two_level ? pts : nullptr;
+    na.q_out = q_out;
+    na.scale_out = scale_out;
+    na.gout = pts_out;
+    na.at = c.at;
+    na.bp = c.bp;
+    na.red = c.red;
+    na.M = M;
+    na.N = N;
+    na.strength = lora->strength;
+    na.swizzled = swz;
+    na.seed = rnd ? rnd->seed : 0;
+    return nv_fast_run(na, c.nkc, sr, c.st);
+  }
   if (two_level) {
     if ((rc = run_blocks<B_NVFP4, P_AMAX>(a, cd, c.nkc, false, dense != nullptr, c.st))) return rc;
     if ((rc = run_blocks<B_NVFP4, P_QUANT>(a, cd, c.nkc, sr, dense != nullptr, c.st))) return rc;

@@ -1,0 +1,315 @@
+// lm_nvfp4_fast.h -- NVFP4 merge kernels for the production layout: bf16
+// factors, N % 128 == 0, one or two scale levels, plain or 128x4-swizzled
+// block scales.  P/ = the reference's src/piper_offload/.
+//
+// Work decomposition: a 512-thread workgroup (8 waves) owns 16 rows; each
+// wave walks the 128-column macro tiles mt = wave, wave + 8, ...  A lane holds
+// row (lane & 15) and the 32 consecutive columns 32*(lane >> 4) .. +31 of a
+// macro tile: two NVFP4 blocks, i.e. one 16-byte code load and one 2-byte
+// scale load, so block reductions never leave the lane.  The delta of a
+// macro tile is 8 x NKC v_mfma_f32_16x16x16_bf16 (tile_delta's SPAN = 32
+// orientation).
+//
+// Two-level tensors take two passes (P/_triton_nvfp4_lora.py:437-512, 327-366):
+//   k_nv_amax  -- max |merged| over the tensor into red[0] (float bits, so
+//                 atomicMax on uint orders them); the reference reduces
+//                 bf16(merged), and since RNE is monotone the max of the
+//                 rounded values is the rounded max of the unrounded ones;
+//   k_nv_quant -- g = max(amax / 2688, eps); per block s = e4m3(clamp(
+//                 (bmax / 6) / g, 2^-6, 448)); codes = e2m1(merged * ((1/g)/s));
+//   k_nv_finalize -- writes g once every quant workgroup has read the inputs
+//                 (the outputs may alias them).
+// Single-level tensors skip the amax pass and divide by the block scale.
+#pragma once
+#include "lm_impl.h"
+
+struct NvArgs {
+  const uint8_t* q;        // [M, N/2] e2m1 pairs, even column in the low nibble
+  const uint8_t* scale;    // e4m3 block-16 scales (plain [M, N/16] or swizzled)
+  const float* gin;        // input per-tensor scale; nullptr = single level
+  uint8_t* q_out;
+  uint8_t* scale_out;
+  float* gout;             // output per-tensor scale (two-level)
+  const uint16_t* at;
+  const uint16_t* bp;
+  uint32_t* red;           // red[0]: max |merged| bits (cleared by the prep kernel)
+  int64_t M, N;
+  float strength;
+  int swizzled;
+  uint64_t seed;
+};
+struct NvStackItem {
+  NvArgs a;
+  int64_t tile_begin;  // prefix of 16-row groups
+};
+
+constexpr int NV_NW = 8;
+
+// decode the two e2m1 codes of byte `b` of w to fp32 (low nibble -> .x)
+DEV v2f32 e2m1_pair(uint32_t w, int b) {
+  switch (b) {
+    case 0: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
+    case 1: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
+    case 2: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
+    default: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+  }
+}
+
+template <int NKC>
+struct NvTileIn {
+  uint4 codes;
+  uint32_t sc;  // the lane's two block-scale bytes
+  v4i16 aop[8][NKC];
+};
+
+template <int NKC>
+DEV void nv_load_tile(const NvArgs& a, int64_t rowc, int mt, int lane, NvTileIn<NKC>& t) {
+  constexpr int RPAD = NKC * 16;
+  const int p = lane & 15, g = lane >> 4;
+  const int64_t c0 = (int64_t)mt * 128 + 32 * g;
+  t.codes = *(const uint4*)(a.q + rowc * (a.N >> 1) + (c0 >> 1));
+  // c0/16 is even: both blocks' scales are adjacent bytes in either layout
+  t.sc = *(const uint16_t*)(a.scale + blocked_offset(rowc, c0 >> 4, a.N >> 4, a.swizzled));
+  const int64_t colbase = (int64_t)mt * 128 + 32 * (p >> 2) + (p & 3);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) load_kchunks<NKC>(a.at + (colbase + 4 * k) * RPAD + g * (NKC * 4), t.aop[k]);
+}
+
+// merged values of the lane's 32 columns; ZFIX applies the reference's
+// "update == 0 keeps the base" rule (P/_triton_nvfp4_lora.py:183-186), which
+// only changes the sign of a zero and so is not needed for max |merged|.
+template <int NKC, bool ZFIX>
+DEV void nv_merged(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], bool two, float gin,
+                   float (&m)[32]) {
+  float d[32];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const v4f32 acc = mfma_chain<NKC, false>(in.aop[k], bop);
+    d[4 * k + 0] = acc[0];
+    d[4 * k + 1] = acc[1];
+    d[4 * k + 2] = acc[2];
+    d[4 * k + 3] = acc[3];
+  }
+  float bs[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    float v = fp8_decode<E4M3>(in.sc, b);  // e4m3 is exact in bf16
+    bs[b] = two ? bf16r(v * gin) : v;
+  }
+  const uint32_t w[4] = {in.codes.x, in.codes.y, in.codes.z, in.codes.w};
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const v2f32 pr = e2m1_pair(w[q >> 2], q & 3);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int j = 2 * q + e;
+      const float base = bf16r(pr[e] * bs[j >> 4]);
+      const float mm = __builtin_fmaf(d[j], a.strength, base);
+      if constexpr (ZFIX) m[j] = (d[j] * a.strength == 0.0f) ? base : mm;
+      else m[j] = mm;
+    }
+  }
+}
+
+// Stochastic e2m1 code of a clamped value v (|v| <= 6) with h = 16 random
+// bits: the grid step below 2 is 0.5, then 1, then 2, so with e the step's
+// exponent, Y = |v| * 2^(16-e) is exact and q = (ceil(Y) + 65535 - h) >> 16
+// is floor(|v|/2^e) + [h * 2^-16 < frac]; exact and saturated values keep
+// their code (P/_triton_stochastic_quantization.py:110-130).
+DEV float nv_sr_value(float v, uint32_t nh) {
+  const float mag = __builtin_fabsf(v);
+  int ex = __builtin_amdgcn_frexp_expf(mag);  // floor(log2 mag) + 1 (0 for 0)
+  ex = ex < 1 ? 1 : (ex > 3 ? 3 : ex);        // e = ex - 2 in {-1, 0, 1}
+  const float y = __builtin_ldexpf(mag, 18 - ex);
+  const int tneg = (int)__builtin_floorf(-y);
+  const int q = (int)(nh - (uint32_t)tneg) >> 16;
+  return __builtin_copysignf(__builtin_ldexpf((float)q, ex - 2), v);
+}
+
+template <int NKC>
+DEV void nv_quant_store(const NvArgs& a, int64_t row, int mt, int lane, bool two, float gq, float inv_g, bool sr,
+                        const float (&m)[32]) {
+  const int64_t N = a.N;
+  const int64_t c0 = (int64_t)mt * 128 + 32 * (lane >> 4);
+  uint32_t rw[16];
+  if (sr) sr_words_aligned<32>(a.seed, (uint64_t)(row * N + c0), rw);
+  uint32_t words[4];
+  uint32_t scb = 0;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    float mb[16];
+    float bmax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      mb[j] = bf16r(m[16 * b + j]);
+      bmax = __builtin_fmaxf(bmax, __builtin_fabsf(mb[j]));
+    }
+    float fs = bmax / 6.0f;
+    if (two) fs = fs / gq;
+    fs = __builtin_fminf(__builtin_fmaxf(fs, 0.015625f), 448.0f);
+    const uint32_t s8 = fp8_encode1<E4M3>(fs);
+    fs = fp8_value<E4M3>(s8);
+    scb |= s8 << (8 * b);
+    const float recip = inv_g / fs, rfs = 1.0f / fs;
+    float x[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      float v = two ? mb[j] * recip : div_rn(mb[j], fs, rfs);
+      if (sr) {
+        const uint32_t nw = ~rw[(16 * b + j) >> 1];
+        const uint32_t nh = (j & 1) ? (nw >> 16) : (nw & 0xffffu);
+        v = nv_sr_value(__builtin_amdgcn_fmed3f(v, -6.0f, 6.0f), nh);
+      }
+      x[j] = v;  // the e2m1 conversion saturates to +-6 (checked on gfx950)
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      uint32_t wd = 0;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        wd |= (__builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, x[8 * k + 2 * t], x[8 * k + 2 * t + 1], 1.0f, 0) & 0xffu)
+              << (8 * t);
+      words[2 * b + k] = wd;
+    }
+  }
+  *(uint4*)(a.q_out + row * (N >> 1) + (c0 >> 1)) = make_uint4(words[0], words[1], words[2], words[3]);
+  *(uint16_t*)(a.scale_out + blocked_offset(row, c0 >> 4, N >> 4, a.swizzled)) = (uint16_t)scb;
+}
+
+// ---- pass bodies -------------------------------------------------------------
+template <int NKC>
+DEV void nv_amax_body(const NvArgs& a, int64_t row0) {
+  __shared__ float sh[NV_NW];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
+  const int64_t row = row0 + rl;
+  const bool rok = row < a.M;
+  const int64_t rowc = rok ? row : a.M - 1;  // in-bounds loads; results dropped
+  const int ntiles = (int)(a.N >> 7);
+  const float gin = *a.gin;
+  v4i16 bop[NKC];
+  load_bop<NKC>(a.bp, row, lane, bop);
+  float mx = 0.0f;
+  if (wave < ntiles) {
+    NvTileIn<NKC> cur;
+    nv_load_tile<NKC>(a, rowc, wave, lane, cur);
+    for (int mt = wave; mt < ntiles; mt += NV_NW) {
+      NvTileIn<NKC> nxt;
+      nv_load_tile<NKC>(a, rowc, mt + NV_NW < ntiles ? mt + NV_NW : mt, lane, nxt);
+      float m[32];
+      nv_merged<NKC, false>(a, cur, bop, true, gin, m);
+#pragma unroll
+      for (int j = 0; j < 32; ++j) mx = __builtin_fmaxf(mx, __builtin_fabsf(m[j]));
+      cur = nxt;
+    }
+  }
+  mx = rok ? mx : 0.0f;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) sh[wave] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float r = sh[0];
+#pragma unroll
+    for (int w = 1; w < NV_NW; ++w) r = __builtin_fmaxf(r, sh[w]);
+    atomicMax(a.red, f2u(bf16r(r)));
+  }
+}
+
+template <int NKC, bool SR>
+DEV void nv_quant_body(const NvArgs& a, int64_t row0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
+  const int64_t row = row0 + rl;
+  const bool rok = row < a.M;
+  const int64_t rowc = rok ? row : a.M - 1;
+  const int ntiles = (int)(a.N >> 7);
+  const bool two = a.gin != nullptr;
+  const float gin = two ? *a.gin : 1.0f;
+  float gq = 1.0f, inv_g = 1.0f;
+  if (two) {
+    gq = __builtin_fmaxf(u2f(*a.red) / 2688.0f, kEps);
+    inv_g = 1.0f / gq;
+  }
+  v4i16 bop[NKC];
+  load_bop<NKC>(a.bp, row, lane, bop);
+  if (wave >= ntiles) return;
+  NvTileIn<NKC> cur;
+  nv_load_tile<NKC>(a, rowc, wave, lane, cur);
+  for (int mt = wave; mt < ntiles; mt += NV_NW) {
+    NvTileIn<NKC> nxt;
+    nv_load_tile<NKC>(a, rowc, mt + NV_NW < ntiles ? mt + NV_NW : mt, lane, nxt);
+    float m[32];
+    nv_merged<NKC, true>(a, cur, bop, two, gin, m);
+    if (rok) nv_quant_store<NKC>(a, row, mt, lane, two, gq, inv_g, SR, m);
+    cur = nxt;
+  }
+}
+
+DEV int nv_find(const NvStackItem* __restrict__ items, int count, int64_t t) {
+  int lo = 0, hi = count - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (items[mid].tile_begin <= t) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// ---- kernels: single tensor (args by value) and grouped (descriptor table) ---
+template <int NKC>
+__global__ __launch_bounds__(NV_NW * 64) void k_nv_amax(NvArgs a) {
+  nv_amax_body<NKC>(a, (int64_t)blockIdx.x * 16);
+}
+template <int NKC, bool SR>
+__global__ __launch_bounds__(NV_NW * 64) void k_nv_quant(NvArgs a) {
+  nv_quant_body<NKC, SR>(a, (int64_t)blockIdx.x * 16);
+}
+template <int NKC>
+__global__ __launch_bounds__(NV_NW * 64) void k_nv_amax_stack(const NvStackItem* __restrict__ items, int count) {
+  const int i = nv_find(items, count, blockIdx.x);
+  const NvArgs a = items[i].a;
+  if (a.gin == nullptr) return;  // single-level item: no global scale to find
+  nv_amax_body<NKC>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16);
+}
+template <int NKC, bool SR>
+__global__ __launch_bounds__(NV_NW * 64) void k_nv_quant_stack(const NvStackItem* __restrict__ items, int count) {
+  const int i = nv_find(items, count, blockIdx.x);
+  const NvArgs a = items[i].a;
+  nv_quant_body<NKC, SR>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16);
+}
+// one thread per item: g = max(amax / 2688, eps)
+static __global__ void k_nv_finalize(const NvStackItem* __restrict__ items, int count) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  const NvArgs& a = items[i].a;
+  if (a.gin != nullptr && a.gout != nullptr) *a.gout = __builtin_fmaxf(u2f(*a.red) / 2688.0f, kEps);
+}
+static __global__ void k_nv_finalize1(NvArgs a) {
+  if (threadIdx.x == 0 && a.gin != nullptr && a.gout != nullptr) *a.gout = __builtin_fmaxf(u2f(*a.red) / 2688.0f, kEps);
+}
+
+// bf16 factors, a rank bucket, whole macro tiles
+static inline bool nv_fast_ok(int cd, int nkc, int64_t N) { return cd == LM_BF16 && nkc > 0 && (N % 128) == 0; }
+
+// single tensor: amax (two-level), quant, finalize on `st`
+static int nv_fast_run(const NvArgs& a, int nkc, bool sr, hipStream_t st) {
+  const dim3 grid((unsigned)((a.M + 15) / 16)), block(NV_NW * 64);
+  if (a.gin) {
+    TimedLaunch timed("nvfp4", st);
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_amax<NKC_>), grid, block, 0, st, a));
+    LAUNCH_CHECK();
+  }
+  {
+    TimedLaunch timed("nvfp4", st);
+    if (sr) {
+      NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant<NKC_, true>), grid, block, 0, st, a));
+    } else {
+      NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant<NKC_, false>), grid, block, 0, st, a));
+    }
+    LAUNCH_CHECK();
+  }
+  if (a.gin) {
+    hipLaunchKernelGGL(k_nv_finalize1, dim3(1), dim3(64), 0, st, a);
+    LAUNCH_CHECK();
+  }
+  return LM_OK;
+}

@@ -1,5 +1,5 @@
 // lm_stack.hip -- grouped multi-target (stack) entry points.
-#include "lm_impl.h"
+#include "lm_nvfp4_fast.h"
 
 // ---------------------------------------------------------------------------
 // stacks
@@ -145,8 +145,81 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
   return rc;
 }
 
-// NVFP4 stack: every item is processed by its own block-kernel launches after
-// one grouped prep (two-level items need their own amax pass).
+// Grouped NVFP4 merge: one amax launch over every two-level item, one quant
+// launch over all items, one finalize.  `dev_items` is workspace for the
+// descriptor table (fits in the BlkArgs region of lm_stack_workspace_extra).
+static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swizzled, bool sr, const PrepItem* preps,
+                         uint8_t* dev_items, hipStream_t st) {
+  static_assert(sizeof(NvStackItem) <= sizeof(BlkArgs), "NVFP4 stack descriptors must fit the workspace slot");
+  NvStackItem* h = (NvStackItem*)calloc(count, sizeof(NvStackItem));
+  if (!h) return fail(LM_EINVAL, "host allocation failed");
+  int64_t tiles = 0;
+  bool any_two = false;
+  int rc = LM_OK;
+  for (int i = 0; i < count && rc == LM_OK; ++i) {
+    const lm_stack_item& s = items[i];
+    if (!s.q || !s.scale || !s.q_out || !s.scale_out) rc = fail(LM_EINVAL, "stack item %d has a null pointer", i);
+    if (s.aux && !s.aux_out) rc = fail(LM_EINVAL, "stack item %d: two-level NVFP4 needs a per-tensor scale output", i);
+    NvArgs& a = h[i].a;
+    a.q = (const uint8_t*)s.q;
+    a.scale = (const uint8_t*)s.scale;
+    a.gin = (const float*)s.aux;
+    a.q_out = (uint8_t*)s.q_out;
+    a.scale_out = (uint8_t*)s.scale_out;
+    a.gout = (float*)s.aux_out;
+    a.at = preps[i].at;
+    a.bp = preps[i].bp;
+    a.red = preps[i].red;
+    a.M = s.M;
+    a.N = s.N;
+    a.strength = s.lora.strength;
+    a.swizzled = swizzled;
+    a.seed = s.seed;
+    h[i].tile_begin = tiles;
+    tiles += (s.M + 15) / 16;
+    any_two = any_two || s.aux != nullptr;
+    if (rc == LM_OK && swizzled) rc = zero_swizzle_pad((uint8_t*)s.scale_out, s.M, s.N / 16, st);
+  }
+  if (rc == LM_OK) {
+    hipError_t e = hipMemcpyAsync(dev_items, h, sizeof(NvStackItem) * count, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) rc = fail(LM_EHIP, "hipMemcpyAsync: %s", hipGetErrorString(e));
+  }
+  const int nkc = preps[0].rpad / 16;
+  const dim3 grid((unsigned)tiles), block(NV_NW * 64);
+  const NvStackItem* d = (const NvStackItem*)dev_items;
+  if (rc == LM_OK && any_two) {
+    TimedLaunch timed("nvfp4", st);
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_amax_stack<NKC_>), grid, block, 0, st, d, count));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 amax launch: %s", hipGetErrorString(e));
+  }
+  if (rc == LM_OK) {
+    TimedLaunch timed("nvfp4", st);
+    if (sr) {
+      NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, true>), grid, block, 0, st, d, count));
+    } else {
+      NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, false>), grid, block, 0, st, d, count));
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 quant launch: %s", hipGetErrorString(e));
+  }
+  if (rc == LM_OK && any_two) {
+    hipLaunchKernelGGL(k_nv_finalize, dim3((count + 63) / 64), dim3(64), 0, st, d, count);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 finalize launch: %s", hipGetErrorString(e));
+  }
+  // the host table must outlive the async copy: the caller synchronizes before freeing
+  if (rc == LM_OK) {
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) rc = fail(LM_EHIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+  }
+  free(h);
+  return rc;
+}
+
+// NVFP4 stack: the grouped fast kernels when every item qualifies; otherwise
+// every item is processed by its own block-kernel launches after one grouped
+// prep (two-level items need their own amax pass).
 extern "C" int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, int32_t swizzled, int32_t rounding_mode,
                                     void* workspace, size_t workspace_bytes, void* stream) {
   if (count <= 0) return LM_OK;
@@ -161,6 +234,21 @@ extern "C" int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, i
   if (!preps) return fail(LM_EINVAL, "host allocation failed");
   int rc = stack_layout(items, count, workspace, workspace_bytes, preps, cursor);
   if (rc == LM_OK) rc = stack_prep(preps, count, base, st);
+  bool fast = rc == LM_OK;
+  for (int i = 0; fast && i < count; ++i)
+    fast = nv_fast_ok(items[i].lora.dtype, preps[i].rpad / 16, items[i].N) &&
+           nkc_bucket(preps[i].rpad / 16) == nkc_bucket(preps[0].rpad / 16) && check_nvfp4(items[i].M, items[i].N) == 0;
+  if (fast) {
+    rc = nv_stack_fast(items, count, swizzled, rounding_mode == LM_ROUND_STOCHASTIC, preps,
+                       base + align256((size_t)count * sizeof(PrepItem)) + align256((size_t)count * sizeof(RowStackItem)),
+                       st);
+    if (rc == LM_OK) {
+      hipError_t e = hipStreamSynchronize(st);
+      if (e != hipSuccess) rc = fail(LM_EHIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+    }
+    free(preps);
+    return rc;
+  }
   lm_rounding rnd;
   rnd.mode = rounding_mode;
   rnd.reserved = 0;

@@ -44,7 +44,7 @@ def test_nvfp4_requant_bit_exact(shape, two_level, swizzled, sr):
         assert np.array_equal(pts.cpu().numpy().reshape(-1), opts)
 
 
-@pytest.mark.parametrize("shape,rank", [((128, 4096), 16), ((48, 256), 32), ((16, 64), 5)])
+@pytest.mark.parametrize("shape,rank", [((128, 4096), 16), ((48, 256), 32), ((16, 64), 5), ((40, 384), 64)])
 @pytest.mark.parametrize("two_level", [True, False])
 @pytest.mark.parametrize("swizzled", [False, True])
 @pytest.mark.parametrize("sr", [False, True])
