@@ -131,6 +131,7 @@ class Int8Stack(Workload):
     def __init__(self, layers: int, stochastic: bool) -> None:
         from piper_offload_amd.stack import StackTarget
 
+        self.plan = None  # descriptor table + workspace, built on the first step
         self.stochastic = stochastic
         self.paths, self.targets = [], []
         rank = 16
@@ -157,11 +158,12 @@ class Int8Stack(Workload):
 
     def step(self, index: int) -> None:
         from piper_offload_amd import derive_seed
-        from piper_offload_amd.stack import merge_int8_stack
 
-        for t, p in zip(self.targets, self.paths):
-            t.seed = derive_seed(p, index)
-        merge_int8_stack(self.targets, stochastic=self.stochastic)
+        if self.plan is None:
+            from piper_offload_amd.stack import StackPlan
+
+            self.plan = StackPlan(self.targets, "int8")
+        self.plan.merge([derive_seed(p, index) for p in self.paths], stochastic=self.stochastic)
 
 
 class Nvfp4Stack(Workload):
@@ -170,6 +172,7 @@ class Nvfp4Stack(Workload):
     def __init__(self, layers: int, stochastic: bool) -> None:
         from piper_offload_amd.stack import StackTarget
 
+        self.plan = None  # descriptor table + workspace, built on the first step
         self.stochastic = stochastic
         self.paths, self.targets = [], []
         rank = 16
@@ -193,11 +196,12 @@ class Nvfp4Stack(Workload):
 
     def step(self, index: int) -> None:
         from piper_offload_amd import derive_seed
-        from piper_offload_amd.stack import merge_nvfp4_stack
 
-        for t, p in zip(self.targets, self.paths):
-            t.seed = derive_seed(p, index)
-        merge_nvfp4_stack(self.targets, stochastic=self.stochastic)
+        if self.plan is None:
+            from piper_offload_amd.stack import StackPlan
+
+            self.plan = StackPlan(self.targets, "nvfp4")
+        self.plan.merge([derive_seed(p, index) for p in self.paths], stochastic=self.stochastic)
 
 
 class Copy(Workload):

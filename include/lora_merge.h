@@ -28,9 +28,12 @@
  *    N = logical in columns, rank = r.
  *  - `stream` is a hipStream_t passed as void*.  No entry point allocates
  *    device memory (scratch comes from the caller's `workspace`, sized by
- *    lm_workspace_size()); single-tensor entry points are asynchronous on
- *    `stream`, the *_stack entry points synchronize it once before returning
- *    (their descriptor tables are staged from host memory).
+ *    lm_workspace_size()) and none synchronizes: every call is asynchronous
+ *    on `stream`.  The *_stack entry points copy their descriptor tables
+ *    into the workspace through pinned host staging owned by the library,
+ *    so the caller's item array may be reused as soon as the call returns;
+ *    the workspace must stay allocated until the stream has run the call
+ *    (stream-ordered allocators such as torch's satisfy this).
  *  - Return value: LM_OK or an lm_status; lm_last_error() returns a
  *    thread-local message for the last failure on the calling thread.
  *  - The deterministic path rounds to nearest even.  Stochastic rounding

@@ -96,3 +96,58 @@ int launch_prep(const PrepItem& it, hipStream_t st) {
   return LM_OK;
 }
 
+
+// ---- host -> device staging of descriptor tables ---------------------------
+// The stack entries upload per-call descriptor tables.  They go through a
+// small pool of pinned host buffers, each guarded by an event recorded after
+// its copy, so the entry points return without synchronizing the stream: a
+// buffer is reused once its previous copy has completed (waiting on the
+// oldest one when all are in flight).
+namespace {
+struct StageSlot {
+  void* host = nullptr;
+  size_t cap = 0;
+  hipEvent_t ev = nullptr;
+  int device = -1;
+  uint64_t stamp = 0;
+};
+std::mutex g_stage_mu;
+std::vector<StageSlot> g_stage;
+uint64_t g_stage_clock = 0;
+constexpr size_t kStageSlots = 8;
+}  // namespace
+
+int lm_stage_h2d(void* dst, const void* src, size_t bytes, hipStream_t st) {
+  if (bytes == 0) return LM_OK;
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_stage_mu);
+  StageSlot* pick = nullptr;
+  for (auto& s : g_stage)  // a free slot of this device that is large enough
+    if (s.device == dev && s.cap >= bytes && hipEventQuery(s.ev) == hipSuccess) { pick = &s; break; }
+  if (!pick && g_stage.size() < kStageSlots) {
+    g_stage.emplace_back();
+    pick = &g_stage.back();
+    pick->device = dev;
+    HIP_TRY(hipEventCreateWithFlags(&pick->ev, hipEventDisableTiming));
+  }
+  if (!pick) {  // every slot busy or too small: wait for the oldest of this device
+    for (auto& s : g_stage)
+      if (s.device == dev && (!pick || s.stamp < pick->stamp)) pick = &s;
+    if (!pick) return fail(LM_EHIP, "no staging slot for device %d", dev);
+    HIP_TRY(hipEventSynchronize(pick->ev));
+  }
+  if (pick->cap < bytes) {
+    if (pick->host) HIP_TRY(hipHostFree(pick->host));
+    pick->host = nullptr;
+    pick->cap = 0;
+    const size_t cap = bytes < 65536 ? 65536 : bytes * 2;
+    HIP_TRY(hipHostMalloc(&pick->host, cap, hipHostMallocDefault));
+    pick->cap = cap;
+  }
+  memcpy(pick->host, src, bytes);
+  HIP_TRY(hipMemcpyAsync(dst, pick->host, bytes, hipMemcpyHostToDevice, st));
+  HIP_TRY(hipEventRecord(pick->ev, st));
+  pick->stamp = ++g_stage_clock;
+  return LM_OK;
+}

@@ -280,6 +280,19 @@ DEV uint32_t pack_byte2s(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
 // y16 = 65536 * y must be exactly representable (|y| < 2^7 for fp32 inputs
 // of 24-bit precision keeps every step exact).  Equivalent to
 // lower + (u < frac) for all finite y; an integer y stays y.
+// floor(-x) as int32 in one v_cvt_flr_i32_f32 (= -ceil(x)); |x| < 2^31
+DEV int cvt_flr_neg(float x) {
+  int r;
+  asm("v_cvt_flr_i32_f32_e64 %0, -%1" : "=v"(r) : "v"(x));
+  return r;
+}
+// (w & 0xffff) - t in one SDWA subtract (word 0 of w)
+DEV uint32_t sub_lo16(uint32_t w, uint32_t t) {
+  uint32_t r;
+  asm("v_sub_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD"
+      : "=v"(r) : "v"(w), "v"(t));
+  return r;
+}
 DEV int sr_grid(float y16, uint32_t h) {
   int fneg = (int)__builtin_floorf(-y16);  // floor(-y16) = -ceil(y16)
   return ((int)(65535u - h) - fneg) >> 16;

@@ -146,6 +146,8 @@ static __global__ __launch_bounds__(256) void k_prep_many(const PrepItem* __rest
 }
 
 int launch_prep(const PrepItem& it, hipStream_t st);
+// asynchronous host -> device copy through pinned staging (lm_common.hip)
+int lm_stage_h2d(void* dst, const void* src, size_t bytes, hipStream_t st);
 
 // kernel timer (lm_timer_enable / lm_timer_read): bracket a launch on `st`
 bool lm_timer_on();
@@ -528,7 +530,7 @@ __device__ __forceinline__ void fast_load_tile(const RowArgs& a, int64_t rowc, i
 
 template <int KIND, int NKC>
 __device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const FastTileIn<NKC>& in,
-                                                 const v4i16 (&bop)[NKC], float s_in, float base_off,
+                                                 const v4i16 (&bop)[NKC], float s_in,
                                                  uint32_t (&out)[8]) {
   float d[16];
 #pragma unroll
@@ -546,10 +548,9 @@ __device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const FastTil
     const int b0 = (2 * k) & 3, b1 = (2 * k + 1) & 3;
     float x0, x1;
     if constexpr (KIND == K_INT8) {
-      // (u ^ 0x80) - 128 = signed byte: fma(u', s, -128 s) = RN(q * s) exactly
-      const uint32_t ws = word ^ 0x80808080u;
-      x0 = __builtin_fmaf((float)((ws >> (8 * b0)) & 0xffu), s_in, base_off);
-      x1 = __builtin_fmaf((float)((ws >> (8 * b1)) & 0xffu), s_in, base_off);
+      // signed byte -> fp32 is one sign-extending SDWA convert; RN(q * s)
+      x0 = (float)(int8_t)(word >> (8 * b0)) * s_in;
+      x1 = (float)(int8_t)(word >> (8 * b1)) * s_in;
     } else {
       x0 = fp8_decode<FmtLimit<KIND>::fmt>(word, b0) * s_in;
       x1 = fp8_decode<FmtLimit<KIND>::fmt>(word, b1) * s_in;
@@ -585,10 +586,9 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, int64_t row, 
         const float q0 = m * qp.inv;  // qp.inv = 65536 * RN(1/s)
         const float e = __builtin_fmaf(-q0, qp.rcp, m);  // qp.rcp = s / 65536
         const float y16 = __builtin_amdgcn_fmed3f(__builtin_fmaf(e, qp.inv, q0), lo16, hi16);
-        const int tneg = (int)__builtin_floorf(-y16);  // -ceil(Y)
-        const uint32_t nw = ~rw[j >> 1];                 // 65535 - h in each half
-        const uint32_t nh = (j & 1) ? (nw >> 16) : (nw & 0xffffu);
-        y[j] = nh - (uint32_t)tneg;
+        const uint32_t tneg = (uint32_t)cvt_flr_neg(y16);  // -ceil(Y)
+        const uint32_t nw = ~rw[j >> 1];                    // 65535 - h in each half
+        y[j] = (j & 1) ? (nw >> 16) - tneg : sub_lo16(nw, tneg);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) out[i] = pack_byte2s(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
@@ -650,11 +650,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   const int ntiles = (int)(a.N >> 6);
   v4i16 bop[NKC];
   load_bop<NKC>(a.bp, row, lane, bop);
-  float s_in = 0.0f, base_off = 0.0f;
-  if (rok) {
-    s_in = ((const float*)a.scale)[row];
-    base_off = -128.0f * s_in;
-  }
+  const float s_in = rok ? ((const float*)a.scale)[row] : 0.0f;
   uint32_t cache[CACHE][8];
   uint32_t pmax = 0u;
   if (wave + (CACHE - 1) * NW < ntiles) {
@@ -665,7 +661,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
 #pragma unroll
     for (int i = 0; i < CACHE; ++i) {
       if (i + PF < CACHE) fast_load_tile<NKC>(a, rowc, wave + (i + PF) * NW, lane, in[i + PF]);
-      fast_merged_tile<KIND, NKC>(a, in[i], bop, s_in, base_off, cache[i]);
+      fast_merged_tile<KIND, NKC>(a, in[i], bop, s_in, cache[i]);
 #pragma unroll
       for (int k = 0; k < 8; ++k) pmax = pk_max_u16(pmax, cache[i][k] & 0x7fff7fffu);
     }
@@ -676,7 +672,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
       if (mt < ntiles) {
         FastTileIn<NKC> in;
         fast_load_tile<NKC>(a, rowc, mt, lane, in);
-        fast_merged_tile<KIND, NKC>(a, in, bop, s_in, base_off, cache[i]);
+        fast_merged_tile<KIND, NKC>(a, in, bop, s_in, cache[i]);
 #pragma unroll
         for (int k = 0; k < 8; ++k) pmax = pk_max_u16(pmax, cache[i][k] & 0x7fff7fffu);
       }
@@ -691,7 +687,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
       FastTileIn<NKC> nxt;
       fast_load_tile<NKC>(a, rowc, mt + NW < ntiles ? mt + NW : mt, lane, nxt);
       uint32_t t[8];
-      fast_merged_tile<KIND, NKC>(a, cur, bop, s_in, base_off, t);
+      fast_merged_tile<KIND, NKC>(a, cur, bop, s_in, t);
 #pragma unroll
       for (int k = 0; k < 8; ++k) pmax = pk_max_u16(pmax, t[k] & 0x7fff7fffu);
       cur = nxt;
@@ -745,7 +741,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
       FastTileIn<NKC> nxt;
       fast_load_tile<NKC>(a, rowc, mt + NW < ntiles ? mt + NW : mt, lane, nxt);
       uint32_t t[8];
-      fast_merged_tile<KIND, NKC>(a, cur, bop, s_in, base_off, t);
+      fast_merged_tile<KIND, NKC>(a, cur, bop, s_in, t);
       fast_quant_store<KIND, SR>(a, row, rok, mt, lane, qp, t);
       cur = nxt;
     }

@@ -2,13 +2,17 @@
 // factors, N % 128 == 0, one or two scale levels, plain or 128x4-swizzled
 // block scales.  P/ = the reference's src/piper_offload/.
 //
-// Work decomposition: a 512-thread workgroup (8 waves) owns 16 rows; each
-// wave walks the 128-column macro tiles mt = wave, wave + 8, ...  A lane holds
-// row (lane & 15) and the 32 consecutive columns 32*(lane >> 4) .. +31 of a
-// macro tile: two NVFP4 blocks, i.e. one 16-byte code load and one 2-byte
-// scale load, so block reductions never leave the lane.  The delta of a
-// macro tile is 8 x NKC v_mfma_f32_16x16x16_bf16 (tile_delta's SPAN = 32
-// orientation).
+// Work decomposition: a 512-thread workgroup owns 16 rows; wave w walks the
+// 128-column macro tiles mt = w, w + 8, ..., so at any time the workgroup
+// streams 8 consecutive tiles (512 contiguous bytes) of each of its rows.
+// (Measured on MI355X with copy kernels of the same footprint: ~5.3 TB/s for
+// NVFP4 row lengths, against ~3.7 TB/s for 128-row workgroups whose waves
+// share one tile.)  A lane holds row (lane & 15) and the 32 consecutive
+// columns 32*(lane >> 4) .. +31 of a macro tile: two NVFP4 blocks, i.e. one
+// 16-byte code load and one 2-byte scale load, so block reductions never
+// leave the lane.  The delta of a macro tile is 8 x NKC
+// v_mfma_f32_16x16x16_bf16 (tile_delta's SPAN = 32 orientation), with the
+// A^T fragments read through per-lane pointers.
 //
 // Two-level tensors take two passes (P/_triton_nvfp4_lora.py:437-512, 327-366):
 //   k_nv_amax  -- max |merged| over the tensor into red[0] (float bits, so
@@ -62,25 +66,46 @@ struct NvTileIn {
   v4i16 aop[8][NKC];
 };
 
+// Per-lane base pointers; every per-tile address is base + mt * stride, and
+// the A^T fragments of a tile use immediate offsets.  Scales: mt advances the
+// scale column by 8, which is 8 bytes in the plain layout and 2 col-blocks =
+// 1024 bytes in the 128x4 swizzle (P/_triton_nvfp4_lora.py:88-104).
 template <int NKC>
-DEV void nv_load_tile(const NvArgs& a, int64_t rowc, int mt, int lane, NvTileIn<NKC>& t) {
+struct NvLane {
+  const uint8_t* q;
+  const uint8_t* sc;
+  const uint16_t* at;
+  int64_t sc_stride;
+};
+
+template <int NKC>
+DEV NvLane<NKC> nv_lane(const NvArgs& a, int64_t rowc, int lane) {
   constexpr int RPAD = NKC * 16;
   const int p = lane & 15, g = lane >> 4;
-  const int64_t c0 = (int64_t)mt * 128 + 32 * g;
-  t.codes = *(const uint4*)(a.q + rowc * (a.N >> 1) + (c0 >> 1));
-  // c0/16 is even: both blocks' scales are adjacent bytes in either layout
-  t.sc = *(const uint16_t*)(a.scale + blocked_offset(rowc, c0 >> 4, a.N >> 4, a.swizzled));
-  const int64_t colbase = (int64_t)mt * 128 + 32 * (p >> 2) + (p & 3);
+  NvLane<NKC> l;
+  l.q = a.q + rowc * (a.N >> 1) + 16 * g;
+  l.sc = a.scale + blocked_offset(rowc, 2 * g, a.N >> 4, a.swizzled);
+  l.sc_stride = a.swizzled ? 1024 : 8;
+  l.at = a.at + (int64_t)(32 * (p >> 2) + (p & 3)) * RPAD + g * (NKC * 4);
+  return l;
+}
+
+template <int NKC>
+DEV void nv_load_tile(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
+  constexpr int RPAD = NKC * 16;
+  t.codes = *(const uint4*)(l.q + (int64_t)mt * 64);
+  // the lane's scale column is even: both blocks' scales are adjacent bytes
+  t.sc = *(const uint16_t*)(l.sc + (int64_t)mt * l.sc_stride);
+  const uint16_t* at = l.at + (int64_t)mt * (128 * RPAD);
 #pragma unroll
-  for (int k = 0; k < 8; ++k) load_kchunks<NKC>(a.at + (colbase + 4 * k) * RPAD + g * (NKC * 4), t.aop[k]);
+  for (int k = 0; k < 8; ++k) load_kchunks<NKC>(at + 4 * k * RPAD, t.aop[k]);
 }
 
 // merged values of the lane's 32 columns; ZFIX applies the reference's
 // "update == 0 keeps the base" rule (P/_triton_nvfp4_lora.py:183-186), which
 // only changes the sign of a zero and so is not needed for max |merged|.
-template <int NKC, bool ZFIX>
-DEV void nv_merged(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], bool two, float gin,
-                   float (&m)[32]) {
+template <int NKC, bool TWO, bool ZFIX>
+DEV void nv_merged(const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float strength, float gin, float (&m)[32]) {
   float d[32];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
@@ -93,29 +118,51 @@ DEV void nv_merged(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&bop)[
   float bs[2];
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    float v = fp8_decode<E4M3>(in.sc, b);  // e4m3 is exact in bf16
-    bs[b] = two ? bf16r(v * gin) : v;
+    const float v = fp8_decode<E4M3>(in.sc, b);  // e4m3 is exact in bf16
+    bs[b] = TWO ? bf16r(v * gin) : v;
   }
   const uint32_t w[4] = {in.codes.x, in.codes.y, in.codes.z, in.codes.w};
+  bool zfix = false;
+  if constexpr (ZFIX) {
+    // The rule can only matter where d * strength == 0; every such product is
+    // bounded below by min|d| * |strength|, so lanes with a non-zero bound
+    // skip it (a zero LoRA row, an exact cancellation or an underflow takes
+    // the exact per-element path).
+    float dmin = __builtin_fabsf(d[0]);
 #pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const v2f32 pr = e2m1_pair(w[q >> 2], q & 3);
+    for (int j = 1; j < 32; ++j) dmin = __builtin_fminf(dmin, __builtin_fabsf(d[j]));
+    zfix = dmin * __builtin_fabsf(strength) == 0.0f;
+  }
+  if (zfix) {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int j = 2 * q + e;
-      const float base = bf16r(pr[e] * bs[j >> 4]);
-      const float mm = __builtin_fmaf(d[j], a.strength, base);
-      if constexpr (ZFIX) m[j] = (d[j] * a.strength == 0.0f) ? base : mm;
-      else m[j] = mm;
+    for (int q = 0; q < 16; ++q) {
+      const v2f32 pr = e2m1_pair(w[q >> 2], q & 3);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int j = 2 * q + e;
+        const float base = bf16r(pr[e] * bs[j >> 4]);
+        m[j] = (d[j] * strength == 0.0f) ? base : __builtin_fmaf(d[j], strength, base);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const v2f32 pr = e2m1_pair(w[q >> 2], q & 3);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int j = 2 * q + e;
+        m[j] = __builtin_fmaf(d[j], strength, bf16r(pr[e] * bs[j >> 4]));
+      }
     }
   }
 }
 
-// Stochastic e2m1 code of a clamped value v (|v| <= 6) with h = 16 random
-// bits: the grid step below 2 is 0.5, then 1, then 2, so with e the step's
-// exponent, Y = |v| * 2^(16-e) is exact and q = (ceil(Y) + 65535 - h) >> 16
-// is floor(|v|/2^e) + [h * 2^-16 < frac]; exact and saturated values keep
-// their code (P/_triton_stochastic_quantization.py:110-130).
+// Stochastic e2m1 code of a clamped value v (|v| <= 6) with nh = 65535 - h,
+// h the 16 random bits: the grid step below 2 is 0.5, then 1, then 2, so
+// with e the step's exponent, Y = |v| * 2^(16-e) is exact and
+// q = (ceil(Y) + 65535 - h) >> 16 is floor(|v|/2^e) + [h * 2^-16 < frac];
+// exact and saturated values keep their code
+// (P/_triton_stochastic_quantization.py:110-130).
 DEV float nv_sr_value(float v, uint32_t nh) {
   const float mag = __builtin_fabsf(v);
   int ex = __builtin_amdgcn_frexp_expf(mag);  // floor(log2 mag) + 1 (0 for 0)
@@ -126,14 +173,25 @@ DEV float nv_sr_value(float v, uint32_t nh) {
   return __builtin_copysignf(__builtin_ldexpf((float)q, ex - 2), v);
 }
 
-template <int NKC>
-DEV void nv_quant_store(const NvArgs& a, int64_t row, int mt, int lane, bool two, float gq, float inv_g, bool sr,
-                        const float (&m)[32]) {
-  const int64_t N = a.N;
-  const int64_t c0 = (int64_t)mt * 128 + 32 * (lane >> 4);
+// RN(a / b) from y = RN(1 / b): q0 = RN(a y), r = a - b q0 (exact by fma),
+// RN(q0 + r y).  Correctly rounded when a, b and the quotient are normal
+// with room for the residual (Markstein); checked against IEEE division on
+// 4e8 random binary32 pairs within 2^+-60 of 1, the range of NVFP4 scales.
+DEV float div_markstein(float a, float b, float y) {
+  const float q0 = a * y;
+  return __builtin_fmaf(__builtin_fmaf(-q0, b, a), y, q0);
+}
+
+// RN(1 / (1 + k/8)), k = 0..7: the reciprocal mantissas of e4m3 values
+static __device__ __constant__ const float kRcpE4M3[8] = {1.0f / 1.0f, 1.0f / 1.125f, 1.0f / 1.25f, 1.0f / 1.375f,
+                                                   1.0f / 1.5f, 1.0f / 1.625f, 1.0f / 1.75f, 1.0f / 1.875f};
+
+template <int NKC, bool TWO, bool SR>
+DEV void nv_quant_store(const NvArgs& a, int64_t row, int mt, int lane, float gq, float inv_g, const float* rtab,
+                        const float (&m)[32], uint8_t* qo, uint8_t* so, int64_t so_stride) {
   uint32_t rw[16];
-  if (sr) sr_words_aligned<32>(a.seed, (uint64_t)(row * N + c0), rw);
-  uint32_t words[4];
+  if constexpr (SR) sr_words_aligned<32>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4)), rw);
+  uint32_t words[4] = {0u, 0u, 0u, 0u};
   uint32_t scb = 0;
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
@@ -144,59 +202,66 @@ DEV void nv_quant_store(const NvArgs& a, int64_t row, int mt, int lane, bool two
       mb[j] = bf16r(m[16 * b + j]);
       bmax = __builtin_fmaxf(bmax, __builtin_fabsf(mb[j]));
     }
-    float fs = bmax / 6.0f;
-    if (two) fs = fs / gq;
+    // bmax is a bf16 value and 6 is exact in bf16: div_rn is the IEEE quotient
+    float fs = div_rn(bmax, 6.0f, 1.0f / 6.0f);
+    if constexpr (TWO) fs = div_markstein(fs, gq, inv_g);
     fs = __builtin_fminf(__builtin_fmaxf(fs, 0.015625f), 448.0f);
     const uint32_t s8 = fp8_encode1<E4M3>(fs);
     fs = fp8_value<E4M3>(s8);
     scb |= s8 << (8 * b);
-    const float recip = inv_g / fs, rfs = 1.0f / fs;
+    const uint32_t fb = f2u(fs);
+    const float rfs = __builtin_ldexpf(rtab[(fb >> 20) & 7u], 127 - (int)((fb >> 23) & 255u));  // RN(1/fs)
+    const float recip = TWO ? div_markstein(inv_g, fs, rfs) : 0.0f;
     float x[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      float v = two ? mb[j] * recip : div_rn(mb[j], fs, rfs);
-      if (sr) {
+      float v = TWO ? mb[j] * recip : div_rn(mb[j], fs, rfs);
+      if constexpr (SR) {
         const uint32_t nw = ~rw[(16 * b + j) >> 1];
         const uint32_t nh = (j & 1) ? (nw >> 16) : (nw & 0xffffu);
         v = nv_sr_value(__builtin_amdgcn_fmed3f(v, -6.0f, 6.0f), nh);
       }
       x[j] = v;  // the e2m1 conversion saturates to +-6 (checked on gfx950)
     }
+    // dst_sel k writes byte k and keeps the others (checked on gfx950)
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      uint32_t wd = 0;
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        wd |= (__builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, x[8 * k + 2 * t], x[8 * k + 2 * t + 1], 1.0f, 0) & 0xffu)
-              << (8 * t);
+      uint32_t wd = 0u;
+      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 0], x[8 * k + 1], 1.0f, 0);
+      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 2], x[8 * k + 3], 1.0f, 1);
+      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 4], x[8 * k + 5], 1.0f, 2);
+      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 6], x[8 * k + 7], 1.0f, 3);
       words[2 * b + k] = wd;
     }
   }
-  *(uint4*)(a.q_out + row * (N >> 1) + (c0 >> 1)) = make_uint4(words[0], words[1], words[2], words[3]);
-  *(uint16_t*)(a.scale_out + blocked_offset(row, c0 >> 4, N >> 4, a.swizzled)) = (uint16_t)scb;
+  *(uint4*)(qo + (int64_t)mt * 64) = make_uint4(words[0], words[1], words[2], words[3]);
+  *(uint16_t*)(so + (int64_t)mt * so_stride) = (uint16_t)scb;
 }
 
 // ---- pass bodies -------------------------------------------------------------
+// Rows past M load row M-1 (valid memory) and store nothing.
 template <int NKC>
 DEV void nv_amax_body(const NvArgs& a, int64_t row0) {
   __shared__ float sh[NV_NW];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int64_t row = row0 + rl;
   const bool rok = row < a.M;
-  const int64_t rowc = rok ? row : a.M - 1;  // in-bounds loads; results dropped
+  const int64_t rowc = rok ? row : a.M - 1;
   const int ntiles = (int)(a.N >> 7);
   const float gin = *a.gin;
+  const float strength = a.strength;
+  const NvLane<NKC> l = nv_lane<NKC>(a, rowc, lane);
   v4i16 bop[NKC];
-  load_bop<NKC>(a.bp, row, lane, bop);
+  load_bop<NKC>(a.bp, row, lane, bop);  // Bp holds ceil(M/16)*16 rows
   float mx = 0.0f;
   if (wave < ntiles) {
     NvTileIn<NKC> cur;
-    nv_load_tile<NKC>(a, rowc, wave, lane, cur);
+    nv_load_tile<NKC>(l, wave, cur);
     for (int mt = wave; mt < ntiles; mt += NV_NW) {
       NvTileIn<NKC> nxt;
-      nv_load_tile<NKC>(a, rowc, mt + NV_NW < ntiles ? mt + NV_NW : mt, lane, nxt);
+      nv_load_tile<NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
       float m[32];
-      nv_merged<NKC, false>(a, cur, bop, true, gin, m);
+      nv_merged<NKC, true, false>(cur, bop, strength, gin, m);
 #pragma unroll
       for (int j = 0; j < 32; ++j) mx = __builtin_fmaxf(mx, __builtin_fabsf(m[j]));
       cur = nxt;
@@ -215,31 +280,34 @@ DEV void nv_amax_body(const NvArgs& a, int64_t row0) {
   }
 }
 
-template <int NKC, bool SR>
-DEV void nv_quant_body(const NvArgs& a, int64_t row0) {
+template <int NKC, bool TWO, bool SR>
+DEV void nv_quant_body(const NvArgs& a, int64_t row0, const float* rtab) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int64_t row = row0 + rl;
   const bool rok = row < a.M;
   const int64_t rowc = rok ? row : a.M - 1;
   const int ntiles = (int)(a.N >> 7);
-  const bool two = a.gin != nullptr;
-  const float gin = two ? *a.gin : 1.0f;
+  const float gin = TWO ? *a.gin : 1.0f;
+  const float strength = a.strength;
   float gq = 1.0f, inv_g = 1.0f;
-  if (two) {
+  if constexpr (TWO) {
     gq = __builtin_fmaxf(u2f(*a.red) / 2688.0f, kEps);
     inv_g = 1.0f / gq;
   }
+  const NvLane<NKC> l = nv_lane<NKC>(a, rowc, lane);
+  uint8_t* qo = a.q_out + rowc * (a.N >> 1) + 16 * (lane >> 4);
+  uint8_t* so = a.scale_out + blocked_offset(rowc, 2 * (lane >> 4), a.N >> 4, a.swizzled);
   v4i16 bop[NKC];
   load_bop<NKC>(a.bp, row, lane, bop);
   if (wave >= ntiles) return;
   NvTileIn<NKC> cur;
-  nv_load_tile<NKC>(a, rowc, wave, lane, cur);
+  nv_load_tile<NKC>(l, wave, cur);
   for (int mt = wave; mt < ntiles; mt += NV_NW) {
     NvTileIn<NKC> nxt;
-    nv_load_tile<NKC>(a, rowc, mt + NV_NW < ntiles ? mt + NV_NW : mt, lane, nxt);
+    nv_load_tile<NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
     float m[32];
-    nv_merged<NKC, true>(a, cur, bop, two, gin, m);
-    if (rok) nv_quant_store<NKC>(a, row, mt, lane, two, gq, inv_g, SR, m);
+    nv_merged<NKC, TWO, true>(cur, bop, strength, gin, m);
+    if (rok) nv_quant_store<NKC, TWO, SR>(a, row, mt, lane, gq, inv_g, rtab, m, qo, so, l.sc_stride);
     cur = nxt;
   }
 }
@@ -255,13 +323,24 @@ DEV int nv_find(const NvStackItem* __restrict__ items, int count, int64_t t) {
 }
 
 // ---- kernels: single tensor (args by value) and grouped (descriptor table) ---
+// One workgroup per 16 rows (tile_begin counts 16-row groups).
+static inline int64_t nv_units(int64_t M, int64_t /*N*/) { return (M + 15) / 16; }
+
 template <int NKC>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_amax(NvArgs a) {
   nv_amax_body<NKC>(a, (int64_t)blockIdx.x * 16);
 }
 template <int NKC, bool SR>
+DEV void nv_quant_dispatch(const NvArgs& a, int64_t row0) {
+  __shared__ float rtab[8];
+  if (threadIdx.x < 8) rtab[threadIdx.x] = kRcpE4M3[threadIdx.x];
+  __syncthreads();
+  if (a.gin != nullptr) nv_quant_body<NKC, true, SR>(a, row0, rtab);
+  else nv_quant_body<NKC, false, SR>(a, row0, rtab);
+}
+template <int NKC, bool SR>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant(NvArgs a) {
-  nv_quant_body<NKC, SR>(a, (int64_t)blockIdx.x * 16);
+  nv_quant_dispatch<NKC, SR>(a, (int64_t)blockIdx.x * 16);
 }
 template <int NKC>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_amax_stack(const NvStackItem* __restrict__ items, int count) {
@@ -274,7 +353,7 @@ template <int NKC, bool SR>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant_stack(const NvStackItem* __restrict__ items, int count) {
   const int i = nv_find(items, count, blockIdx.x);
   const NvArgs a = items[i].a;
-  nv_quant_body<NKC, SR>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16);
+  nv_quant_dispatch<NKC, SR>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16);
 }
 // one thread per item: g = max(amax / 2688, eps)
 static __global__ void k_nv_finalize(const NvStackItem* __restrict__ items, int count) {
@@ -292,7 +371,7 @@ static inline bool nv_fast_ok(int cd, int nkc, int64_t N) { return cd == LM_BF16
 
 // single tensor: amax (two-level), quant, finalize on `st`
 static int nv_fast_run(const NvArgs& a, int nkc, bool sr, hipStream_t st) {
-  const dim3 grid((unsigned)((a.M + 15) / 16)), block(NV_NW * 64);
+  const dim3 grid((unsigned)nv_units(a.M, a.N)), block(NV_NW * 64);
   if (a.gin) {
     TimedLaunch timed("nvfp4", st);
     NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_amax<NKC_>), grid, block, 0, st, a));

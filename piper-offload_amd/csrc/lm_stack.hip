@@ -41,7 +41,8 @@ static int stack_prep(PrepItem* preps, int32_t count, uint8_t* dev_items, hipStr
     preps[i].work_begin = total;
     total += prep_units(preps[i]);
   }
-  HIP_TRY(hipMemcpyAsync(dev_items, preps, sizeof(PrepItem) * count, hipMemcpyHostToDevice, st));
+  int rc = lm_stage_h2d(dev_items, preps, sizeof(PrepItem) * count, st);
+  if (rc != LM_OK) return rc;
   int64_t nb = (total + 255) / 256;
   if (nb > 8192) nb = 8192;
   TimedLaunch timed("prep", st);
@@ -63,7 +64,7 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
   uint8_t* dev_prep = base;
   uint8_t* dev_rows = base + align256((size_t)count * sizeof(PrepItem));
   size_t cursor = extra;
-  // host staging (pageable; hipMemcpyAsync copies it before returning)
+  // host tables; lm_stage_h2d copies them into pinned staging before returning
   PrepItem* preps = (PrepItem*)calloc(count, sizeof(PrepItem));
   RowStackItem* rows = (RowStackItem*)calloc(count, sizeof(RowStackItem));
   if (!preps || !rows) {
@@ -106,10 +107,7 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
       if (nkc_bucket(rpad_of(items[i].lora.rank) / 16) != nkc_bucket(nkc_max))
         rc = fail(LM_EUNSUPPORTED, "stack items must share one rank bucket (16/32/64)");
   }
-  if (rc == LM_OK) {
-    hipError_t e = hipMemcpyAsync(dev_rows, rows, sizeof(RowStackItem) * count, hipMemcpyHostToDevice, st);
-    if (e != hipSuccess) rc = fail(LM_EHIP, "hipMemcpyAsync: %s", hipGetErrorString(e));
-  }
+  if (rc == LM_OK) rc = lm_stage_h2d(dev_rows, rows, sizeof(RowStackItem) * count, st);
   if (rc == LM_OK) {
     const bool sr = rounding_mode == LM_ROUND_STOCHASTIC;
     dim3 grid((unsigned)tiles), block(ROW_NW * 64);
@@ -134,11 +132,6 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "stack launch: %s", hipGetErrorString(e));
-  }
-  // the pageable host buffers must outlive the async copies: wait for them
-  if (rc == LM_OK) {
-    hipError_t e = hipStreamSynchronize(st);
-    if (e != hipSuccess) rc = fail(LM_EHIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
   }
   free(preps);
   free(rows);
@@ -176,14 +169,11 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
     a.swizzled = swizzled;
     a.seed = s.seed;
     h[i].tile_begin = tiles;
-    tiles += (s.M + 15) / 16;
+    tiles += nv_units(s.M, s.N);
     any_two = any_two || s.aux != nullptr;
     if (rc == LM_OK && swizzled) rc = zero_swizzle_pad((uint8_t*)s.scale_out, s.M, s.N / 16, st);
   }
-  if (rc == LM_OK) {
-    hipError_t e = hipMemcpyAsync(dev_items, h, sizeof(NvStackItem) * count, hipMemcpyHostToDevice, st);
-    if (e != hipSuccess) rc = fail(LM_EHIP, "hipMemcpyAsync: %s", hipGetErrorString(e));
-  }
+  if (rc == LM_OK) rc = lm_stage_h2d(dev_items, h, sizeof(NvStackItem) * count, st);
   const int nkc = preps[0].rpad / 16;
   const dim3 grid((unsigned)tiles), block(NV_NW * 64);
   const NvStackItem* d = (const NvStackItem*)dev_items;
@@ -207,11 +197,6 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
     hipLaunchKernelGGL(k_nv_finalize, dim3((count + 63) / 64), dim3(64), 0, st, d, count);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 finalize launch: %s", hipGetErrorString(e));
-  }
-  // the host table must outlive the async copy: the caller synchronizes before freeing
-  if (rc == LM_OK) {
-    hipError_t e = hipStreamSynchronize(st);
-    if (e != hipSuccess) rc = fail(LM_EHIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
   }
   free(h);
   return rc;
@@ -242,10 +227,6 @@ extern "C" int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, i
     rc = nv_stack_fast(items, count, swizzled, rounding_mode == LM_ROUND_STOCHASTIC, preps,
                        base + align256((size_t)count * sizeof(PrepItem)) + align256((size_t)count * sizeof(RowStackItem)),
                        st);
-    if (rc == LM_OK) {
-      hipError_t e = hipStreamSynchronize(st);
-      if (e != hipSuccess) rc = fail(LM_EHIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
-    }
     free(preps);
     return rc;
   }
@@ -280,10 +261,6 @@ extern "C" int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, i
     } else {
       rc = run_blocks<B_NVFP4, P_FULL>(a, s.lora.dtype, c.nkc, sr, false, st);
     }
-  }
-  if (rc == LM_OK) {
-    hipError_t e = hipStreamSynchronize(st);
-    if (e != hipSuccess) rc = fail(LM_EHIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
   }
   free(preps);
   return rc;

@@ -18,7 +18,7 @@ import torch
 
 from . import _lib as L
 
-__all__ = ["StackTarget", "merge_int8_stack", "merge_nvfp4_stack"]
+__all__ = ["StackPlan", "StackTarget", "merge_int8_stack", "merge_nvfp4_stack"]
 
 
 @dataclass(slots=True)
@@ -64,39 +64,75 @@ def _items(targets: Sequence[StackTarget], kind: str) -> tuple[ctypes.Array, int
     return arr, total, device
 
 
+class StackPlan:
+    """A reusable grouped merge over fixed targets.
+
+    Building the descriptor table (pointers, shapes, factors) and sizing the
+    workspace happen once; :meth:`merge` only rewrites the per-target seeds
+    and issues the grouped call, asynchronously on the current stream.  The
+    targets' storage and factors must stay alive and keep their addresses for
+    the plan's lifetime; their contents may change between merges (that is
+    the point: each merge updates the weights in place).
+    """
+
+    def __init__(self, targets: Sequence[StackTarget], kind: str) -> None:
+        if kind not in ("int8", "nvfp4"):
+            raise ValueError(f"unknown stack kind {kind!r}")
+        if not targets:
+            raise ValueError("a stack plan needs at least one target")
+        self.kind = kind
+        self.targets = list(targets)
+        if kind == "int8":
+            for t in self.targets:
+                w = t.weight
+                if w.qdata.dtype is not torch.int8 or tuple(w.block_size) != (1, w.qdata.shape[1]):
+                    raise ValueError("merge_int8_stack supports per-row INT8 weights")
+                if getattr(w, "zero_point", None) is not None and bool(w.zero_point.any()):
+                    raise ValueError("merge_int8_stack supports symmetric INT8 weights")
+            self._scale_dtype = self.targets[0].weight.scale.dtype
+            if any(t.weight.scale.dtype is not self._scale_dtype for t in self.targets):
+                raise ValueError("stack targets must share one scale dtype")
+        else:
+            self._swizzled = bool(self.targets[0].weight.is_swizzled_scales)
+            if any(bool(t.weight.is_swizzled_scales) != self._swizzled for t in self.targets):
+                raise ValueError("stack targets must share one scale layout")
+        self._arr, self._ws_bytes, self.device = _items(self.targets, kind)
+        with torch.cuda.device(self.device):
+            self._ws = L.workspace(self._ws_bytes, self.device)
+        self._ws_ptr = L.aligned_ptr(self._ws)
+
+    def merge(self, seeds: Sequence[int] | None = None, *, stochastic: bool = True) -> None:
+        """Merge every target once; ``seeds`` (one per target) replace the targets' seeds."""
+        if seeds is not None:
+            if len(seeds) != len(self.targets):
+                raise ValueError("one seed per target is required")
+            for it, seed in zip(self._arr, seeds):
+                it.seed = int(seed)
+        lib = L.lib()
+        mode = L.LM_ROUND_STOCHASTIC if stochastic else L.LM_ROUND_NEAREST
+        with torch.cuda.device(self.device):
+            stream = L.stream_ptr(self.device)
+            if self.kind == "int8":
+                rc = lib.lm_int8_merge_stack(self._arr, len(self.targets), L.torch_dtype_id(self._scale_dtype), mode,
+                                             self._ws_ptr, self._ws_bytes, stream)
+            else:
+                rc = lib.lm_nvfp4_merge_stack(self._arr, len(self.targets), int(self._swizzled), mode,
+                                              self._ws_ptr, self._ws_bytes, stream)
+            # the workspace is reused by the next merge on this stream: keep the
+            # caching allocator from handing it to another stream meanwhile
+            self._ws.record_stream(torch.cuda.current_stream(self.device))
+        L.check(rc)
+
+
 def merge_int8_stack(targets: Sequence[StackTarget], *, stochastic: bool = True) -> None:
     """Merge many per-row symmetric INT8 weights in place with one grouped launch."""
     if not targets:
         return
-    for t in targets:
-        w = t.weight
-        if w.qdata.dtype is not torch.int8 or tuple(w.block_size) != (1, w.qdata.shape[1]):
-            raise ValueError("merge_int8_stack supports per-row INT8 weights")
-        if getattr(w, "zero_point", None) is not None and bool(w.zero_point.any()):
-            raise ValueError("merge_int8_stack supports symmetric INT8 weights")
-    scale_dtype = targets[0].weight.scale.dtype
-    if any(t.weight.scale.dtype is not scale_dtype for t in targets):
-        raise ValueError("stack targets must share one scale dtype")
-    arr, total, device = _items(targets, "int8")
-    with torch.cuda.device(device):
-        ws = L.workspace(total, device)
-        rc = L.lib().lm_int8_merge_stack(arr, len(targets), L.torch_dtype_id(scale_dtype),
-                                        L.LM_ROUND_STOCHASTIC if stochastic else L.LM_ROUND_NEAREST,
-                                        L.aligned_ptr(ws), total, L.stream_ptr(device))
-    L.check(rc)
+    StackPlan(targets, "int8").merge([t.seed for t in targets], stochastic=stochastic)
 
 
 def merge_nvfp4_stack(targets: Sequence[StackTarget], *, stochastic: bool = True) -> None:
-    """Merge many NVFP4 weights in place (one grouped prep, per-target passes)."""
+    """Merge many NVFP4 weights in place: one amax launch and one quant launch over all targets."""
     if not targets:
         return
-    swz = bool(targets[0].weight.is_swizzled_scales)
-    if any(bool(t.weight.is_swizzled_scales) != swz for t in targets):
-        raise ValueError("stack targets must share one scale layout")
-    arr, total, device = _items(targets, "nvfp4")
-    with torch.cuda.device(device):
-        ws = L.workspace(total, device)
-        rc = L.lib().lm_nvfp4_merge_stack(arr, len(targets), int(swz),
-                                         L.LM_ROUND_STOCHASTIC if stochastic else L.LM_ROUND_NEAREST,
-                                         L.aligned_ptr(ws), total, L.stream_ptr(device))
-    L.check(rc)
+    StackPlan(targets, "nvfp4").merge([t.seed for t in targets], stochastic=stochastic)

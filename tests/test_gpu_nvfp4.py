@@ -44,7 +44,7 @@ def test_nvfp4_requant_bit_exact(shape, two_level, swizzled, sr):
         assert np.array_equal(pts.cpu().numpy().reshape(-1), opts)
 
 
-@pytest.mark.parametrize("shape,rank", [((128, 4096), 16), ((48, 256), 32), ((16, 64), 5), ((40, 384), 64)])
+@pytest.mark.parametrize("shape,rank", [((128, 4096), 16), ((48, 256), 32), ((16, 64), 5), ((40, 384), 64), ((300, 256), 16)])
 @pytest.mark.parametrize("two_level", [True, False])
 @pytest.mark.parametrize("swizzled", [False, True])
 @pytest.mark.parametrize("sr", [False, True])
@@ -115,3 +115,26 @@ def test_nvfp4_sr_two_neighbours_and_unbiased():
     vals = np.concatenate([v.reshape(-1) for v in samples])
     assert set(np.unique(vals).tolist()) == {0.5, 1.0}
     assert float(vals.mean()) == pytest.approx(x, abs=3e-3)
+
+
+@pytest.mark.parametrize("two_level", [True, False])
+@pytest.mark.parametrize("sr", [False, True])
+def test_nvfp4_zero_update_rows_keep_signed_zero_codes(two_level, sr):
+    # B rows of zeros make delta == 0 exactly: the reference keeps the base
+    # there, including -0.0 (code 8), where base + 0 would give +0.0
+    # (P/_triton_nvfp4_lora.py:183-186)
+    rows, cols, rank = 64, 512, 16
+    w = normal_bf16((rows, cols), 0.02, 21)
+    q, s, pts = _encode(w, two_level, False)
+    assert ((u8_np(q) & 15) == 8).any() or ((u8_np(q) >> 4) == 8).any()
+    b, a = lora_factors(rows, cols, rank, 22)
+    b[::3] = 0.0
+    qd, sd, bd, ad = q.to(DEV), s.to(DEV), b.to(DEV), a.to(DEV)
+    ptsd = None if pts is None else pts.to(DEV)
+    dense = K.dequantize_nvfp4(qd, sd, ptsd, lora=(bd, ad, 1.0))
+    seed = derive_seed("nvfp4.zero_rows", 0) if sr else None
+    oq, os_, opts = K.merge_nvfp4_lora(qd, sd, ptsd, 16, False, bd, ad, 1.0, rounding_seed=seed)
+    rq, rs, rpts = O.nvfp4_requant(bf16_np(dense), two_level=two_level, sr_mode=O.SR_PHILOX8 if sr else O.SR_OFF,
+                                   seed=seed or 0)
+    assert np.array_equal(u8_np(oq), rq)
+    assert np.array_equal(u8_np(os_), rs)

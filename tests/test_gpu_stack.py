@@ -87,3 +87,26 @@ def test_nvfp4_stack_equals_per_target_merges(shapes, swizzled, sr):
         assert np.array_equal(u8_np(t.weight.scale), es)
         if ep is not None:
             assert np.array_equal(t.weight.per_tensor_scale.cpu().numpy().reshape(-1), ep)
+
+
+def test_stack_plan_reuse_equals_repeated_per_target_merges():
+    from piper_offload_amd.stack import StackPlan
+
+    tg = _int8_targets([(64, 256), (32, 512), (16, 128)], 16, 40)
+    expected = []
+    for i, (q, s, b, a, strength, _seed) in enumerate(tg):
+        cq, cs = q.to(DEV), s.to(DEV)
+        for step in range(2):
+            cq, cs, _ = K.merge_int8_lora(cq, cs, None, (1, q.shape[1]), b.to(DEV), a.to(DEV), strength,
+                                          asymmetric=False, reduce_range=False,
+                                          rounding_seed=derive_seed(f"w{i}", step))
+        expected.append((cq.cpu(), cs.cpu()))
+    targets = [StackTarget(Int8Weight(q.clone().to(DEV), s.clone().to(DEV), (1, q.shape[1]), torch.bfloat16),
+                           b.to(DEV), a.to(DEV), strength, 0) for q, s, b, a, strength, _ in tg]
+    plan = StackPlan(targets, "int8")
+    for step in range(2):
+        plan.merge([derive_seed(f"w{i}", step) for i in range(len(targets))])
+    torch.cuda.synchronize()
+    for t, (eq, es) in zip(targets, expected):
+        assert torch.equal(t.weight.qdata.cpu(), eq)
+        assert torch.equal(t.weight.scale.cpu().reshape(-1), es.reshape(-1))
