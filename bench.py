@@ -265,7 +265,7 @@ class Single(Workload):
             rows, cols, rank, self.strength = 14336, 4096, 16, 1.0
             q, s = K.requantize_mx(_normal((rows, cols), 0.02, derive_seed(self.path, 0)), torch.float4_e2m1fn_x2)
             self.q, self.s = q, s
-            self.family = "blocks_full"
+            self.family = "mx"
             self.bytes_per_step = 2 * (rows * cols // 2 + rows * cols // 32) + 2 * rank * (rows + cols)
         self.b, self.a = _factors(self.path, rows, cols, rank)
         self.name = kind

@@ -1,5 +1,5 @@
 // lm_mx.hip -- MX (TorchAO MXTensor: MXFP4 / MXFP8) entry points.
-#include "lm_impl.h"
+#include "lm_mx_fast.h"
 
 // ---------------------------------------------------------------------------
 // MX
@@ -28,6 +28,20 @@ extern "C" int lm_mx_merge(uint8_t* q, uint8_t* scale, int64_t M, int64_t N, int
   if ((rc = check_rounding(rounding))) return rc;
   Ctx c;
   if ((rc = setup(c, M, N, lora, workspace, workspace_bytes, stream))) return rc;
+  if (mx_fast_ok(lora->dtype, c.nkc, N)) {
+    MxArgs ma;
+    ma.q = q;
+    ma.scale = scale;
+    ma.at = c.at;
+    ma.bp = c.bp;
+    ma.M = M;
+    ma.N = N;
+    ma.strength = lora->strength;
+    ma.swizzled = swizzled;
+    ma.mode = scaling;
+    ma.seed = rounding ? rounding->seed : 0;
+    return mx_fast_run(ma, elem_dtype, c.nkc, is_sr(rounding), c.st);
+  }
   BlkArgs a = blk_args_base(c, M, N, lora, rounding);
   a.q = q;
   a.scale = scale;

@@ -1,0 +1,208 @@
+// lm_mx_fast.h -- in-place MX merge (MXFP4 / MXFP8 e4m3 / e5m2 elements,
+// e8m0 block-32 scales, plain or 128x4-swizzled) for bf16 factors and
+// N % 128 == 0.  P/ = the reference's src/piper_offload/.
+//
+// Same decomposition as the NVFP4 kernels: a 512-thread workgroup owns 16
+// rows, wave w walks the 128-column macro tiles mt = w, w + 8, ..., and a
+// lane holds row (lane & 15) and the 32 columns 32*(lane >> 4) .. +31 of a
+// macro tile -- exactly one MX block, so the block max, the shared exponent
+// and the codes never leave the lane (P/_triton_mx_lora.py:333-425 does one
+// pass: merge, block amax, scale, encode, all in place).
+//
+// Arithmetic (P/_triton_mx_lora.py:209-295, bf16 compute):
+//   base   = bf16(bf16(code) * bf16(2^e))  -- an e2m1 value times a power of
+//            two is exact in fp32 and in bf16, so this is one multiply; fp8
+//            elements can fall below bf16's subnormal range and keep the
+//            rounding;
+//   merged = bf16(fma(delta, strength, base));
+//   scale  = mx_scale(max |merged|, mode); codes = enc(clamp(merged * 1/scale)).
+#pragma once
+#include "lm_nvfp4_fast.h"
+
+struct MxArgs {
+  uint8_t* q;       // MXFP4: [M, N/2] e2m1 pairs; MXFP8: [M, N] codes (in place)
+  uint8_t* scale;   // e8m0 block-32 scales (in place)
+  const uint16_t* at;
+  const uint16_t* bp;
+  int64_t M, N;
+  float strength;
+  int swizzled;
+  int mode;         // MX_FLOOR / MX_RCEIL / MX_CEIL / MX_EVEN
+  uint64_t seed;
+};
+
+template <int ELEM>
+struct MxTraits {
+  static constexpr int emax = ELEM == E2M1 ? 2 : (ELEM == E4M3 ? 8 : 15);
+  static constexpr float maxpos = ELEM == E2M1 ? 6.0f : (ELEM == E4M3 ? 448.0f : 57344.0f);
+  static constexpr int mbits = ELEM == E2M1 ? 1 : (ELEM == E4M3 ? 3 : 2);
+  static constexpr int lane_bytes = ELEM == E2M1 ? 16 : 32;  // code bytes of one lane's block
+};
+
+template <int ELEM, int NKC>
+struct MxTileIn {
+  uint4 codes[MxTraits<ELEM>::lane_bytes / 16];
+  uint32_t sc;
+  v4i16 aop[8][NKC];
+};
+
+template <int ELEM, int NKC>
+struct MxLane {
+  uint8_t* q;
+  uint8_t* sc;
+  const uint16_t* at;
+  int64_t sc_stride;
+};
+
+// per-tile strides: codes advance 64 (fp4) / 128 (fp8) bytes per macro tile;
+// the scale column advances by 4: 4 bytes plain, one 512-byte col-block swizzled
+template <int ELEM, int NKC>
+DEV MxLane<ELEM, NKC> mx_lane(const MxArgs& a, int64_t rowc, int lane) {
+  constexpr int RPAD = NKC * 16;
+  constexpr int LB = MxTraits<ELEM>::lane_bytes;
+  const int p = lane & 15, g = lane >> 4;
+  MxLane<ELEM, NKC> l;
+  l.q = a.q + rowc * (ELEM == E2M1 ? (a.N >> 1) : a.N) + LB * g;
+  l.sc = a.scale + blocked_offset(rowc, g, a.N >> 5, a.swizzled);
+  l.sc_stride = a.swizzled ? 512 : 4;
+  l.at = a.at + (int64_t)(32 * (p >> 2) + (p & 3)) * RPAD + g * (NKC * 4);
+  return l;
+}
+
+template <int ELEM, int NKC>
+DEV void mx_load_tile(const MxLane<ELEM, NKC>& l, int mt, MxTileIn<ELEM, NKC>& t) {
+  constexpr int RPAD = NKC * 16;
+  constexpr int LB = MxTraits<ELEM>::lane_bytes;
+  const uint8_t* q = l.q + (int64_t)mt * (4 * LB);
+#pragma unroll
+  for (int i = 0; i < LB / 16; ++i) t.codes[i] = *(const uint4*)(q + 16 * i);
+  t.sc = l.sc[(int64_t)mt * l.sc_stride];
+  const uint16_t* at = l.at + (int64_t)mt * (128 * RPAD);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) load_kchunks<NKC>(at + 4 * k * RPAD, t.aop[k]);
+}
+
+template <int ELEM, int NKC, bool SR>
+DEV void mx_tile(const MxArgs& a, const MxTileIn<ELEM, NKC>& in, const v4i16 (&bop)[NKC], int64_t row, int mt,
+                 int lane, uint8_t* qo, uint8_t* so) {
+  constexpr float L = MxTraits<ELEM>::maxpos;
+  float d[32];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const v4f32 acc = mfma_chain<NKC, false>(in.aop[k], bop);
+    d[4 * k + 0] = acc[0];
+    d[4 * k + 1] = acc[1];
+    d[4 * k + 2] = acc[2];
+    d[4 * k + 3] = acc[3];
+  }
+  const float s = e8m0_value(in.sc);
+  float m[32];
+  float amax = 0.0f;
+  if constexpr (ELEM == E2M1) {
+    const uint32_t w[4] = {in.codes[0].x, in.codes[0].y, in.codes[0].z, in.codes[0].w};
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const v2f32 pr = e2m1_pair(w[q >> 2], q & 3);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int j = 2 * q + e;
+        m[j] = bf16r(__builtin_fmaf(d[j], a.strength, pr[e] * s));
+        amax = __builtin_fmaxf(amax, __builtin_fabsf(m[j]));
+      }
+    }
+  } else {
+    const uint32_t w[8] = {in.codes[0].x, in.codes[0].y, in.codes[0].z, in.codes[0].w,
+                           in.codes[1].x, in.codes[1].y, in.codes[1].z, in.codes[1].w};
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const float base = bf16r(fp8_decode<ELEM>(w[j >> 2], j & 3) * s);
+      m[j] = bf16r(__builtin_fmaf(d[j], a.strength, base));
+      amax = __builtin_fmaxf(amax, __builtin_fabsf(m[j]));
+    }
+  }
+  float inv;
+  const uint32_t enc = mx_scale(amax, a.mode, MxTraits<ELEM>::emax, L, MxTraits<ELEM>::mbits, inv);
+  uint32_t rw[16];
+  if constexpr (SR) sr_words_aligned<32>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4)), rw);
+  float x[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    float v = m[j] * inv;
+    if constexpr (SR) {
+      v = __builtin_amdgcn_fmed3f(v, -L, L);
+      const uint32_t nw = ~rw[j >> 1];
+      const uint32_t nh = (j & 1) ? (nw >> 16) : (nw & 0xffffu);
+      if constexpr (ELEM == E2M1) {
+        v = nv_sr_value(v, nh);
+      } else {
+        // grid spacing of the fp8 value: 2^(E - mbits), at least the subnormal step
+        constexpr int MB = ELEM == E4M3 ? 3 : 2;
+        constexpr int MINE = ELEM == E4M3 ? -9 : -16;
+        const float mag = __builtin_fabsf(v);
+        int e = (int)((f2u(mag) >> 23) & 255u) - 127 - MB;
+        e = e < MINE ? MINE : e;
+        const int qv = (int)(nh - (uint32_t)cvt_flr_neg(__builtin_ldexpf(mag, 16 - e))) >> 16;
+        v = __builtin_copysignf(__builtin_ldexpf((float)qv, e), v);
+      }
+    } else if constexpr (ELEM != E2M1) {
+      v = __builtin_amdgcn_fmed3f(v, -L, L);  // the e2m1 conversion saturates by itself
+    }
+    x[j] = v;
+  }
+  if constexpr (ELEM == E2M1) {
+    uint32_t words[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t wd = 0u;
+      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 0], x[8 * k + 1], 1.0f, 0);
+      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 2], x[8 * k + 3], 1.0f, 1);
+      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 4], x[8 * k + 5], 1.0f, 2);
+      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 6], x[8 * k + 7], 1.0f, 3);
+      words[k] = wd;
+    }
+    *(uint4*)(qo + (int64_t)mt * 64) = make_uint4(words[0], words[1], words[2], words[3]);
+  } else {
+    uint32_t wv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wv[i] = fp8_pack4<ELEM>(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+    uint4* dst = (uint4*)(qo + (int64_t)mt * 128);
+    dst[0] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+    dst[1] = make_uint4(wv[4], wv[5], wv[6], wv[7]);
+  }
+  so[0] = (uint8_t)enc;
+}
+
+template <int ELEM, int NKC, bool SR>
+__global__ __launch_bounds__(NV_NW * 64) void k_mx_fast(MxArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
+  const int64_t row = (int64_t)blockIdx.x * 16 + rl;
+  const bool rok = row < a.M;
+  const int64_t rowc = rok ? row : a.M - 1;  // in-bounds loads; results dropped
+  const int ntiles = (int)(a.N >> 7);
+  const MxLane<ELEM, NKC> l = mx_lane<ELEM, NKC>(a, rowc, lane);
+  v4i16 bop[NKC];
+  load_bop<NKC>(a.bp, row, lane, bop);  // Bp holds ceil(M/16)*16 rows
+  if (wave >= ntiles) return;
+  MxTileIn<ELEM, NKC> cur;
+  mx_load_tile<ELEM, NKC>(l, wave, cur);
+  for (int mt = wave; mt < ntiles; mt += NV_NW) {
+    MxTileIn<ELEM, NKC> nxt;
+    mx_load_tile<ELEM, NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
+    if (rok) mx_tile<ELEM, NKC, SR>(a, cur, bop, row, mt, lane, l.q, l.sc + (int64_t)mt * l.sc_stride);
+    cur = nxt;
+  }
+}
+
+static inline bool mx_fast_ok(int cd, int nkc, int64_t N) { return cd == LM_BF16 && nkc > 0 && (N % 128) == 0; }
+
+static int mx_fast_run(const MxArgs& a, int elem, int nkc, bool sr, hipStream_t st) {
+  const dim3 grid((unsigned)((a.M + 15) / 16)), block(NV_NW * 64);
+  TimedLaunch timed("mx", st);
+#define MXL(E_, SR_) NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_mx_fast<E_, NKC_, SR_>), grid, block, 0, st, a))
+  if (elem == LM_E2M1) { if (sr) { MXL(E2M1, true); } else { MXL(E2M1, false); } }
+  else if (elem == LM_E4M3) { if (sr) { MXL(E4M3, true); } else { MXL(E4M3, false); } }
+  else { if (sr) { MXL(E5M2, true); } else { MXL(E5M2, false); } }
+#undef MXL
+  LAUNCH_CHECK();
+  return LM_OK;
+}

@@ -37,12 +37,13 @@ def test_mx_requant_bit_exact(elem, mode, swizzled, sr):
     assert np.array_equal(u8_np(s), os_)
 
 
-@pytest.mark.parametrize("elem", ["fp4", "e4m3"])
-@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("elem", ["fp4", "e4m3", "e5m2"])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
 @pytest.mark.parametrize("swizzled", [False, True])
 @pytest.mark.parametrize("sr", [False, True])
-@pytest.mark.parametrize("shape,rank", [((128, 4096), 16), ((24, 96), 5)])
-def test_mx_fused_equals_requant_of_gpu_dense(elem, mode, swizzled, sr, shape, rank):
+@pytest.mark.parametrize("shape,rank,strength", [((128, 4096), 16, 1.0), ((24, 96), 5, 1.0), ((40, 256), 32, 0.75),
+                                                 ((16, 128), 64, -0.5)])
+def test_mx_fused_equals_requant_of_gpu_dense(elem, mode, swizzled, sr, shape, rank, strength):
     tdt, fmt = ELEMS[elem]
     rows, cols = shape
     w = normal_bf16(shape, 0.02, 4)
@@ -53,11 +54,11 @@ def test_mx_fused_equals_requant_of_gpu_dense(elem, mode, swizzled, sr, shape, r
     base = K.dequantize_mx(qd, sd, tdt, cols, swizzled=swizzled)
     obase = O.mx_dequant(q, s, fmt, cols, swizzled=swizzled)
     assert np.array_equal(bf16_np(base), obase)
-    dense = K.dequantize_mx(qd, sd, tdt, cols, swizzled=swizzled, lora=(b.to(DEV), a.to(DEV), 1.0))
-    assert_merged_close(bf16_np(dense), O.merge_dense(obase, bf16_np(b), bf16_np(a), 1.0), obase)
+    dense = K.dequantize_mx(qd, sd, tdt, cols, swizzled=swizzled, lora=(b.to(DEV), a.to(DEV), strength))
+    assert_merged_close(bf16_np(dense), O.merge_dense(obase, bf16_np(b), bf16_np(a), strength), obase)
     seed = derive_seed("mx.fused", rows) if sr else None
     qstore = qd.clone() if elem == "fp4" else qd.clone().view(tdt)
-    K.merge_mx_lora_(qstore, sd, tdt, 32, torch.bfloat16, b.to(DEV), a.to(DEV), 1.0, scaling_mode=mode,
+    K.merge_mx_lora_(qstore, sd, tdt, 32, torch.bfloat16, b.to(DEV), a.to(DEV), strength, scaling_mode=mode,
                      swizzled=swizzled, rounding_seed=seed)
     rq, rs = O.mx_requant(bf16_np(dense), fmt, mode, swizzled=swizzled, sr_mode=O.SR_PHILOX8 if sr else O.SR_OFF,
                           seed=seed or 0)
