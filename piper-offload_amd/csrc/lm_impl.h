@@ -748,9 +748,9 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   }
 }
 
-template <int KIND, bool SR, int NKC, int NW, int CACHE>
+template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC>()>
 __global__ __launch_bounds__(NW * 64) void k_rows_fast(RowArgs a) {
-  rows_fast_body<KIND, SR, NKC, NW, CACHE>(a, (int64_t)blockIdx.x * 16);
+  rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_>(a, (int64_t)blockIdx.x * 16);
 }
 template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC>()>
 __global__ __launch_bounds__(NW * 64) void k_rows_fast_stack(const RowStackItem* __restrict__ items, int count) {
@@ -1393,11 +1393,28 @@ static inline bool rows_fast_ok(int kind, int cd, int sdt, bool asym, int nkc, i
   return cd == LM_BF16 && nkc > 0 && (N % 64) == 0 && (kind != K_INT8 || (!asym && sdt == LM_F32));
 }
 
+// Rows with more macro tiles per wave than the register cache holds are
+// merged twice (the surplus tiles are recomputed in pass 2).  A 16-tile cache
+// removes most of that: measured on MI355X it pays for rank 64 (FP8
+// [8192, 8192] r64: RTN 0.124 -> 0.083 ms, SR 0.137 -> 0.115 ms) and for
+// round-to-nearest long rows (down_proj RTN -16%), while stochastic rounding
+// at rank <= 32 is VALU-bound and loses the occupancy it costs.
+static constexpr int ROW_DEEP_CACHE = 16;
+static inline bool rows_deep_cache(int nkc, bool sr, int64_t N) {
+  const int64_t tpw = (N / 64 + ROW_NW - 1) / ROW_NW;
+  return tpw > ROW_CACHE && (nkc == 4 || !sr);
+}
+
 template <int KIND, bool SR, int NKC>
 static int launch_rows_fast(const RowArgs& a, hipStream_t st) {
   dim3 grid((unsigned)((a.M + 15) / 16)), block(ROW_NW * 64);
   TimedLaunch timed("rows", st);
-  hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_CACHE>), grid, block, 0, st, a);
+  if (rows_deep_cache(NKC, SR, a.N)) {
+    if constexpr (NKC == 4 || !SR)
+      hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_DEEP_CACHE, NKC == 4 ? 1 : 2>), grid, block, 0, st, a);
+  } else {
+    hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_CACHE>), grid, block, 0, st, a);
+  }
   LAUNCH_CHECK();
   return LM_OK;
 }

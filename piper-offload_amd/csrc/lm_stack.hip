@@ -74,13 +74,27 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
   }
   int rc = stack_layout(items, count, workspace, workspace_bytes, preps, cursor);
   int nkc_max = 0, cd = items[0].lora.dtype;
-  int64_t tiles = 0;
+  for (int i = 0; i < count; ++i) {
+    const int nkc = rpad_of(items[i].lora.rank) / 16;
+    nkc_max = nkc > nkc_max ? nkc : nkc_max;
+  }
+  const bool sr = rounding_mode == LM_ROUND_STOCHASTIC;
+  bool fast = true;
+  for (int i = 0; i < count; ++i) fast = fast && rows_fast_ok(K_INT8, cd, scale_dtype, false, nkc_max, items[i].N);
+  // fast kernels: items whose rows want the deep register cache go to a
+  // second launch; each launch numbers its 16-row groups from 0
+  int n_regular = 0;
+  for (int i = 0; i < count; ++i) n_regular += (fast && rows_deep_cache(nkc_max, sr, items[i].N)) ? 0 : 1;
+  int64_t tiles[2] = {0, 0};
+  int slot[2] = {0, n_regular};
   for (int i = 0; rc == LM_OK && i < count; ++i) {
     const lm_stack_item& s = items[i];
     if (s.lora.dtype != cd) rc = fail(LM_EUNSUPPORTED, "all stack items must share one factor dtype");
     if (s.M <= 0 || s.N <= 0 || !s.q || !s.scale || !s.q_out || !s.scale_out)
       rc = fail(LM_EINVAL, "stack item %d has an invalid shape or null pointer", i);
-    RowArgs& a = rows[i].a;
+    const int grp = (fast && rows_deep_cache(nkc_max, sr, s.N)) ? 1 : 0;
+    RowStackItem& r = rows[slot[grp]++];
+    RowArgs& a = r.a;
     a.q = s.q;
     a.scale = s.scale;
     a.zp = nullptr;
@@ -94,10 +108,8 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
     a.qmin = -128;
     a.qmax = 127;
     a.seed = s.seed;
-    rows[i].tile_begin = tiles;
-    tiles += (s.M + 15) / 16;
-    int nkc = rpad_of(s.lora.rank) / 16;
-    nkc_max = nkc > nkc_max ? nkc : nkc_max;
+    r.tile_begin = tiles[grp];
+    tiles[grp] += (s.M + 15) / 16;
   }
   if (rc == LM_OK) rc = stack_prep(preps, count, dev_prep, st);
   if (rc == LM_OK) {
@@ -109,18 +121,27 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
   }
   if (rc == LM_OK) rc = lm_stage_h2d(dev_rows, rows, sizeof(RowStackItem) * count, st);
   if (rc == LM_OK) {
-    const bool sr = rounding_mode == LM_ROUND_STOCHASTIC;
-    dim3 grid((unsigned)tiles), block(ROW_NW * 64);
+    const dim3 block(ROW_NW * 64);
     TimedLaunch timed("rows_stack", st);
-    bool fast = true;
-    for (int i = 0; i < count; ++i)
-      fast = fast && rows_fast_ok(K_INT8, cd, scale_dtype, false, nkc_max, items[i].N);
+    const RowStackItem* d0 = (const RowStackItem*)dev_rows;
     if (fast) {
-#define RF(SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, ROW_CACHE>), grid, block, 0, st, (const RowStackItem*)dev_rows, count))
-      if (sr) { RF(true); } else { RF(false); }
+      if (tiles[0] > 0) {
+        const dim3 grid((unsigned)tiles[0]);
+#define RF(SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, ROW_CACHE>), grid, block, 0, st, d0, n_regular))
+        if (sr) { RF(true); } else { RF(false); }
 #undef RF
+      }
+      if (tiles[1] > 0) {
+        const dim3 grid((unsigned)tiles[1]);
+        const RowStackItem* d1 = d0 + n_regular;
+        const int n_deep = count - n_regular;
+#define RD(SR_, PF_) NKC_SWITCH(nkc_bucket(nkc_max), if constexpr (NKC_ == 4 || !SR_) hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, ROW_DEEP_CACHE, PF_>), grid, block, 0, st, d1, n_deep))
+        if (sr) { RD(true, 1); } else if (nkc_max == 4) { RD(false, 1); } else { RD(false, 2); }
+#undef RD
+      }
     } else {
-#define RS(CD_, SDT_, SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_stack<K_INT8, CD_, SDT_, SR_, NKC_, ROW_NW, ROW_CACHE>), grid, block, 0, st, (const RowStackItem*)dev_rows, count, scale_dtype))
+      const dim3 grid((unsigned)tiles[0]);
+#define RS(CD_, SDT_, SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_stack<K_INT8, CD_, SDT_, SR_, NKC_, ROW_NW, ROW_CACHE>), grid, block, 0, st, d0, count, scale_dtype))
     if (cd == LM_F16) {
       if (scale_dtype == LM_BF16) { if (sr) { RS(F16, BF16, true); } else { RS(F16, BF16, false); } }
       else { if (sr) { RS(F16, F32, true); } else { RS(F16, F32, false); } }
