@@ -16,8 +16,9 @@ whole stack once, in place, through the grouped HIP kernel.
 ``cpu_baseline`` block times the CPU oracle (a C restatement of the same
 merge) on a bounded sample of the same workload.
 
-    python bench.py [--steps K] [--warmup W] [--workload int8_stack|nvfp4_stack|int8|fp8|q8_0|nvfp4|mxfp4|copy]
-                    [--rounding stochastic|nearest] [--cpu-seconds S]
+    python bench.py [--steps K] [--warmup W]
+                    [--workload int8_stack|nvfp4_stack|int8|fp8|q8_0|nvfp4|mxfp4|gguf|copy]
+                    [--rounding stochastic|nearest] [--gguf-type Q4_K] [--cpu-seconds S]
 """
 
 from __future__ import annotations
@@ -46,13 +47,42 @@ LAYER_SHAPES = (
 )
 
 
+GGUF_TYPES = {"F32": 0, "F16": 1, "BF16": 30, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8, "Q2_K": 10,
+              "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_NL": 20, "IQ4_XS": 23}
+# byte offsets of the fp16 fields (d, dmin / m) of each GGUF block struct
+GGUF_F16_FIELDS = {2: (0,), 3: (0, 2), 6: (0,), 7: (0, 2), 8: (0,), 20: (0,), 10: (80, 82), 11: (108,),
+                   12: (0, 2), 13: (0, 2), 14: (208,), 23: (0,)}
+
+
+def _gguf_bytes(qtype: int, rows: int, cols: int, seed: int):  # noqa: ANN202
+    """Random GGUF blocks of one type (finite fp16 scale fields) as a numpy uint8 [rows, row_bytes]."""
+    import numpy as np
+
+    from piper_offload_amd.gguf_dequant import GGML_QUANT_SIZES
+
+    bs, ts = GGML_QUANT_SIZES[qtype]
+    rng = np.random.default_rng(seed)
+    nblk = rows * cols // bs
+    if qtype in (0, 1, 30):
+        vals = (rng.standard_normal(rows * cols, dtype=np.float32) * 0.02)
+        raw = vals.view(np.uint8) if qtype == 0 else (
+            vals.astype(np.float16).view(np.uint8) if qtype == 1 else (vals.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8))
+        return np.ascontiguousarray(raw).reshape(rows, -1)
+    raw = rng.integers(0, 256, (nblk, ts), dtype=np.uint8)
+    for off in GGUF_F16_FIELDS[qtype]:
+        raw[:, off:off + 2] = (rng.uniform(1e-4, 1e-3, nblk).astype(np.float16)).view(np.uint8).reshape(nblk, 2)
+    return raw.reshape(rows, -1)
+
+
 def _parse() -> argparse.Namespace:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="int8_stack",
-                   choices=["int8_stack", "nvfp4_stack", "int8", "fp8", "q8_0", "nvfp4", "mxfp4", "copy"])
+                   choices=["int8_stack", "nvfp4_stack", "int8", "fp8", "q8_0", "nvfp4", "mxfp4", "gguf", "copy"])
+    p.add_argument("--gguf-type", default="Q4_K", choices=sorted(GGUF_TYPES),
+                   help="GGUF type of --workload gguf (dequantize to bf16)")
     p.add_argument("--rounding", default="stochastic", choices=["stochastic", "nearest"])
     p.add_argument("--layers", type=int, default=32)
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-oracle baseline (0: skip)")
@@ -227,6 +257,33 @@ class Copy(Workload):
         torch.bitwise_not(self.src, out=self.dst)
 
 
+class Gguf(Workload):
+    """GGUF dequantize (P/gguf_dequant.py:303-331) of one gate_proj-shaped [14336, 4096] tensor to bf16."""
+
+    family = "gguf"
+
+    def __init__(self, type_name: str) -> None:
+        import torch
+
+        from piper_offload_amd.gguf_dequant import GGML_QUANT_SIZES
+
+        self.qtype = GGUF_TYPES[type_name]
+        rows, cols = 14336, 4096
+        raw = _gguf_bytes(self.qtype, rows, cols, 0)
+        self.data = torch.from_numpy(raw).to("cuda")
+        self.out_bytes = 2 * rows * cols
+        self.bytes_per_step = raw.size + self.out_bytes
+        self.name = f"gguf_{type_name.lower()}"
+        bs, ts = GGML_QUANT_SIZES[self.qtype]
+        self.config = {"workload": f"GGUF {type_name} dequantize [{rows},{cols}] -> bf16 ({ts} B per {bs} elements)",
+                       "quant_type": type_name, "algorithmic_bytes_per_step": self.bytes_per_step}
+
+    def step(self, index: int) -> None:
+        from piper_offload_amd.gguf_dequant import dequantize
+
+        dequantize(self.data, self.qtype)
+
+
 class Single(Workload):
     """One tensor of configs 2-4 (or NVFP4 / MXFP4 at the gate_proj shape)."""
 
@@ -303,7 +360,7 @@ class Single(Workload):
 # ---------------------------------------------------------------------------
 # CPU baseline: the oracle (C restatement, OpenMP) on a bounded sample
 # ---------------------------------------------------------------------------
-def cpu_baseline(kind: str, stochastic: bool, budget_s: float) -> dict | None:
+def cpu_baseline(kind: str, stochastic: bool, budget_s: float, gguf_type: str = "Q4_K") -> dict | None:
     if budget_s <= 0:
         return None
     import numpy as np
@@ -330,6 +387,20 @@ def cpu_baseline(kind: str, stochastic: bool, budget_s: float) -> dict | None:
         def nbytes(rows):  # noqa: ANN001, ANN202
             return _int8_bytes(rows, cols, rank)
         shape_note = f"{cols} gate_proj-shaped INT8 tensor (rank {rank})"
+        what = f"oracle dequant + fp32 B@A + requant ({'SR' if stochastic else 'RTN'})"
+    elif kind == "gguf":
+        qtype, cols = GGUF_TYPES[gguf_type], 4096
+        def make(rows):  # noqa: ANN001, ANN202
+            return _gguf_bytes(qtype, rows, cols, 1)
+        def run(data):  # noqa: ANN001, ANN202
+            O.gguf_dequant(data, qtype, cd=O.DT_BF16)
+        from piper_offload_amd.gguf_dequant import GGML_QUANT_SIZES
+
+        bs, ts = GGML_QUANT_SIZES[qtype]
+        def nbytes(rows):  # noqa: ANN001, ANN202
+            return rows * cols * 2 + rows * cols // bs * ts
+        shape_note = f"{cols} GGUF {gguf_type} tensor"
+        what = "oracle GGUF dequantize to bf16"
     else:
         return None
     # the sample is one full gate_proj-shaped tensor, merged repeatedly until
@@ -344,8 +415,7 @@ def cpu_baseline(kind: str, stochastic: bool, budget_s: float) -> dict | None:
     t = time.perf_counter() - t0
     return {"value": round(nbytes(rows) * reps / t / 1e9, 3), "unit": "GB/s",
             "cores": int(os.environ.get("OMP_NUM_THREADS", cores)), "kind": "port",
-            "sample": f"oracle dequant + fp32 B@A + requant ({'SR' if stochastic else 'RTN'}) of one {rows} x "
-                      f"{shape_note}, {reps} repeats in {t:.1f} s"}
+            "sample": f"{what} of one {rows} x {shape_note}, {reps} repeats in {t:.1f} s"}
 
 
 def _traffic(name: str) -> int | None:
@@ -379,6 +449,8 @@ def main() -> int:
         wl = Copy()
     elif args.workload == "nvfp4_stack":
         wl = Nvfp4Stack(args.layers, stochastic)
+    elif args.workload == "gguf":
+        wl = Gguf(args.gguf_type)
     else:
         wl = Single(args.workload, stochastic)
     torch.cuda.synchronize()
@@ -407,7 +479,7 @@ def main() -> int:
     # quant launches of a two-level NVFP4 merge) against the step's bytes
     achieved = wl.bytes_per_step * args.steps / (kern_ms * 1e-3) / 1e9 if launches else None
     print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
-    cpu = cpu_baseline(args.workload, stochastic, args.cpu_seconds)
+    cpu = cpu_baseline(args.workload, stochastic, args.cpu_seconds, args.gguf_type)
     out = {
         "metric": METRIC,
         "value": round(value, 2),

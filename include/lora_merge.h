@@ -75,7 +75,25 @@ enum lm_rounding_mode {
 enum lm_mx_scaling { LM_MX_FLOOR = 0, LM_MX_RCEIL = 1, LM_MX_CEIL = 2, LM_MX_EVEN = 3 };
 
 /* GGUF quant types (ggml numbering) */
-enum lm_gguf_type { LM_GGUF_F32 = 0, LM_GGUF_F16 = 1, LM_GGUF_Q8_0 = 8, LM_GGUF_BF16 = 30 };
+/* GGML quantization type ids (the values of gguf.GGMLQuantizationType) of the
+ * types P/gguf_dequant.py:278-294 dispatches */
+enum lm_gguf_type {
+  LM_GGUF_F32 = 0,
+  LM_GGUF_F16 = 1,
+  LM_GGUF_Q4_0 = 2,
+  LM_GGUF_Q4_1 = 3,
+  LM_GGUF_Q5_0 = 6,
+  LM_GGUF_Q5_1 = 7,
+  LM_GGUF_Q8_0 = 8,
+  LM_GGUF_Q2_K = 10,
+  LM_GGUF_Q3_K = 11,
+  LM_GGUF_Q4_K = 12,
+  LM_GGUF_Q5_K = 13,
+  LM_GGUF_Q6_K = 14,
+  LM_GGUF_IQ4_NL = 20,
+  LM_GGUF_IQ4_XS = 23,
+  LM_GGUF_BF16 = 30
+};
 
 enum lm_status {
   LM_OK = 0,
@@ -178,8 +196,14 @@ int lm_q8_0_merge(const uint8_t* packed, uint8_t* packed_out, int64_t M, int64_t
                   const lm_rounding* rounding, void* workspace, size_t workspace_bytes, void* stream);
 int lm_q8_0_requant(const void* dense, int32_t dense_dtype, uint8_t* packed_out, int64_t M, int64_t N,
                     const lm_rounding* rounding, void* workspace, size_t workspace_bytes, void* stream);
-/* GGUF dequantize of `rows` rows of `cols` logical elements
- * (P/gguf_dequant.py:303-331; out dtype LM_BF16/LM_F16/LM_F32). */
+/* GGUF dequantize of `rows` rows of `cols` logical elements of any
+ * lm_gguf_type (replaces P/gguf_dequant.py:303-331 `dequantize`; out dtype
+ * LM_BF16/LM_F16/LM_F32, the reference's `dtype`, which is also the precision
+ * every step rounds to).  `packed` holds rows*cols/block whole blocks back to
+ * back (any alignment); `out` is 16-byte aligned.  With `lora` NULL no
+ * workspace is used.  A non-NULL `lora` adds strength*B@A to the dequantized
+ * values (Q8_0 only; workspace as lm_workspace_size).  An unknown type returns
+ * LM_EUNSUPPORTED (the reference raises NotImplementedError). */
 int lm_gguf_dequant(const uint8_t* packed, int32_t quant_type, int64_t rows, int64_t cols, const lm_lora* lora,
                     void* out, int32_t out_dtype, void* workspace, size_t workspace_bytes, void* stream);
 

@@ -58,6 +58,8 @@ _SIGS = {
     "lmo_mx_requant": (None, [_P, _I, _I64, _I64, _I, _I, _I, _I, _U64, _P, _P]),
     "lmo_q8_0_dequant": (None, [_P, _I64, _I64, _I, _P]),
     "lmo_q8_0_requant": (None, [_P, _I, _I64, _I64, _I, _U64, _P]),
+    "lmo_gguf_sizes": (_I, [_I, _P, _P]),
+    "lmo_gguf_dequant": (_I, [_P, _I, _I64, _I, _P]),
     "lmo_f32_to_bf16": (None, [_P, _P, _I64]),
     "lmo_f32_to_f16": (None, [_P, _P, _I64]),
     "lmo_f16_to_f32": (None, [_P, _P, _I64]),
@@ -359,3 +361,27 @@ def q8_0_requant(dense, *, cd=DT_BF16, sr_mode=SR_OFF, seed=0):
     packed = np.empty((M, N // 32 * 34), np.uint8)
     load().lmo_q8_0_requant(_p(dense), cd, M, N, sr_mode, seed, _p(packed))
     return packed
+
+
+def gguf_sizes(quant_type: int) -> tuple[int, int] | None:
+    """(block size, bytes per block) of a GGUF type the reference dequantizes."""
+    b, t = ctypes.c_int(0), ctypes.c_int(0)
+    if not load().lmo_gguf_sizes(int(quant_type), ctypes.byref(b), ctypes.byref(t)):
+        return None
+    return b.value, t.value
+
+
+def gguf_dequant(packed, quant_type: int, *, cd=DT_BF16):
+    """P/gguf_dequant.py:303-331 over a flat run of whole blocks (uint8 bytes);
+    returns the logical values as a 1-D array (bf16/fp16 bit patterns or fp32)."""
+    packed = np.ascontiguousarray(packed, np.uint8).reshape(-1)
+    sizes = gguf_sizes(quant_type)
+    if sizes is None:
+        raise NotImplementedError(f"GGUF quant type {quant_type} is not dispatched by the reference")
+    bs, ts = sizes
+    if packed.size % ts:
+        raise ValueError("packed bytes are not a whole number of blocks")
+    nblocks = packed.size // ts
+    out = _dense_empty((nblocks * bs,), cd)
+    load().lmo_gguf_dequant(_p(packed), int(quant_type), nblocks, cd, _p(out))
+    return out

@@ -603,6 +603,186 @@ EXPORT void lmo_q8_0_requant(const void* dense, int cd, int64_t M, int64_t N, in
 /* ------------------------------------------------------------------ */
 /* small codec entry points (for exhaustive tests)                      */
 /* ------------------------------------------------------------------ */
+/* ------------------------------------------------------------------ */
+/* GGUF dequantize, every type P/gguf_dequant.py:278-294 dispatches      */
+/* ------------------------------------------------------------------ */
+/* The reference evaluates each type as a short sequence of torch ops in the
+ * output dtype `dt` (P/gguf_dequant.py:303-331): every op computes in fp32
+ * and rounds to `dt` (round_dt), fp16 block scales are first converted to
+ * `dt`, and integer codes are exact in every dt.  Byte offsets are the ggml
+ * block structs (block_q4_0 ... block_iq4_xs); the element order is the one
+ * the reference's reshapes produce, cited per type. */
+enum {
+  GG_F32 = 0, GG_F16 = 1, GG_Q4_0 = 2, GG_Q4_1 = 3, GG_Q5_0 = 6, GG_Q5_1 = 7, GG_Q8_0 = 8, GG_Q2_K = 10,
+  GG_Q3_K = 11, GG_Q4_K = 12, GG_Q5_K = 13, GG_Q6_K = 14, GG_IQ4_NL = 20, GG_IQ4_XS = 23, GG_BF16 = 30
+};
+static const int8_t kIQ4NL[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+static inline float gg_f16(const uint8_t* p) { return f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* P/gguf_dequant.py:44-49 (_get_scale_min): 6-bit scale and min of sub-block j */
+static void gg_scale_min(const uint8_t* s, int j, int* sc, int* mn) {
+  if (j < 4) {
+    *sc = s[j] & 0x3F;
+    *mn = s[4 + j] & 0x3F;
+  } else {
+    *sc = (s[8 + j - 4] & 0x0F) | ((s[j - 4] >> 2) & 0x30);
+    *mn = (s[8 + j - 4] >> 4) | ((s[4 + j - 4] >> 2) & 0x30);
+  }
+}
+
+/* block size and bytes per block (ggml GGML_QUANT_SIZES); 0 if unsupported */
+EXPORT int lmo_gguf_sizes(int type, int* block, int* bytes) {
+  int b = 0, t = 0;
+  switch (type) {
+    case GG_F32: b = 1; t = 4; break;
+    case GG_F16: b = 1; t = 2; break;
+    case GG_BF16: b = 1; t = 2; break;
+    case GG_Q4_0: b = 32; t = 18; break;
+    case GG_Q4_1: b = 32; t = 20; break;
+    case GG_Q5_0: b = 32; t = 22; break;
+    case GG_Q5_1: b = 32; t = 24; break;
+    case GG_Q8_0: b = 32; t = 34; break;
+    case GG_IQ4_NL: b = 32; t = 18; break;
+    case GG_Q2_K: b = 256; t = 84; break;
+    case GG_Q3_K: b = 256; t = 110; break;
+    case GG_Q4_K: b = 256; t = 144; break;
+    case GG_Q5_K: b = 256; t = 176; break;
+    case GG_Q6_K: b = 256; t = 210; break;
+    case GG_IQ4_XS: b = 256; t = 136; break;
+    default: return 0;
+  }
+  if (block) *block = b;
+  if (bytes) *bytes = t;
+  return 1;
+}
+
+static void gg_block(int type, const uint8_t* b, int dt, float* y) {
+  switch (type) {
+    case GG_F32: { /* :222-223, then .to(dtype) at :328-330 */
+      float v;
+      memcpy(&v, b, 4);
+      y[0] = round_dt(dt, v);
+      break;
+    }
+    case GG_F16: y[0] = round_dt(dt, gg_f16(b)); break;                               /* :218-219 */
+    case GG_BF16: y[0] = round_dt(dt, bf16_to_f32((uint16_t)(b[0] | (b[1] << 8)))); break; /* :214-215 */
+    case GG_Q8_0: { /* :57-61 */
+      const float d = round_dt(dt, gg_f16(b));
+      for (int e = 0; e < 32; ++e) y[e] = round_dt(dt, d * (float)(int8_t)b[2 + e]);
+      break;
+    }
+    case GG_Q4_0:   /* :107-115: element e < 16 is the low nibble of qs[e], e >= 16 the high nibble of qs[e-16] */
+    case GG_IQ4_NL: { /* :226-242: the same nibbles index the IQ4_NL table */
+      const float d = round_dt(dt, gg_f16(b));
+      for (int e = 0; e < 32; ++e) {
+        const int nib = (b[2 + (e & 15)] >> (e < 16 ? 0 : 4)) & 15;
+        y[e] = round_dt(dt, d * (float)(type == GG_Q4_0 ? nib - 8 : kIQ4NL[nib]));
+      }
+      break;
+    }
+    case GG_Q4_1: { /* :95-104: (d * q) + m */
+      const float d = round_dt(dt, gg_f16(b)), m = round_dt(dt, gg_f16(b + 2));
+      for (int e = 0; e < 32; ++e) {
+        const int nib = (b[4 + (e & 15)] >> (e < 16 ? 0 : 4)) & 15;
+        y[e] = round_dt(dt, round_dt(dt, d * (float)nib) + m);
+      }
+      break;
+    }
+    case GG_Q5_0:   /* :80-92: bit e of the little-endian qh word is bit 4 of element e; q - 16 */
+    case GG_Q5_1: { /* :64-77: (d * q) + m */
+      const int q1 = type == GG_Q5_1;
+      const float d = round_dt(dt, gg_f16(b)), m = q1 ? round_dt(dt, gg_f16(b + 2)) : 0.0f;
+      const uint8_t* qhp = b + (q1 ? 4 : 2);
+      const uint8_t* qs = b + (q1 ? 8 : 6);
+      const uint32_t qh = (uint32_t)qhp[0] | ((uint32_t)qhp[1] << 8) | ((uint32_t)qhp[2] << 16) | ((uint32_t)qhp[3] << 24);
+      for (int e = 0; e < 32; ++e) {
+        const int q = ((qs[e & 15] >> (e < 16 ? 0 : 4)) & 15) | (int)(((qh >> e) & 1u) << 4);
+        y[e] = q1 ? round_dt(dt, round_dt(dt, d * (float)q) + m) : round_dt(dt, d * (float)(q - 16));
+      }
+      break;
+    }
+    case GG_Q2_K: { /* :200-211: scales[16] | qs[64] | d | dmin; dl*q - ml per 16 elements */
+      const float d = round_dt(dt, gg_f16(b + 80)), dmin = round_dt(dt, gg_f16(b + 82));
+      for (int e = 0; e < 256; ++e) {
+        const int sc = b[e >> 4];
+        const float dl = round_dt(dt, d * (float)(sc & 15)), ml = round_dt(dt, dmin * (float)(sc >> 4));
+        const int q = (b[16 + 32 * (e >> 7) + (e & 31)] >> (2 * ((e & 127) >> 5))) & 3;
+        y[e] = round_dt(dt, round_dt(dt, dl * (float)q) - ml);
+      }
+      break;
+    }
+    case GG_Q3_K: { /* :172-197: hmask[32] | qs[64] | scales[12] | d */
+      const float d = round_dt(dt, gg_f16(b + 108));
+      const uint8_t *hm = b, *qs = b + 32, *sc = b + 96;
+      for (int e = 0; e < 256; ++e) {
+        const int i = e >> 4;
+        const int lo = i < 8 ? (sc[i] & 15) : (sc[i - 8] >> 4);
+        const int hi = (sc[8 + (i & 3)] >> (2 * (i >> 2))) & 3;
+        const float dl = round_dt(dt, d * (float)((lo | (hi << 4)) - 32));
+        const int ql = (qs[32 * (e >> 7) + (e & 31)] >> (2 * ((e & 127) >> 5))) & 3;
+        const int hbit = (hm[e & 31] >> (e >> 5)) & 1;
+        y[e] = round_dt(dt, dl * (float)(ql - (hbit ? 0 : 4)));
+      }
+      break;
+    }
+    case GG_Q4_K:   /* :157-169: d | dmin | scales[12] | qs[128] */
+    case GG_Q5_K: { /* :137-154: d | dmin | scales[12] | qh[32] | qs[128] */
+      const int q5 = type == GG_Q5_K;
+      const float d = round_dt(dt, gg_f16(b)), dmin = round_dt(dt, gg_f16(b + 2));
+      const uint8_t* qh = b + 16;
+      const uint8_t* qs = b + (q5 ? 48 : 16);
+      for (int e = 0; e < 256; ++e) {
+        const int j = e >> 5;
+        int sc, mn;
+        gg_scale_min(b + 4, j, &sc, &mn);
+        const float ds = round_dt(dt, d * (float)sc), dm = round_dt(dt, dmin * (float)mn);
+        int q = (qs[32 * (j >> 1) + (e & 31)] >> (4 * (j & 1))) & 15;
+        if (q5) q |= ((qh[e & 31] >> j) & 1) << 4;
+        y[e] = round_dt(dt, round_dt(dt, ds * (float)q) - dm);
+      }
+      break;
+    }
+    case GG_Q6_K: { /* :118-134: ql[128] | qh[64] | scales[16] (int8) | d */
+      const float d = round_dt(dt, gg_f16(b + 208));
+      for (int e = 0; e < 256; ++e) {
+        const int h = e >> 7, r = e & 127;
+        const float ds = round_dt(dt, d * (float)(int8_t)b[192 + (e >> 4)]);
+        const int lo = (b[64 * h + (r & 63)] >> (4 * (r >> 6))) & 15;
+        const int hi = (b[128 + 32 * h + (r & 31)] >> (2 * (r >> 5))) & 3;
+        y[e] = round_dt(dt, ds * (float)((lo | (hi << 4)) - 32));
+      }
+      break;
+    }
+    case GG_IQ4_XS: { /* :245-274: d | scales_h (u16) | scales_l[4] | qs[128] */
+      const float d = round_dt(dt, gg_f16(b));
+      const int sh = b[2] | (b[3] << 8);
+      for (int e = 0; e < 256; ++e) {
+        const int j = e >> 5, p = e & 31;
+        const int ls = (((b[4 + (j >> 1)] >> (4 * (j & 1))) & 15) | (((sh >> (2 * j)) & 3) << 4)) - 32;
+        const float dl = round_dt(dt, d * (float)ls);
+        const int nib = (b[8 + 16 * j + (p & 15)] >> (p < 16 ? 0 : 4)) & 15;
+        y[e] = round_dt(dt, dl * (float)kIQ4NL[nib]);
+      }
+      break;
+    }
+  }
+}
+
+/* P/gguf_dequant.py:303-331 over `nblocks` consecutive blocks; returns 0 for
+ * a type the reference does not dispatch */
+EXPORT int lmo_gguf_dequant(const uint8_t* packed, int type, int64_t nblocks, int dt, void* out) {
+  int bs, ts;
+  if (!lmo_gguf_sizes(type, &bs, &ts)) return 0;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < nblocks; ++i) {
+    float y[256];
+    gg_block(type, packed + i * ts, dt, y);
+    for (int e = 0; e < bs; ++e) store_dt(dt, out, i * bs + e, y[e]);
+  }
+  return 1;
+}
+
 EXPORT void lmo_f32_to_bf16(const float* x, uint16_t* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = bf16_bits(x[i]);
 }

@@ -37,12 +37,27 @@ extern "C" int lm_q8_0_requant(const void* dense, int32_t dense_dtype, uint8_t* 
   a.q_out = packed_out;
   return run_blocks<B_Q8_0, P_FULL>(a, dense_dtype, 0, is_sr(rounding), true, c.st);
 }
+bool gguf_block_sizes(int type, int* bs, int* ts);                                       // lm_gguf.hip
+int gguf_dequant_run(const uint8_t* src, int type, int64_t nelem, void* out, int dt, hipStream_t st);  // lm_gguf.hip
+
 extern "C" int lm_gguf_dequant(const uint8_t* packed, int32_t quant_type, int64_t rows, int64_t cols, const lm_lora* lora,
                                void* out, int32_t out_dtype, void* workspace, size_t workspace_bytes, void* stream) {
-  int rc;
+  int rc, bs, ts;
+  if (!gguf_block_sizes(quant_type, &bs, &ts))
+    return fail(LM_EUNSUPPORTED, "Unsupported GGUF quant type: %d", quant_type);
+  if (out_dtype != LM_BF16 && out_dtype != LM_F16 && out_dtype != LM_F32)
+    return fail(LM_EINVAL, "GGUF dequant output dtype must be bf16, f16 or f32");
+  if (rows < 0 || cols < 0) return fail(LM_EINVAL, "GGUF dequant shape must be non-negative");
+  if (cols % bs != 0)
+    return fail(LM_EINVAL, "GGUF type %d needs logical columns divisible by %d, got %lld", quant_type, bs, (long long)cols);
+  if (rows == 0 || cols == 0) return LM_OK;
   if (!packed || !out) return fail(LM_EINVAL, "GGUF dequant pointers must be non-null");
-  if (quant_type != LM_GGUF_Q8_0)
-    return fail(LM_EUNSUPPORTED, "GGUF quant type %d has no HIP dequant kernel yet (Q8_0 only)", quant_type);
+  if (!lora) {
+    if (((uintptr_t)out & 15) != 0) return fail(LM_EINVAL, "GGUF dequant output must be 16-byte aligned");
+    return gguf_dequant_run(packed, quant_type, rows * cols, out, out_dtype, (hipStream_t)stream);
+  }
+  // dequantize with a LoRA delta added: Q8_0 only (the merge extension's format)
+  if (quant_type != LM_GGUF_Q8_0) return fail(LM_EUNSUPPORTED, "GGUF dequant with LoRA factors supports Q8_0 only");
   if ((rc = check_q8(rows, cols))) return rc;
   if ((rc = check_lora(lora, rows, cols))) return rc;
   Ctx c;
@@ -51,7 +66,5 @@ extern "C" int lm_gguf_dequant(const uint8_t* packed, int32_t quant_type, int64_
   a.q = packed;
   a.out = out;
   a.out_dt = out_dtype;
-  const int cd = lora ? lora->dtype : LM_BF16;
-  return run_blocks<B_Q8_0, P_TODENSE>(a, cd, c.nkc, false, false, c.st);
+  return run_blocks<B_Q8_0, P_TODENSE>(a, lora->dtype, c.nkc, false, false, c.st);
 }
-

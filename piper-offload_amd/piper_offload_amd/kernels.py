@@ -11,7 +11,7 @@ the C ABI:
 * :func:`merge_mx_lora_`    <- P/_triton_mx_lora.py:333-425
 * :func:`merge_q8_0_lora`   -- GGUF Q8_0 merge (no reference counterpart)
 * :func:`merge_dense_lora_` <- RegularAdapter.merge_lora_ (P/tensor_adapters.py:686-696)
-* :func:`dequantize_gguf`   <- P/gguf_dequant.py:303-331 (Q8_0 on the GPU)
+* :func:`dequantize_gguf`   <- P/gguf_dequant.py:303-331 (all 15 dispatched types)
 
 The ``*_into`` variants write into caller-provided (possibly aliasing)
 outputs; the adapters use them to merge in place without a copy.
@@ -20,6 +20,7 @@ outputs; the adapters use them to merge in place without a copy.
 from __future__ import annotations
 
 import ctypes
+import math
 
 import torch
 
@@ -27,6 +28,7 @@ from . import _lib as L
 
 __all__ = [
     "dequantize_float8",
+    "GGUF_DEQUANT_TYPES",
     "dequantize_gguf",
     "dequantize_int8",
     "dequantize_mx",
@@ -517,26 +519,54 @@ def requantize_q8_0(dense: torch.Tensor, *, rounding_seed: int | None = None) ->
     return out
 
 
+# block elements and bytes of every type P/gguf_dequant.py:278-294 dispatches
+# (ggml block structs; keys are gguf.GGMLQuantizationType values)
+GGUF_DEQUANT_TYPES: dict[int, tuple[int, int]] = {
+    0: (1, 4), 1: (1, 2), 30: (1, 2),                      # F32, F16, BF16
+    2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24),    # Q4_0, Q4_1, Q5_0, Q5_1
+    8: (32, 34), 20: (32, 18),                             # Q8_0, IQ4_NL
+    10: (256, 84), 11: (256, 110), 12: (256, 144),         # Q2_K, Q3_K, Q4_K
+    13: (256, 176), 14: (256, 210), 23: (256, 136),        # Q5_K, Q6_K, IQ4_XS
+}
+_GGUF_OUT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
 def dequantize_gguf(data: torch.Tensor, quant_type: int, *, dtype: torch.dtype = torch.bfloat16,
                     lora: tuple[torch.Tensor, torch.Tensor, float] | None = None) -> torch.Tensor:
-    """GGUF dequantize on the GPU (P/gguf_dequant.py:303-331); Q8_0 is implemented."""
-    if quant_type != GGML_Q8_0:
-        raise NotImplementedError(f"Unsupported GGUF quant type for the HIP path: {quant_type!r}")
+    """GGUF dequantize on the GPU (P/gguf_dequant.py:303-331) for every type
+    the reference dispatches; ``lora`` (Q8_0 only) adds strength*B@A."""
+    sizes = GGUF_DEQUANT_TYPES.get(int(quant_type))
+    if sizes is None:
+        raise NotImplementedError(f"Unsupported GGUF quant type: {quant_type!r}")
+    if dtype not in _GGUF_OUT_DTYPES:
+        raise ValueError(f"HIP GGUF dequant computes in bf16, fp16 or fp32, not {dtype}.")
+    block, nbytes = sizes
     device = _same_device("GGUF", data)
+    if data.ndim == 0:
+        raise ValueError("GGUF data must have at least one dimension.")
+    shape = (*data.shape[:-1], data.shape[-1] // nbytes * block)  # P/gguf_dequant.py:297-300 on data.shape
     raw = data.view(torch.uint8)
-    shape = q8_0_logical_shape(tuple(raw.shape))
-    cols = shape[-1]
-    rows = raw.numel() // (cols // _Q8_0_BLOCK * _Q8_0_BYTES)
+    if raw.shape[-1] % nbytes != 0:
+        raise ValueError(f"GGUF rows must hold whole {nbytes}-byte blocks of type {quant_type}.")
     raw = raw.contiguous()
-    out = torch.empty((rows, cols), device=device, dtype=dtype)
+    elements = raw.numel() // nbytes * block
+    if math.prod(shape) != elements:
+        raise ValueError(f"GGUF bytes of shape {tuple(data.shape)} do not give a tensor of shape {shape}.")
+    out = torch.empty(shape, device=device, dtype=dtype)
+    if elements == 0:
+        return out
+    cols = shape[-1]
+    rows = elements // cols
     lora_s, rank = None, 0
     if lora is not None:
+        if int(quant_type) != GGML_Q8_0:
+            raise ValueError("GGUF dequant with LoRA factors supports Q8_0 only.")
         b, a = _factors(lora[0], lora[1], rows, cols, "GGUF")
         lora_s, rank = L.lora_struct(b, a, lora[2]), a.shape[0]
-    ws_bytes = L.load_library().lm_workspace_size(rows, cols, rank)
+    ws_bytes = L.load_library().lm_workspace_size(rows, cols, rank) if lora is not None else 0
     _run("lm_gguf_dequant", device, ws_bytes, _ptr(raw), int(quant_type), rows, cols,
          None if lora_s is None else ctypes.byref(lora_s), _ptr(out), L.torch_dtype_id(dtype))
-    return out.reshape(shape)
+    return out
 
 
 # ---------------------------------------------------------------------------

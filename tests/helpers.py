@@ -91,3 +91,43 @@ def assert_merged_close(got: np.ndarray, ref: np.ndarray, base: np.ndarray) -> N
     bad = (ulp > 1) & (np.abs(g - r) > tol)
     assert not bad.any(), f"{int(bad.sum())} merged values outside tolerance, first at {np.argwhere(bad)[0]}"
     assert (ulp > 0).mean() <= MERGED_MISMATCH_FRACTION
+
+
+# byte offsets of the fp16 fields (d, dmin / m) in each GGUF block struct
+GGUF_F16_FIELDS = {2: (0,), 3: (0, 2), 6: (0,), 7: (0, 2), 8: (0,), 20: (0,), 10: (80, 82), 11: (108,),
+                   12: (0, 2), 13: (0, 2), 14: (208,), 23: (0,)}
+
+
+def random_f16_bits(n: int, rng: np.random.Generator, *, with_inf: bool = False) -> np.ndarray:
+    """Finite fp16 bit patterns spread over the whole range: signs, subnormals, zeros, up to 65504."""
+    mag = np.exp2(rng.uniform(-25.0, 16.0, n)) * rng.uniform(1.0, 2.0, n)
+    v = np.minimum(mag, 65504.0).astype(np.float16) * rng.choice(np.array([-1, 1], np.float16), n)
+    bits = v.view(np.uint16).copy()
+    bits[rng.random(n) < 0.03] = 0
+    bits[rng.random(n) < 0.03] = 0x8000
+    if with_inf:
+        bits[rng.random(n) < 0.01] = 0x7C00
+    return bits
+
+
+def gguf_blocks(quant_type: int, nblocks: int, seed: int) -> np.ndarray:
+    """`nblocks` random GGUF blocks of one type as flat bytes; fp16 fields hold finite values
+    (the float types: finite values of every magnitude, fp32 subnormals included)."""
+    rng = np.random.default_rng(seed)
+    bs, ts = O.gguf_sizes(quant_type)
+    if quant_type == 1:
+        return random_f16_bits(nblocks, rng, with_inf=True).view(np.uint8).copy()
+    if quant_type == 30:
+        h = rng.integers(0, 1 << 16, nblocks, dtype=np.uint32).astype(np.uint16)
+        nan = ((h & 0x7F80) == 0x7F80) & ((h & 0x7F) != 0)
+        h[nan] &= 0xFF80  # NaN -> inf of the same sign
+        return h.view(np.uint8).copy()
+    if quant_type == 0:
+        u = rng.integers(0, 1 << 32, nblocks, dtype=np.uint64).astype(np.uint32)
+        nan = ((u & 0x7F800000) == 0x7F800000) & ((u & 0x7FFFFF) != 0)
+        u[nan] &= 0xFF800000
+        return u.view(np.uint8).copy()
+    raw = rng.integers(0, 256, (nblocks, ts), dtype=np.uint8)
+    for off in GGUF_F16_FIELDS[quant_type]:
+        raw[:, off:off + 2] = random_f16_bits(nblocks, rng).view(np.uint8).reshape(nblocks, 2)
+    return raw.reshape(-1)
