@@ -223,6 +223,14 @@ static inline int sr_int(float x, int det, float u, int qmin, int qmax) {
   float rounded = lower + ((u < p) ? 1.0f : 0.0f);
   return (interior && p > 0.0f) ? (int)rounded : det;
 }
+/* The up-probability p = (|x| - lo) / (hi - lo) of the 4- and 8-bit float
+ * formats is exact in fp32 (the grid steps are powers of two).  It is used
+ * truncated to W fraction bits, W = 23 - (target mantissa bits): 22 for e2m1,
+ * 20 for e4m3, 21 for e5m2.  That is the precision of gfx950's stochastic
+ * conversions (v_cvt_scalef32_sr_*), which the GPU kernels use; it changes p
+ * only below 2^-W, i.e. in the formats' subnormal range. */
+static inline float sr_trunc(float p, int w) { return ldexpf(floorf(ldexpf(p, w)), -w); }
+
 /* :110-130 */
 static inline uint8_t sr_e2m1(float v, uint8_t det, float u) {
   float mag = fabsf(v);
@@ -232,7 +240,7 @@ static inline uint8_t sr_e2m1(float v, uint8_t det, float u) {
   int lo = rd ? nc - 1 : nc, hi = rd ? nc : nc + 1;
   float lov = kE2M1[lo & 7], hiv = kE2M1[hi & 7];
   float p = (hiv > lov) ? (mag - lov) / (hiv - lov) : 0.0f;
-  int mc = (u < p) ? hi : lo;
+  int mc = (u < sr_trunc(p, 22)) ? hi : lo;
   int sign = (int)((f2u(v) >> 28) & 8);
   uint8_t chosen = (uint8_t)(mc | sign);
   int interior = (mag > 0.0f) && (mag < 6.0f) && (p > 0.0f);
@@ -247,7 +255,7 @@ static inline uint8_t sr_fp8(int fmt, float v, float u, float limit) {
   uint8_t lo = rd ? (uint8_t)(det - 1) : det, hi = rd ? det : (uint8_t)(det + 1);
   float lov = fp8_decode(fmt, lo), hiv = fp8_decode(fmt, hi);
   float p = (hiv > lov) ? (mag - lov) / (hiv - lov) : 0.0f;
-  uint8_t mb = (u < p) ? hi : lo;
+  uint8_t mb = (u < sr_trunc(p, fmt == DT_E4M3 ? 20 : 21)) ? hi : lo;
   uint8_t sign = (uint8_t)((f2u(v) >> 24) & 0x80);
   int interior = (mag < limit) && (p > 0.0f);
   return interior ? (uint8_t)(mb | sign) : (uint8_t)(det | sign);

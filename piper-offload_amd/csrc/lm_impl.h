@@ -506,8 +506,9 @@ __global__ __launch_bounds__(NW * 64) void k_rows_stack(const RowStackItem* __re
 // N % 64 == 0, INT8 symmetric with fp32 scales or scaled FP8 (fp32 scales).
 // Merged values stay packed bf16 (v_cvt_pk_bf16_f32) from pass 1 to pass 2,
 // the row amax is a packed 16-bit max over |bits|, round-to-nearest uses the
-// 1.5*2^23 magic add, and stochastic rounding uses sr_grid (an exact
-// reformulation of the reference's u < p selection).
+// 1.5*2^23 magic add, INT8 stochastic rounding works on the integer grid (an
+// exact reformulation of the reference's u < p selection) and FP8 stochastic
+// rounding uses the hardware conversions (sr_fp8_word).
 // Global inputs of one 64-column macro tile for one lane: 16 codes of its row
 // and the 4 A^T operands of its MFMAs.  Loading is split from the arithmetic
 // so that a wave can have several tiles' loads in flight.
@@ -610,22 +611,13 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, int64_t row, 
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
-      float v = __builtin_amdgcn_fmed3f(div_rn(m, qp.s, qp.rcp), -L, L);
-      if constexpr (SR) {
-        // grid spacing of the fp8 value: 2^(E - mbits), at least the subnormal step
-        constexpr int MB = F == E4M3 ? 3 : 2;
-        constexpr int MINE = F == E4M3 ? -9 : -16;
-        const uint32_t h = (j & 1) ? (rw[j >> 1] >> 16) : (rw[j >> 1] & 0xffffu);
-        const float mag = __builtin_fabsf(v);
-        int e = (int)((f2u(mag) >> 23) & 255u) - 127 - MB;
-        e = e < MINE ? MINE : e;
-        const int q = sr_grid(__builtin_ldexpf(mag, 16 - e), h);
-        v = __builtin_copysignf(__builtin_ldexpf((float)q, e), v);
-      }
-      x[j] = v;
+      x[j] = __builtin_amdgcn_fmed3f(div_rn(m, qp.s, qp.rcp), -L, L);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = fp8_pack4<F>(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (SR) out[i] = sr_fp8_word<F>(x + 4 * i, rw + 2 * i);
+      else out[i] = fp8_pack4<F>(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+    }
   }
   *(uint4*)((uint8_t*)a.q_out + row * N + c0) = make_uint4(out[0], out[1], out[2], out[3]);
 }

@@ -15,7 +15,8 @@
 //            elements can fall below bf16's subnormal range and keep the
 //            rounding;
 //   merged = bf16(fma(delta, strength, base));
-//   scale  = mx_scale(max |merged|, mode); codes = enc(clamp(merged * 1/scale)).
+//   scale  = mx_scale(max |merged|, mode); codes = enc(clamp(merged * 1/scale)),
+//   stochastic codes by the hardware conversions (lm_device.h).
 #pragma once
 #include "lm_nvfp4_fast.h"
 
@@ -127,44 +128,32 @@ DEV void mx_tile(const MxArgs& a, const MxTileIn<ELEM, NKC>& in, const v4i16 (&b
   float x[32];
 #pragma unroll
   for (int j = 0; j < 32; ++j) {
-    float v = m[j] * inv;
-    if constexpr (SR) {
-      v = __builtin_amdgcn_fmed3f(v, -L, L);
-      const uint32_t nw = ~rw[j >> 1];
-      const uint32_t nh = (j & 1) ? (nw >> 16) : (nw & 0xffffu);
-      if constexpr (ELEM == E2M1) {
-        v = nv_sr_value(v, nh);
-      } else {
-        // grid spacing of the fp8 value: 2^(E - mbits), at least the subnormal step
-        constexpr int MB = ELEM == E4M3 ? 3 : 2;
-        constexpr int MINE = ELEM == E4M3 ? -9 : -16;
-        const float mag = __builtin_fabsf(v);
-        int e = (int)((f2u(mag) >> 23) & 255u) - 127 - MB;
-        e = e < MINE ? MINE : e;
-        const int qv = (int)(nh - (uint32_t)cvt_flr_neg(__builtin_ldexpf(mag, 16 - e))) >> 16;
-        v = __builtin_copysignf(__builtin_ldexpf((float)qv, e), v);
-      }
-    } else if constexpr (ELEM != E2M1) {
-      v = __builtin_amdgcn_fmed3f(v, -L, L);  // the e2m1 conversion saturates by itself
-    }
-    x[j] = v;
+    // the e2m1 conversions saturate by themselves; fp8 ones need the clamp
+    x[j] = ELEM == E2M1 ? m[j] * inv : __builtin_amdgcn_fmed3f(m[j] * inv, -L, L);
   }
   if constexpr (ELEM == E2M1) {
     uint32_t words[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      uint32_t wd = 0u;
-      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 0], x[8 * k + 1], 1.0f, 0);
-      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 2], x[8 * k + 3], 1.0f, 1);
-      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 4], x[8 * k + 5], 1.0f, 2);
-      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 6], x[8 * k + 7], 1.0f, 3);
-      words[k] = wd;
+      if constexpr (SR) {
+        words[k] = sr_e2m1_word(x + 8 * k, rw + 4 * k);
+      } else {
+        uint32_t wd = 0u;
+        wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 0], x[8 * k + 1], 1.0f, 0);
+        wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 2], x[8 * k + 3], 1.0f, 1);
+        wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 4], x[8 * k + 5], 1.0f, 2);
+        wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 6], x[8 * k + 7], 1.0f, 3);
+        words[k] = wd;
+      }
     }
     *(uint4*)(qo + (int64_t)mt * 64) = make_uint4(words[0], words[1], words[2], words[3]);
   } else {
     uint32_t wv[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) wv[i] = fp8_pack4<ELEM>(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (SR) wv[i] = sr_fp8_word<ELEM>(x + 4 * i, rw + 2 * i);
+      else wv[i] = fp8_pack4<ELEM>(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+    }
     uint4* dst = (uint4*)(qo + (int64_t)mt * 128);
     dst[0] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
     dst[1] = make_uint4(wv[4], wv[5], wv[6], wv[7]);

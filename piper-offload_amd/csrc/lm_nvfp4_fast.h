@@ -157,22 +157,6 @@ DEV void nv_merged(const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float stren
   }
 }
 
-// Stochastic e2m1 code of a clamped value v (|v| <= 6) with nh = 65535 - h,
-// h the 16 random bits: the grid step below 2 is 0.5, then 1, then 2, so
-// with e the step's exponent, Y = |v| * 2^(16-e) is exact and
-// q = (ceil(Y) + 65535 - h) >> 16 is floor(|v|/2^e) + [h * 2^-16 < frac];
-// exact and saturated values keep their code
-// (P/_triton_stochastic_quantization.py:110-130).
-DEV float nv_sr_value(float v, uint32_t nh) {
-  const float mag = __builtin_fabsf(v);
-  int ex = __builtin_amdgcn_frexp_expf(mag);  // floor(log2 mag) + 1 (0 for 0)
-  ex = ex < 1 ? 1 : (ex > 3 ? 3 : ex);        // e = ex - 2 in {-1, 0, 1}
-  const float y = __builtin_ldexpf(mag, 18 - ex);
-  const int tneg = (int)__builtin_floorf(-y);
-  const int q = (int)(nh - (uint32_t)tneg) >> 16;
-  return __builtin_copysignf(__builtin_ldexpf((float)q, ex - 2), v);
-}
-
 // RN(a / b) from y = RN(1 / b): q0 = RN(a y), r = a - b q0 (exact by fma),
 // RN(q0 + r y).  Correctly rounded when a, b and the quotient are normal
 // with room for the residual (Markstein); checked against IEEE division on
@@ -214,24 +198,21 @@ DEV void nv_quant_store(const NvArgs& a, int64_t row, int mt, int lane, float gq
     const float recip = TWO ? div_markstein(inv_g, fs, rfs) : 0.0f;
     float x[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      float v = TWO ? mb[j] * recip : div_rn(mb[j], fs, rfs);
-      if constexpr (SR) {
-        const uint32_t nw = ~rw[(16 * b + j) >> 1];
-        const uint32_t nh = (j & 1) ? (nw >> 16) : (nw & 0xffffu);
-        v = nv_sr_value(__builtin_amdgcn_fmed3f(v, -6.0f, 6.0f), nh);
-      }
-      x[j] = v;  // the e2m1 conversion saturates to +-6 (checked on gfx950)
-    }
-    // dst_sel k writes byte k and keeps the others (checked on gfx950)
+    for (int j = 0; j < 16; ++j) x[j] = TWO ? mb[j] * recip : div_rn(mb[j], fs, rfs);
+    // the e2m1 conversions saturate to +-6 (checked on gfx950)
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      uint32_t wd = 0u;
-      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 0], x[8 * k + 1], 1.0f, 0);
-      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 2], x[8 * k + 3], 1.0f, 1);
-      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 4], x[8 * k + 5], 1.0f, 2);
-      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 6], x[8 * k + 7], 1.0f, 3);
-      words[2 * b + k] = wd;
+      if constexpr (SR) {
+        words[2 * b + k] = sr_e2m1_word(x + 8 * k, rw + 8 * b + 4 * k);
+      } else {
+        // dst_sel k writes byte k and keeps the others (checked on gfx950)
+        uint32_t wd = 0u;
+        wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 0], x[8 * k + 1], 1.0f, 0);
+        wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 2], x[8 * k + 3], 1.0f, 1);
+        wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 4], x[8 * k + 5], 1.0f, 2);
+        wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 6], x[8 * k + 7], 1.0f, 3);
+        words[2 * b + k] = wd;
+      }
     }
   }
   *(uint4*)(qo + (int64_t)mt * 64) = make_uint4(words[0], words[1], words[2], words[3]);
