@@ -101,10 +101,10 @@ DEV void nv_load_tile(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
   for (int k = 0; k < 8; ++k) load_kchunks<NKC>(at + 4 * k * RPAD, t.aop[k]);
 }
 
-// merged values of the lane's 32 columns; ZFIX applies the reference's
-// "update == 0 keeps the base" rule (P/_triton_nvfp4_lora.py:183-186), which
-// only changes the sign of a zero and so is not needed for max |merged|.
-template <int NKC, bool TWO, bool ZFIX>
+// merged values of the lane's 32 columns, for max |merged| (the reference's
+// "update == 0 keeps the base" rule only changes the sign of a zero, so the
+// amax pass does not need it)
+template <int NKC, bool TWO>
 DEV void nv_merged(const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float strength, float gin, float (&m)[32]) {
   float d[32];
 #pragma unroll
@@ -122,37 +122,56 @@ DEV void nv_merged(const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float stren
     bs[b] = TWO ? bf16r(v * gin) : v;
   }
   const uint32_t w[4] = {in.codes.x, in.codes.y, in.codes.z, in.codes.w};
-  bool zfix = false;
-  if constexpr (ZFIX) {
-    // The rule can only matter where d * strength == 0; every such product is
-    // bounded below by min|d| * |strength|, so lanes with a non-zero bound
-    // skip it (a zero LoRA row, an exact cancellation or an underflow takes
-    // the exact per-element path).
-    float dmin = __builtin_fabsf(d[0]);
 #pragma unroll
-    for (int j = 1; j < 32; ++j) dmin = __builtin_fminf(dmin, __builtin_fabsf(d[j]));
-    zfix = dmin * __builtin_fabsf(strength) == 0.0f;
+  for (int q = 0; q < 16; ++q) {
+    const v2f32 pr = e2m1_pair(w[q >> 2], q & 3);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) m[2 * q + e] = __builtin_fmaf(d[2 * q + e], strength, bf16r(pr[e] * bs[q >> 3]));
   }
-  if (zfix) {
+}
+
+// Merged values of block B (the lane's columns 16B .. 16B+15) of a tile: the
+// same arithmetic as nv_merged, one 16-element block at a time so that the
+// quantizer keeps half as many values live.
+template <int NKC, bool TWO, int B>
+DEV void nv_merged_block(const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float strength, float gin,
+                         float (&m)[16]) {
+  float d[16];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
+  for (int k = 0; k < 4; ++k) {
+    const v4f32 acc = mfma_chain<NKC, false>(in.aop[4 * B + k], bop);
+    d[4 * k + 0] = acc[0];
+    d[4 * k + 1] = acc[1];
+    d[4 * k + 2] = acc[2];
+    d[4 * k + 3] = acc[3];
+  }
+  const float v = fp8_decode<E4M3>(in.sc, B);  // e4m3 is exact in bf16
+  const float bs = TWO ? bf16r(v * gin) : v;
+  const uint32_t w[2] = {B == 0 ? in.codes.x : in.codes.z, B == 0 ? in.codes.y : in.codes.w};
+  // "update == 0 keeps the base" (P/_triton_nvfp4_lora.py:183-186) can only
+  // matter where d * strength == 0; every such product is bounded below by
+  // min|d| * |strength|, so a block with a non-zero bound skips it (a zero
+  // LoRA row, an exact cancellation or an underflow takes the exact path).
+  float dmin = __builtin_fabsf(d[0]);
+#pragma unroll
+  for (int j = 1; j < 16; ++j) dmin = __builtin_fminf(dmin, __builtin_fabsf(d[j]));
+  if (dmin * __builtin_fabsf(strength) == 0.0f) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
       const v2f32 pr = e2m1_pair(w[q >> 2], q & 3);
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int j = 2 * q + e;
-        const float base = bf16r(pr[e] * bs[j >> 4]);
+        const float base = bf16r(pr[e] * bs);
         m[j] = (d[j] * strength == 0.0f) ? base : __builtin_fmaf(d[j], strength, base);
       }
     }
   } else {
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
+    for (int q = 0; q < 8; ++q) {
       const v2f32 pr = e2m1_pair(w[q >> 2], q & 3);
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int j = 2 * q + e;
-        m[j] = __builtin_fmaf(d[j], strength, bf16r(pr[e] * bs[j >> 4]));
-      }
+      for (int e = 0; e < 2; ++e) m[2 * q + e] = __builtin_fmaf(d[2 * q + e], strength, bf16r(pr[e] * bs));
     }
   }
 }
@@ -170,50 +189,68 @@ DEV float div_markstein(float a, float b, float y) {
 static __device__ __constant__ const float kRcpE4M3[8] = {1.0f / 1.0f, 1.0f / 1.125f, 1.0f / 1.25f, 1.0f / 1.375f,
                                                    1.0f / 1.5f, 1.0f / 1.625f, 1.0f / 1.75f, 1.0f / 1.875f};
 
+// Quantize block B of a tile into two code words and one scale byte
+// (P/_triton_nvfp4_lora.py:316-366).
+template <bool TWO, bool SR, int B>
+DEV void nv_quant_block(const NvArgs& a, int64_t row, int mt, int lane, float gq, float inv_g, const float* rtab,
+                        const float (&m)[16], uint32_t (&words)[4], uint32_t& scb) {
+  uint32_t rw[8];
+  if constexpr (SR)
+    sr_words_aligned<16>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4) + 16 * B), rw);
+  float mb[16];
+  float bmax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    mb[j] = bf16r(m[j]);
+    bmax = __builtin_fmaxf(bmax, __builtin_fabsf(mb[j]));
+  }
+  // bmax is a bf16 value and 6 is exact in bf16: div_rn is the IEEE quotient
+  float fs = div_rn(bmax, 6.0f, 1.0f / 6.0f);
+  if constexpr (TWO) fs = div_markstein(fs, gq, inv_g);
+  fs = __builtin_fminf(__builtin_fmaxf(fs, 0.015625f), 448.0f);
+  const uint32_t s8 = fp8_encode1<E4M3>(fs);
+  fs = fp8_value<E4M3>(s8);
+  scb |= s8 << (8 * B);
+  const uint32_t fb = f2u(fs);
+  const float rfs = __builtin_ldexpf(rtab[(fb >> 20) & 7u], 127 - (int)((fb >> 23) & 255u));  // RN(1/fs)
+  const float recip = TWO ? div_markstein(inv_g, fs, rfs) : 0.0f;
+  float x[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) x[j] = TWO ? mb[j] * recip : div_rn(mb[j], fs, rfs);
+  // the e2m1 conversions saturate to +-6 (checked on gfx950)
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if constexpr (SR) {
+      words[2 * B + k] = sr_e2m1_word(x + 8 * k, rw + 4 * k);
+    } else {
+      // dst_sel k writes byte k and keeps the others (checked on gfx950)
+      uint32_t wd = 0u;
+      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 0], x[8 * k + 1], 1.0f, 0);
+      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 2], x[8 * k + 3], 1.0f, 1);
+      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 4], x[8 * k + 5], 1.0f, 2);
+      wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 6], x[8 * k + 7], 1.0f, 3);
+      words[2 * B + k] = wd;
+    }
+  }
+}
+
+// merge + quantize one tile, block by block, then one 16-byte code store and
+// one 2-byte scale store
 template <int NKC, bool TWO, bool SR>
-DEV void nv_quant_store(const NvArgs& a, int64_t row, int mt, int lane, float gq, float inv_g, const float* rtab,
-                        const float (&m)[32], uint8_t* qo, uint8_t* so, int64_t so_stride) {
-  uint32_t rw[16];
-  if constexpr (SR) sr_words_aligned<32>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4)), rw);
-  uint32_t words[4] = {0u, 0u, 0u, 0u};
+DEV void nv_quant_tile(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float gin, int64_t row,
+                       int mt, int lane, float gq, float inv_g, const float* rtab, uint8_t* qo, uint8_t* so,
+                       int64_t so_stride) {
+  uint32_t words[4];
   uint32_t scb = 0;
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    float mb[16];
-    float bmax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      mb[j] = bf16r(m[16 * b + j]);
-      bmax = __builtin_fmaxf(bmax, __builtin_fabsf(mb[j]));
-    }
-    // bmax is a bf16 value and 6 is exact in bf16: div_rn is the IEEE quotient
-    float fs = div_rn(bmax, 6.0f, 1.0f / 6.0f);
-    if constexpr (TWO) fs = div_markstein(fs, gq, inv_g);
-    fs = __builtin_fminf(__builtin_fmaxf(fs, 0.015625f), 448.0f);
-    const uint32_t s8 = fp8_encode1<E4M3>(fs);
-    fs = fp8_value<E4M3>(s8);
-    scb |= s8 << (8 * b);
-    const uint32_t fb = f2u(fs);
-    const float rfs = __builtin_ldexpf(rtab[(fb >> 20) & 7u], 127 - (int)((fb >> 23) & 255u));  // RN(1/fs)
-    const float recip = TWO ? div_markstein(inv_g, fs, rfs) : 0.0f;
-    float x[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) x[j] = TWO ? mb[j] * recip : div_rn(mb[j], fs, rfs);
-    // the e2m1 conversions saturate to +-6 (checked on gfx950)
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      if constexpr (SR) {
-        words[2 * b + k] = sr_e2m1_word(x + 8 * k, rw + 8 * b + 4 * k);
-      } else {
-        // dst_sel k writes byte k and keeps the others (checked on gfx950)
-        uint32_t wd = 0u;
-        wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 0], x[8 * k + 1], 1.0f, 0);
-        wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 2], x[8 * k + 3], 1.0f, 1);
-        wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 4], x[8 * k + 5], 1.0f, 2);
-        wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 6], x[8 * k + 7], 1.0f, 3);
-        words[2 * b + k] = wd;
-      }
-    }
+  {
+    float m[16];
+    nv_merged_block<NKC, TWO, 0>(in, bop, a.strength, gin, m);
+    nv_quant_block<TWO, SR, 0>(a, row, mt, lane, gq, inv_g, rtab, m, words, scb);
+  }
+  {
+    float m[16];
+    nv_merged_block<NKC, TWO, 1>(in, bop, a.strength, gin, m);
+    nv_quant_block<TWO, SR, 1>(a, row, mt, lane, gq, inv_g, rtab, m, words, scb);
   }
   *(uint4*)(qo + (int64_t)mt * 64) = make_uint4(words[0], words[1], words[2], words[3]);
   *(uint16_t*)(so + (int64_t)mt * so_stride) = (uint16_t)scb;
@@ -242,7 +279,7 @@ DEV void nv_amax_body(const NvArgs& a, int64_t row0) {
       NvTileIn<NKC> nxt;
       nv_load_tile<NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
       float m[32];
-      nv_merged<NKC, true, false>(cur, bop, strength, gin, m);
+      nv_merged<NKC, true>(cur, bop, strength, gin, m);
 #pragma unroll
       for (int j = 0; j < 32; ++j) mx = __builtin_fmaxf(mx, __builtin_fabsf(m[j]));
       cur = nxt;
@@ -269,7 +306,6 @@ DEV void nv_quant_body(const NvArgs& a, int64_t row0, const float* rtab) {
   const int64_t rowc = rok ? row : a.M - 1;
   const int ntiles = (int)(a.N >> 7);
   const float gin = TWO ? *a.gin : 1.0f;
-  const float strength = a.strength;
   float gq = 1.0f, inv_g = 1.0f;
   if constexpr (TWO) {
     gq = __builtin_fmaxf(u2f(*a.red) / 2688.0f, kEps);
@@ -286,9 +322,7 @@ DEV void nv_quant_body(const NvArgs& a, int64_t row0, const float* rtab) {
   for (int mt = wave; mt < ntiles; mt += NV_NW) {
     NvTileIn<NKC> nxt;
     nv_load_tile<NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
-    float m[32];
-    nv_merged<NKC, TWO, true>(cur, bop, strength, gin, m);
-    if (rok) nv_quant_store<NKC, TWO, SR>(a, row, mt, lane, gq, inv_g, rtab, m, qo, so, l.sc_stride);
+    if (rok) nv_quant_tile<NKC, TWO, SR>(a, cur, bop, gin, row, mt, lane, gq, inv_g, rtab, qo, so, l.sc_stride);
     cur = nxt;
   }
 }
@@ -311,17 +345,12 @@ template <int NKC>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_amax(NvArgs a) {
   nv_amax_body<NKC>(a, (int64_t)blockIdx.x * 16);
 }
-template <int NKC, bool SR>
-DEV void nv_quant_dispatch(const NvArgs& a, int64_t row0) {
+template <int NKC, bool SR, bool TWO>
+__global__ __launch_bounds__(NV_NW * 64) void k_nv_quant(NvArgs a) {
   __shared__ float rtab[8];
   if (threadIdx.x < 8) rtab[threadIdx.x] = kRcpE4M3[threadIdx.x];
   __syncthreads();
-  if (a.gin != nullptr) nv_quant_body<NKC, true, SR>(a, row0, rtab);
-  else nv_quant_body<NKC, false, SR>(a, row0, rtab);
-}
-template <int NKC, bool SR>
-__global__ __launch_bounds__(NV_NW * 64) void k_nv_quant(NvArgs a) {
-  nv_quant_dispatch<NKC, SR>(a, (int64_t)blockIdx.x * 16);
+  nv_quant_body<NKC, TWO, SR>(a, (int64_t)blockIdx.x * 16, rtab);
 }
 template <int NKC>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_amax_stack(const NvStackItem* __restrict__ items, int count) {
@@ -330,11 +359,14 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_amax_stack(const NvStackItem*
   if (a.gin == nullptr) return;  // single-level item: no global scale to find
   nv_amax_body<NKC>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16);
 }
-template <int NKC, bool SR>
+// TWO: every item of the launch is two-level (the host splits a mixed stack)
+template <int NKC, bool SR, bool TWO>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant_stack(const NvStackItem* __restrict__ items, int count) {
+  __shared__ float rtab[8];
+  if (threadIdx.x < 8) rtab[threadIdx.x] = kRcpE4M3[threadIdx.x];
+  __syncthreads();
   const int i = nv_find(items, count, blockIdx.x);
-  const NvArgs a = items[i].a;
-  nv_quant_dispatch<NKC, SR>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16);
+  nv_quant_body<NKC, TWO, SR>(items[i].a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16, rtab);
 }
 // one thread per item: g = max(amax / 2688, eps)
 static __global__ void k_nv_finalize(const NvStackItem* __restrict__ items, int count) {
@@ -360,11 +392,10 @@ static int nv_fast_run(const NvArgs& a, int nkc, bool sr, hipStream_t st) {
   }
   {
     TimedLaunch timed("nvfp4", st);
-    if (sr) {
-      NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant<NKC_, true>), grid, block, 0, st, a));
-    } else {
-      NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant<NKC_, false>), grid, block, 0, st, a));
-    }
+#define NQ1(SR_, TWO_) NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant<NKC_, SR_, TWO_>), grid, block, 0, st, a))
+    if (a.gin) { if (sr) { NQ1(true, true); } else { NQ1(false, true); } }
+    else { if (sr) { NQ1(true, false); } else { NQ1(false, false); } }
+#undef NQ1
     LAUNCH_CHECK();
   }
   if (a.gin) {

@@ -159,22 +159,28 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
   return rc;
 }
 
-// Grouped NVFP4 merge: one amax launch over every two-level item, one quant
-// launch over all items, one finalize.  `dev_items` is workspace for the
+// Grouped NVFP4 merge: one amax launch over the two-level items, one quant
+// launch per scale level (two-level, single-level), one finalize.  `dev_items` is workspace for the
 // descriptor table (fits in the BlkArgs region of lm_stack_workspace_extra).
 static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swizzled, bool sr, const PrepItem* preps,
                          uint8_t* dev_items, hipStream_t st) {
   static_assert(sizeof(NvStackItem) <= sizeof(BlkArgs), "NVFP4 stack descriptors must fit the workspace slot");
   NvStackItem* h = (NvStackItem*)calloc(count, sizeof(NvStackItem));
   if (!h) return fail(LM_EINVAL, "host allocation failed");
-  int64_t tiles = 0;
-  bool any_two = false;
+  // two-level items first, then single-level ones; each group numbers its
+  // 16-row units from 0 and gets its own quant launch
+  int n_two = 0;
+  for (int i = 0; i < count; ++i) n_two += items[i].aux != nullptr ? 1 : 0;
+  int64_t tiles[2] = {0, 0};
+  int slot[2] = {0, n_two};
   int rc = LM_OK;
   for (int i = 0; i < count && rc == LM_OK; ++i) {
     const lm_stack_item& s = items[i];
     if (!s.q || !s.scale || !s.q_out || !s.scale_out) rc = fail(LM_EINVAL, "stack item %d has a null pointer", i);
     if (s.aux && !s.aux_out) rc = fail(LM_EINVAL, "stack item %d: two-level NVFP4 needs a per-tensor scale output", i);
-    NvArgs& a = h[i].a;
+    const int grp = s.aux != nullptr ? 0 : 1;
+    NvStackItem& it = h[slot[grp]++];
+    NvArgs& a = it.a;
     a.q = (const uint8_t*)s.q;
     a.scale = (const uint8_t*)s.scale;
     a.gin = (const float*)s.aux;
@@ -189,33 +195,39 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
     a.strength = s.lora.strength;
     a.swizzled = swizzled;
     a.seed = s.seed;
-    h[i].tile_begin = tiles;
-    tiles += nv_units(s.M, s.N);
-    any_two = any_two || s.aux != nullptr;
+    it.tile_begin = tiles[grp];
+    tiles[grp] += nv_units(s.M, s.N);
     if (rc == LM_OK && swizzled) rc = zero_swizzle_pad((uint8_t*)s.scale_out, s.M, s.N / 16, st);
   }
   if (rc == LM_OK) rc = lm_stage_h2d(dev_items, h, sizeof(NvStackItem) * count, st);
   const int nkc = preps[0].rpad / 16;
-  const dim3 grid((unsigned)tiles), block(NV_NW * 64);
+  const dim3 block(NV_NW * 64);
   const NvStackItem* d = (const NvStackItem*)dev_items;
-  if (rc == LM_OK && any_two) {
+  if (rc == LM_OK && tiles[0] > 0) {
     TimedLaunch timed("nvfp4", st);
-    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_amax_stack<NKC_>), grid, block, 0, st, d, count));
+    const dim3 grid((unsigned)tiles[0]);
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_amax_stack<NKC_>), grid, block, 0, st, d, n_two));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 amax launch: %s", hipGetErrorString(e));
   }
   if (rc == LM_OK) {
     TimedLaunch timed("nvfp4", st);
-    if (sr) {
-      NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, true>), grid, block, 0, st, d, count));
-    } else {
-      NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, false>), grid, block, 0, st, d, count));
+#define NQ(SR_, TWO_, D_, N_, T_)                                                                              \
+  NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, SR_, TWO_>), dim3((unsigned)(T_)), block, 0, \
+                                                 st, D_, N_))
+    if (tiles[0] > 0) {
+      if (sr) { NQ(true, true, d, n_two, tiles[0]); } else { NQ(false, true, d, n_two, tiles[0]); }
     }
+    if (tiles[1] > 0) {
+      if (sr) { NQ(true, false, d + n_two, count - n_two, tiles[1]); }
+      else { NQ(false, false, d + n_two, count - n_two, tiles[1]); }
+    }
+#undef NQ
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 quant launch: %s", hipGetErrorString(e));
   }
-  if (rc == LM_OK && any_two) {
-    hipLaunchKernelGGL(k_nv_finalize, dim3((count + 63) / 64), dim3(64), 0, st, d, count);
+  if (rc == LM_OK && n_two > 0) {
+    hipLaunchKernelGGL(k_nv_finalize, dim3((n_two + 63) / 64), dim3(64), 0, st, d, n_two);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 finalize launch: %s", hipGetErrorString(e));
   }
