@@ -311,7 +311,7 @@ class Single(Workload):
         elif kind == "q8_0":
             rows, cols, rank, self.strength = 13824, 5120, 16, 1.0
             self.q = K.requantize_q8_0(_normal((rows, cols), 0.02, derive_seed(self.path, 0)))
-            self.family = "blocks_full"
+            self.family = "q8"
             self.bytes_per_step = 2 * rows * (cols // 32 * 34) + 2 * rank * (rows + cols)
         elif kind == "nvfp4":
             rows, cols, rank, self.strength = 14336, 4096, 16, 1.0

@@ -239,7 +239,7 @@ int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, int32_t swiz
  * No reference counterpart.  When enabled, every entry point brackets its
  * main kernel launches with hipEvents on the caller's stream, keyed by kernel
  * family ("rows", "rows_stack", "blocks_full", "blocks_amax",
- * "blocks_quant", "todense", "prep").  lm_timer_read synchronizes the
+ * "blocks_quant", "todense", "prep", "nvfp4", "mx", "q8", "gguf").  lm_timer_read synchronizes the
  * recorded events and returns the summed milliseconds and launch count of one
  * family.  Enabling (or re-enabling) clears the record. */
 int lm_timer_enable(int32_t enable);

@@ -3,10 +3,11 @@
 // N % 128 == 0.  P/ = the reference's src/piper_offload/.
 //
 // Same decomposition as the NVFP4 kernels: a 512-thread workgroup owns 16
-// rows, wave w walks the 128-column macro tiles mt = w, w + 8, ..., and a
-// lane holds row (lane & 15) and the 32 columns 32*(lane >> 4) .. +31 of a
-// macro tile -- exactly one MX block, so the block max, the shared exponent
-// and the codes never leave the lane (P/_triton_mx_lora.py:333-425 does one
+// rows and a chunk of 16 macro tiles (blockIdx.y), wave w walks the
+// 128-column macro tiles chunk + w, chunk + w + 8, ..., and a lane holds row
+// (lane & 15) and the 32 columns 32*(lane >> 4) .. +31 of a macro tile --
+// exactly one MX block, so the block max, the shared exponent and the codes
+// never leave the lane (P/_triton_mx_lora.py:333-425 does one
 // pass: merge, block amax, scale, encode, all in place).
 //
 // Arithmetic (P/_triton_mx_lora.py:209-295, bf16 compute):
@@ -167,14 +168,15 @@ __global__ __launch_bounds__(NV_NW * 64) void k_mx_fast(MxArgs a) {
   const int64_t row = (int64_t)blockIdx.x * 16 + rl;
   const bool rok = row < a.M;
   const int64_t rowc = rok ? row : a.M - 1;  // in-bounds loads; results dropped
-  const int ntiles = (int)(a.N >> 7);
+  const int t0 = (int)blockIdx.y * NV_CHUNK;  // this workgroup's chunk of macro tiles
+  const int ntiles = (int)((a.N >> 7) < t0 + NV_CHUNK ? (a.N >> 7) : t0 + NV_CHUNK);
   const MxLane<ELEM, NKC> l = mx_lane<ELEM, NKC>(a, rowc, lane);
   v4i16 bop[NKC];
   load_bop<NKC>(a.bp, row, lane, bop);  // Bp holds ceil(M/16)*16 rows
-  if (wave >= ntiles) return;
+  if (t0 + wave >= ntiles) return;
   MxTileIn<ELEM, NKC> cur;
-  mx_load_tile<ELEM, NKC>(l, wave, cur);
-  for (int mt = wave; mt < ntiles; mt += NV_NW) {
+  mx_load_tile<ELEM, NKC>(l, t0 + wave, cur);
+  for (int mt = t0 + wave; mt < ntiles; mt += NV_NW) {
     MxTileIn<ELEM, NKC> nxt;
     mx_load_tile<ELEM, NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
     if (rok) mx_tile<ELEM, NKC, SR>(a, cur, bop, row, mt, lane, l.q, l.sc + (int64_t)mt * l.sc_stride);
@@ -185,7 +187,7 @@ __global__ __launch_bounds__(NV_NW * 64) void k_mx_fast(MxArgs a) {
 static inline bool mx_fast_ok(int cd, int nkc, int64_t N) { return cd == LM_BF16 && nkc > 0 && (N % 128) == 0; }
 
 static int mx_fast_run(const MxArgs& a, int elem, int nkc, bool sr, hipStream_t st) {
-  const dim3 grid((unsigned)((a.M + 15) / 16)), block(NV_NW * 64);
+  const dim3 grid((unsigned)((a.M + 15) / 16), (unsigned)(((a.N >> 7) + NV_CHUNK - 1) / NV_CHUNK)), block(NV_NW * 64);
   TimedLaunch timed("mx", st);
 #define MXL(E_, SR_) NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_mx_fast<E_, NKC_, SR_>), grid, block, 0, st, a))
   if (elem == LM_E2M1) { if (sr) { MXL(E2M1, true); } else { MXL(E2M1, false); } }

@@ -2,9 +2,10 @@
 // factors, N % 128 == 0, one or two scale levels, plain or 128x4-swizzled
 // block scales.  P/ = the reference's src/piper_offload/.
 //
-// Work decomposition: a 512-thread workgroup owns 16 rows; wave w walks the
-// 128-column macro tiles mt = w, w + 8, ..., so at any time the workgroup
-// streams 8 consecutive tiles (512 contiguous bytes) of each of its rows.
+// Work decomposition: a 512-thread workgroup owns 16 rows (and, for single
+// tensors, a chunk of 16 macro tiles); wave w walks the 128-column macro tiles
+// w, w + 8, ... of its range, so at any time the workgroup streams 8
+// consecutive tiles (512 contiguous bytes) of each of its rows.
 // (Measured on MI355X with copy kernels of the same footprint: ~5.3 TB/s for
 // NVFP4 row lengths, against ~3.7 TB/s for 128-row workgroups whose waves
 // share one tile.)  A lane holds row (lane & 15) and the 32 consecutive
@@ -258,24 +259,25 @@ DEV void nv_quant_tile(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&b
 
 // ---- pass bodies -------------------------------------------------------------
 // Rows past M load row M-1 (valid memory) and store nothing.
+// Tiles [t0, t1) of rows row0 .. row0+15 (the stack passes whole rows).
 template <int NKC>
-DEV void nv_amax_body(const NvArgs& a, int64_t row0) {
+DEV void nv_amax_body(const NvArgs& a, int64_t row0, int t0, int t1) {
   __shared__ float sh[NV_NW];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int64_t row = row0 + rl;
   const bool rok = row < a.M;
   const int64_t rowc = rok ? row : a.M - 1;
-  const int ntiles = (int)(a.N >> 7);
+  const int ntiles = t1;
   const float gin = *a.gin;
   const float strength = a.strength;
   const NvLane<NKC> l = nv_lane<NKC>(a, rowc, lane);
   v4i16 bop[NKC];
   load_bop<NKC>(a.bp, row, lane, bop);  // Bp holds ceil(M/16)*16 rows
   float mx = 0.0f;
-  if (wave < ntiles) {
+  if (t0 + wave < ntiles) {
     NvTileIn<NKC> cur;
-    nv_load_tile<NKC>(l, wave, cur);
-    for (int mt = wave; mt < ntiles; mt += NV_NW) {
+    nv_load_tile<NKC>(l, t0 + wave, cur);
+    for (int mt = t0 + wave; mt < ntiles; mt += NV_NW) {
       NvTileIn<NKC> nxt;
       nv_load_tile<NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
       float m[32];
@@ -299,12 +301,12 @@ DEV void nv_amax_body(const NvArgs& a, int64_t row0) {
 }
 
 template <int NKC, bool TWO, bool SR>
-DEV void nv_quant_body(const NvArgs& a, int64_t row0, const float* rtab) {
+DEV void nv_quant_body(const NvArgs& a, int64_t row0, int t0, int t1, const float* rtab) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int64_t row = row0 + rl;
   const bool rok = row < a.M;
   const int64_t rowc = rok ? row : a.M - 1;
-  const int ntiles = (int)(a.N >> 7);
+  const int ntiles = t1;
   const float gin = TWO ? *a.gin : 1.0f;
   float gq = 1.0f, inv_g = 1.0f;
   if constexpr (TWO) {
@@ -316,10 +318,10 @@ DEV void nv_quant_body(const NvArgs& a, int64_t row0, const float* rtab) {
   uint8_t* so = a.scale_out + blocked_offset(rowc, 2 * (lane >> 4), a.N >> 4, a.swizzled);
   v4i16 bop[NKC];
   load_bop<NKC>(a.bp, row, lane, bop);
-  if (wave >= ntiles) return;
+  if (t0 + wave >= ntiles) return;
   NvTileIn<NKC> cur;
-  nv_load_tile<NKC>(l, wave, cur);
-  for (int mt = wave; mt < ntiles; mt += NV_NW) {
+  nv_load_tile<NKC>(l, t0 + wave, cur);
+  for (int mt = t0 + wave; mt < ntiles; mt += NV_NW) {
     NvTileIn<NKC> nxt;
     nv_load_tile<NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
     if (rok) nv_quant_tile<NKC, TWO, SR>(a, cur, bop, gin, row, mt, lane, gq, inv_g, rtab, qo, so, l.sc_stride);
@@ -341,23 +343,31 @@ DEV int nv_find(const NvStackItem* __restrict__ items, int count, int64_t t) {
 // One workgroup per 16 rows (tile_begin counts 16-row groups).
 static inline int64_t nv_units(int64_t M, int64_t /*N*/) { return (M + 15) / 16; }
 
+// Single tensors: blocks are independent once the global scale is known, so a
+// workgroup owns 16 rows x NV_CHUNK macro tiles (blockIdx.y picks the chunk);
+// a [14336, 4096] tensor becomes 1792 workgroups instead of 896 whole-row ones.
+constexpr int NV_CHUNK = 2 * NV_NW;
+DEV int nv_chunk_end(const NvArgs& a) {
+  const int t1 = ((int)blockIdx.y + 1) * NV_CHUNK, nt = (int)(a.N >> 7);
+  return t1 < nt ? t1 : nt;
+}
 template <int NKC>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_amax(NvArgs a) {
-  nv_amax_body<NKC>(a, (int64_t)blockIdx.x * 16);
+  nv_amax_body<NKC>(a, (int64_t)blockIdx.x * 16, (int)blockIdx.y * NV_CHUNK, nv_chunk_end(a));
 }
 template <int NKC, bool SR, bool TWO>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant(NvArgs a) {
   __shared__ float rtab[8];
   if (threadIdx.x < 8) rtab[threadIdx.x] = kRcpE4M3[threadIdx.x];
   __syncthreads();
-  nv_quant_body<NKC, TWO, SR>(a, (int64_t)blockIdx.x * 16, rtab);
+  nv_quant_body<NKC, TWO, SR>(a, (int64_t)blockIdx.x * 16, (int)blockIdx.y * NV_CHUNK, nv_chunk_end(a), rtab);
 }
 template <int NKC>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_amax_stack(const NvStackItem* __restrict__ items, int count) {
   const int i = nv_find(items, count, blockIdx.x);
   const NvArgs a = items[i].a;
   if (a.gin == nullptr) return;  // single-level item: no global scale to find
-  nv_amax_body<NKC>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16);
+  nv_amax_body<NKC>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16, 0, (int)(a.N >> 7));
 }
 // TWO: every item of the launch is two-level (the host splits a mixed stack)
 template <int NKC, bool SR, bool TWO>
@@ -366,7 +376,8 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant_stack(const NvStackItem
   if (threadIdx.x < 8) rtab[threadIdx.x] = kRcpE4M3[threadIdx.x];
   __syncthreads();
   const int i = nv_find(items, count, blockIdx.x);
-  nv_quant_body<NKC, TWO, SR>(items[i].a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16, rtab);
+  const NvArgs& a = items[i].a;
+  nv_quant_body<NKC, TWO, SR>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16, 0, (int)(a.N >> 7), rtab);
 }
 // one thread per item: g = max(amax / 2688, eps)
 static __global__ void k_nv_finalize(const NvStackItem* __restrict__ items, int count) {
@@ -384,7 +395,7 @@ static inline bool nv_fast_ok(int cd, int nkc, int64_t N) { return cd == LM_BF16
 
 // single tensor: amax (two-level), quant, finalize on `st`
 static int nv_fast_run(const NvArgs& a, int nkc, bool sr, hipStream_t st) {
-  const dim3 grid((unsigned)nv_units(a.M, a.N)), block(NV_NW * 64);
+  const dim3 grid((unsigned)nv_units(a.M, a.N), (unsigned)(((a.N >> 7) + NV_CHUNK - 1) / NV_CHUNK)), block(NV_NW * 64);
   if (a.gin) {
     TimedLaunch timed("nvfp4", st);
     NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_amax<NKC_>), grid, block, 0, st, a));

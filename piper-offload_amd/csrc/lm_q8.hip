@@ -1,5 +1,5 @@
 // lm_q8.hip -- GGUF Q8_0 merge / requant and GGUF dequant entry points.
-#include "lm_impl.h"
+#include "lm_q8_fast.h"
 
 // ---------------------------------------------------------------------------
 // GGUF Q8_0
@@ -19,6 +19,18 @@ extern "C" int lm_q8_0_merge(const uint8_t* packed, uint8_t* packed_out, int64_t
   if ((rc = check_rounding(rounding))) return rc;
   Ctx c;
   if ((rc = setup(c, M, N, lora, workspace, workspace_bytes, stream))) return rc;
+  if (q8_fast_ok(lora->dtype, c.nkc, N)) {
+    Q8Args qa;
+    qa.q = packed;
+    qa.q_out = packed_out;
+    qa.at = c.at;
+    qa.bp = c.bp;
+    qa.M = M;
+    qa.N = N;
+    qa.strength = lora->strength;
+    qa.seed = rounding ? rounding->seed : 0;
+    return q8_fast_run(qa, c.nkc, is_sr(rounding), c.st);
+  }
   BlkArgs a = blk_args_base(c, M, N, lora, rounding);
   a.q = packed;
   a.q_out = packed_out;

@@ -83,9 +83,13 @@ def test_mx_zero_update_is_identity_and_code0_subnormal():
     assert np.array_equal(u8_np(t.scale), rs)
 
 
-@pytest.mark.parametrize("shape,rank", [((13824 // 64, 5120), 16), ((48, 96), 5), ((33, 64), 16)])
+# N % 128 == 0 with bf16 factors takes the one-block-per-lane kernel (k_q8_fast);
+# the other shapes take the generic block kernel
+@pytest.mark.parametrize("shape,rank,strength", [
+    ((13824 // 64, 5120), 16, 1.0), ((48, 96), 5, 1.0), ((33, 64), 16, 1.0),
+    ((37, 384), 32, 0.5), ((40, 256), 64, -1.25), ((17, 128), 16, 2.0)])
 @pytest.mark.parametrize("sr", [False, True])
-def test_q8_0_merge(shape, rank, sr):
+def test_q8_0_merge(shape, rank, strength, sr):
     rows, cols = shape
     w = normal_bf16(shape, 0.02, 1)
     packed = O.q8_0_requant(bf16_np(w))
@@ -94,14 +98,28 @@ def test_q8_0_merge(shape, rank, sr):
     base = K.dequantize_gguf(pd, 8)
     obase = O.q8_0_dequant(packed, cols)
     assert np.array_equal(bf16_np(base), obase)
-    dense = K.dequantize_gguf(pd, 8, lora=(b.to(DEV), a.to(DEV), 1.0))
-    assert_merged_close(bf16_np(dense), O.merge_dense(obase, bf16_np(b), bf16_np(a), 1.0), obase)
+    dense = K.dequantize_gguf(pd, 8, lora=(b.to(DEV), a.to(DEV), strength))
+    assert_merged_close(bf16_np(dense), O.merge_dense(obase, bf16_np(b), bf16_np(a), strength), obase)
     seed = derive_seed("q8.fused", rows) if sr else None
-    out = K.merge_q8_0_lora(pd, b.to(DEV), a.to(DEV), 1.0, rounding_seed=seed)
+    out = K.merge_q8_0_lora(pd, b.to(DEV), a.to(DEV), strength, rounding_seed=seed)
     ref = O.q8_0_requant(bf16_np(dense), sr_mode=O.SR_PHILOX8 if sr else O.SR_OFF, seed=seed or 0)
     assert np.array_equal(u8_np(out), ref)
     rq = K.requantize_q8_0(dense, rounding_seed=seed)
     assert np.array_equal(u8_np(rq), ref)
+    # in place (the output aliases the input) gives the same bytes
+    K.merge_q8_0_lora(pd, b.to(DEV), a.to(DEV), strength, rounding_seed=seed, out=pd)
+    assert np.array_equal(u8_np(pd), ref)
+
+
+def test_q8_0_merge_config4_full_size():
+    # [13824, 5120] rank 16, strength 1.0, RTN
+    rows, cols = 13824, 5120
+    packed = O.q8_0_requant(bf16_np(normal_bf16((rows, cols), 0.02, 11)))
+    b, a = lora_factors(rows, cols, 16, 12)
+    pd = torch.from_numpy(packed).to(DEV)
+    dense = K.dequantize_gguf(pd, 8, lora=(b.to(DEV), a.to(DEV), 1.0))
+    out = K.merge_q8_0_lora(pd, b.to(DEV), a.to(DEV), 1.0)
+    assert np.array_equal(u8_np(out), O.q8_0_requant(bf16_np(dense)))
 
 
 def test_gguf_adapter_in_place():
