@@ -562,9 +562,12 @@ __device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const FastTil
   }
 }
 
+// `wide` (wave-uniform): some row of the wave has a scale above 2^100, where
+// the two-term reciprocal's low part would be subnormal (weights above 1e30);
+// those waves use the three-instruction quotient, exact for every normal scale.
 template <int KIND, bool SR>
 __device__ __forceinline__ void fast_quant_store(const RowArgs& a, int64_t row, bool rok, int mt, int lane,
-                                                 const RowQP& qp, const uint32_t (&w)[8]) {
+                                                 const RowQP& qp, const uint32_t (&w)[8], bool wide) {
   if (!rok) return;
   const int64_t N = a.N;
   const int64_t c0 = (int64_t)mt * 64 + 16 * (lane >> 4);
@@ -580,15 +583,33 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, int64_t row, 
       // Y is first clamped to [qmin, qmax] * 65536, which yields the bound for
       // exactly the inputs the reference keeps at their (clamped) RTN code.
       // The code byte is bit 16..23 of T + 65535 - h, picked by v_perm.
+      // RN(m / s) = RN(m hi + RN(m lo)) with 1/s = hi + lo (qp.inv, qp.rcp,
+      // scaled by 65536): m and s are bf16 values (8-bit significands), so m/s
+      // is representable or at least 2^-33 (relative) away from a rounding
+      // midpoint, far more than the ~2^-47 error of the two-term product.
       const float lo16 = (float)a.qmin * 65536.0f, hi16 = (float)a.qmax * 65536.0f;
+      float y16[16];
+      if (!wide) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
+          y16[j] = __builtin_amdgcn_fmed3f(__builtin_fmaf(m, qp.inv, m * qp.rcp), lo16, hi16);
+        }
+      } else {
+        // q0 = m 65536 RN(1/s), e = m - q0 s / 65536 (exact), Y = q0 + e 65536 RN(1/s)
+        const float rs = qp.s * (1.0f / 65536.0f);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
+          const float q0 = m * qp.inv;
+          const float e = __builtin_fmaf(-q0, rs, m);
+          y16[j] = __builtin_amdgcn_fmed3f(__builtin_fmaf(e, qp.inv, q0), lo16, hi16);
+        }
+      }
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
-        const float q0 = m * qp.inv;  // qp.inv = 65536 * RN(1/s)
-        const float e = __builtin_fmaf(-q0, qp.rcp, m);  // qp.rcp = s / 65536
-        const float y16 = __builtin_amdgcn_fmed3f(__builtin_fmaf(e, qp.inv, q0), lo16, hi16);
-        const uint32_t tneg = (uint32_t)cvt_flr_neg(y16);  // -ceil(Y)
-        const uint32_t nw = ~rw[j >> 1];                    // 65535 - h in each half
+        const uint32_t tneg = (uint32_t)cvt_flr_neg(y16[j]);  // -ceil(Y)
+        const uint32_t nw = ~rw[j >> 1];                       // 65535 - h in each half
         y[j] = (j & 1) ? (nw >> 16) - tneg : sub_lo16(nw, tneg);
       }
 #pragma unroll
@@ -703,8 +724,11 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
       if (r < a.M) ((float*)a.scale_out)[r] = stored;
       if (r < a.M && a.zp_out) a.zp_out[r] = 0;
       if constexpr (SR) {
-        qp.inv = qp.rcp * 65536.0f;  // 65536 * RN(1/s)
-        qp.rcp = qp.s * (1.0f / 65536.0f);
+        // 1/s as hi + lo: hi = RN(1/s), lo = (1 - s hi) hi (the fma residual is
+        // exact), together within ~2^-47 of 1/s; both scaled by 65536
+        const float lo = __builtin_fmaf(-qp.s, qp.rcp, 1.0f) * qp.rcp;
+        qp.inv = qp.rcp * 65536.0f;
+        qp.rcp = lo * 65536.0f;
       }
     } else {
       qp = fp8_qparams<BF16, KIND>(mx, stored);
@@ -721,10 +745,11 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   qp.inv = sh_qp[1][rl];
   qp.rcp = sh_qp[2][rl];
   qp.zp = sh_qp[3][rl];
+  const bool wide = KIND == K_INT8 && SR && __any(qp.s > 0x1p100f);
 #pragma unroll
   for (int i = 0; i < CACHE; ++i) {
     const int mt = wave + i * NW;
-    if (mt < ntiles) fast_quant_store<KIND, SR>(a, row, rok, mt, lane, qp, cache[i]);
+    if (mt < ntiles) fast_quant_store<KIND, SR>(a, row, rok, mt, lane, qp, cache[i], wide);
   }
   if (wave + CACHE * NW < ntiles) {
     FastTileIn<NKC> cur;
@@ -734,7 +759,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
       fast_load_tile<NKC>(a, rowc, mt + NW < ntiles ? mt + NW : mt, lane, nxt);
       uint32_t t[8];
       fast_merged_tile<KIND, NKC>(a, cur, bop, s_in, t);
-      fast_quant_store<KIND, SR>(a, row, rok, mt, lane, qp, t);
+      fast_quant_store<KIND, SR>(a, row, rok, mt, lane, qp, t, wide);
       cur = nxt;
     }
   }
