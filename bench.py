@@ -17,7 +17,7 @@ whole stack once, in place, through the grouped HIP kernel.
 merge) on a bounded sample of the same workload.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload int8_stack|nvfp4_stack|int8|fp8|q8_0|nvfp4|mxfp4|gguf|copy]
+                    [--workload int8_stack|nvfp4_stack|int8|fp8|q8_0|nvfp4|mxfp4|gguf|reload|h2d|copy]
                     [--rounding stochastic|nearest] [--gguf-type Q4_K] [--cpu-seconds S]
 """
 
@@ -80,7 +80,8 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="int8_stack",
-                   choices=["int8_stack", "nvfp4_stack", "int8", "fp8", "q8_0", "nvfp4", "mxfp4", "gguf", "copy"])
+                   choices=["int8_stack", "nvfp4_stack", "int8", "fp8", "q8_0", "nvfp4", "mxfp4", "gguf", "reload", "h2d",
+                            "copy"])
     p.add_argument("--gguf-type", default="Q4_K", choices=sorted(GGUF_TYPES),
                    help="GGUF type of --workload gguf (dequantize to bf16)")
     p.add_argument("--rounding", default="stochastic", choices=["stochastic", "nearest"])
@@ -255,6 +256,82 @@ class Copy(Workload):
         import torch
 
         torch.bitwise_not(self.src, out=self.dst)
+
+
+class _HostStack:
+    """The 8B-shaped INT8 stack with its stored weights in pinned host memory
+    (what an offloaded model keeps between reloads) and its factors on the GPU."""
+
+    def __init__(self, layers: int) -> None:
+        from piper_offload_amd.reload import HostInt8Target
+
+        self.layers = []
+        self.h2d_bytes = 0
+        for layer in range(layers):
+            targets = []
+            for name, rows, cols in LAYER_SHAPES:
+                path = f"model.layers.{layer}.{name}.weight"
+                w = _int8_weight(path, rows, cols)
+                b, a = _factors(path, rows, cols, 16)
+                targets.append(HostInt8Target(path, w.qdata.cpu().pin_memory(), w.scale.cpu().pin_memory(), b, a, 1.0))
+                self.h2d_bytes += w.qdata.numel() + 4 * w.scale.numel()
+                del w
+            self.layers.append(targets)
+
+
+class Reload(Workload):
+    """Merge on reload (P/model_offloader.py:245-288): every step reloads all
+    layers of the stack from pinned host memory through two device slots and
+    merges each layer (one grouped launch) while the next layer is copied."""
+
+    family = "rows_stack"
+
+    def __init__(self, layers: int, stochastic: bool) -> None:
+        from piper_offload_amd.reload import ReloadMergePipeline
+
+        host = _HostStack(layers)
+        self.pipe = ReloadMergePipeline(host.layers, slots=2, stochastic=stochastic)
+        self.n = len(host.layers)
+        self.bytes_per_step = host.h2d_bytes
+        # the merge kernels' own algorithmic bytes, for the roofline block
+        self.kernel_bytes_per_step = layers * sum(_int8_bytes(r, c, 16) for _, r, c in LAYER_SHAPES)
+        self.name = "reload"
+        self.config = {"workload": f"{layers}-layer 8B-shaped INT8 stack reloaded from pinned host memory and merged "
+                                   f"on reload (copy stream + merge stream, 2 device slots, one grouped merge per "
+                                   f"layer, {'stochastic' if stochastic else 'round-to-nearest'} requant, seed "
+                                   f"derive_seed(param_path, step)); value = host-to-device GB/s of the stored weights",
+                       "h2d_bytes_per_step": self.bytes_per_step}
+
+    def step(self, index: int) -> None:
+        for layer in range(self.n):
+            r = self.pipe.reload(layer, index)
+            r.wait()  # the consumer (the current stream) uses the merged layer ...
+            self.pipe.release(r)  # ... and hands the slot back
+
+
+class H2D(Workload):
+    """The reload workload's copies alone (same bytes, same two slots, one
+    stream, no merge): the host-link baseline the merge hides behind."""
+
+    family = ""
+
+    def __init__(self, layers: int) -> None:
+        import torch
+
+        host = _HostStack(layers)
+        self.layers = host.layers
+        self.slots = [[(torch.empty_like(t.qdata, device="cuda"), torch.empty_like(t.scale, device="cuda"))
+                       for t in self.layers[0]] for _ in range(2)]
+        self.bytes_per_step = host.h2d_bytes
+        self.name = "h2d"
+        self.config = {"workload": f"{layers}-layer 8B-shaped INT8 stack copied from pinned host memory (no merge)",
+                       "h2d_bytes_per_step": self.bytes_per_step}
+
+    def step(self, index: int) -> None:
+        for layer, targets in enumerate(self.layers):
+            for (q, s), t in zip(self.slots[layer % 2], targets):
+                q.copy_(t.qdata, non_blocking=True)
+                s.copy_(t.scale, non_blocking=True)
 
 
 class Gguf(Workload):
@@ -451,6 +528,10 @@ def main() -> int:
         wl = Nvfp4Stack(args.layers, stochastic)
     elif args.workload == "gguf":
         wl = Gguf(args.gguf_type)
+    elif args.workload == "reload":
+        wl = Reload(args.layers, stochastic)
+    elif args.workload == "h2d":
+        wl = H2D(args.layers)
     else:
         wl = Single(args.workload, stochastic)
     torch.cuda.synchronize()
@@ -477,7 +558,8 @@ def main() -> int:
           f"{wl.family}: {launches} launches {kern_ms / max(launches, 1):.3f} ms avg", file=sys.stderr, flush=True)
     # the dominant kernel family's time per step (one launch, or the amax +
     # quant launches of a two-level NVFP4 merge) against the step's bytes
-    achieved = wl.bytes_per_step * args.steps / (kern_ms * 1e-3) / 1e9 if launches else None
+    kbytes = getattr(wl, "kernel_bytes_per_step", wl.bytes_per_step)
+    achieved = kbytes * args.steps / (kern_ms * 1e-3) / 1e9 if launches else None
     print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
     cpu = cpu_baseline(args.workload, stochastic, args.cpu_seconds, args.gguf_type)
     out = {

@@ -196,3 +196,14 @@ def test_stochastic_seed_is_derived_per_target_and_merge_index() -> None:
             LoRATransform([f], target_key="k").apply_weight(t)
     finally:
         remove()
+
+
+def test_reload_pipeline_rejects_unpinned_weights() -> None:
+    from piper_offload_amd.reload import HostInt8Target, ReloadMergePipeline
+
+    t = HostInt8Target("w", torch.zeros(4, 8, dtype=torch.int8), torch.ones(4, 1), torch.zeros(4, 2),
+                       torch.zeros(2, 8))
+    with pytest.raises(ValueError, match="pinned host memory"):
+        ReloadMergePipeline([[t]])
+    with pytest.raises(ValueError, match="at least one target"):
+        ReloadMergePipeline([[]])
