@@ -81,7 +81,7 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="int8_stack",
                    choices=["int8_stack", "nvfp4_stack", "int8", "fp8", "q8_0", "nvfp4", "mxfp4", "gguf", "reload", "h2d",
-                            "copy"])
+                            "api", "copy"])
     p.add_argument("--gguf-type", default="Q4_K", choices=sorted(GGUF_TYPES),
                    help="GGUF type of --workload gguf (dequantize to bf16)")
     p.add_argument("--rounding", default="stochastic", choices=["stochastic", "nearest"])
@@ -334,6 +334,48 @@ class H2D(Workload):
                 s.copy_(t.scale, non_blocking=True)
 
 
+class Api(Workload):
+    """The 8B-shaped INT8 stack merged through the drop-in API, ``merge_lora(model, [(lora, 1.0)])``
+    (P/merge.py:54-87): a module whose 224 weights are INT8 tensors on the GPU and a LoRA whose factors
+    sit in pinned host memory, so every step resolves the targets, stages each target's factors with
+    one host-to-device copy and runs one merge launch per target."""
+
+    family = "rows"
+
+    def __init__(self, layers: int, stochastic: bool) -> None:
+        from torch import nn
+
+        from piper_offload_amd import LoRA
+
+        self.stochastic = stochastic
+        self.model = nn.Module()
+        sd = {}
+        rank = 16
+        for i in range(layers):
+            for name, rows, cols in LAYER_SHAPES:
+                path = f"model.layers.{i}.{name}.weight"
+                key = f"layers_{i}_{name.replace('.', '_')}"  # one holder module per weight: parameter '<key>.weight'
+                holder = nn.Module()
+                holder.weight = nn.Parameter(_int8_weight(path, rows, cols), requires_grad=False)
+                self.model.add_module(key, holder)
+                b, a = _factors(path, rows, cols, rank)
+                sd[f"{key}.lora_A.weight"] = a.cpu()
+                sd[f"{key}.lora_B.weight"] = b.cpu()
+                self.bytes_per_step += _int8_bytes(rows, cols, rank)
+        self.lora = LoRA.from_state_dict(sd)
+        self.name = "api"
+        self.config = {"workload": f"{layers}-layer 8B-shaped INT8 stack ({7 * layers} targets) merged by "
+                                   "merge_lora(model, [(lora, 1.0)]): factors in pinned host memory, one staging "
+                                   "copy and one merge launch per target, "
+                                   f"{'stochastic' if stochastic else 'round-to-nearest'} requant",
+                       "targets": 7 * layers, "rank": rank, "algorithmic_bytes_per_step": self.bytes_per_step}
+
+    def step(self, index: int) -> None:
+        from piper_offload_amd import merge_lora
+
+        merge_lora(self.model, [(self.lora, 1.0)], stochastic_rounding=self.stochastic)
+
+
 class Gguf(Workload):
     """GGUF dequantize (P/gguf_dequant.py:303-331) of one gate_proj-shaped [14336, 4096] tensor to bf16."""
 
@@ -532,6 +574,8 @@ def main() -> int:
         wl = Reload(args.layers, stochastic)
     elif args.workload == "h2d":
         wl = H2D(args.layers)
+    elif args.workload == "api":
+        wl = Api(args.layers, stochastic)
     else:
         wl = Single(args.workload, stochastic)
     torch.cuda.synchronize()

@@ -152,6 +152,23 @@ class Int8Adapter:
                                out_zero_point=zp)
 
     @staticmethod
+    def stack_key(target: torch.Tensor) -> tuple | None:
+        """Key of the grouped launch (``lm_int8_merge_stack``) that merges ``target`` exactly as
+        :meth:`merge_lora_` does, or None: per-row symmetric codes with full range, no
+        ``act_pre_scale``, contiguous storage, float32/bfloat16 scales.  Targets with equal keys
+        share one launch."""
+        qt = _require(target, Int8Adapter.ATTRS, "INT8")
+        q, s, zp = qt.qdata, qt.scale, qt.zero_point
+        if q.device.type != "cuda" or q.dtype is not torch.int8 or q.ndim != 2 or bool(qt.reduce_range) \
+                or getattr(qt, "act_pre_scale", None) is not None or tuple(qt.block_size) != (1, q.shape[1]) \
+                or s.dtype not in (torch.float32, torch.bfloat16) or s.numel() != q.shape[0] \
+                or not q.is_contiguous() or not s.is_contiguous() or s.device != q.device:
+            return None
+        if zp is not None and bool(zp.any()):  # mapping type from the zero point, as merge_lora_ infers it
+            return None
+        return ("int8", q.device, s.dtype)
+
+    @staticmethod
     def stage_lora_factors(target: torch.Tensor, factors: tuple[tuple[float, torch.Tensor, torch.Tensor], ...], *,
                            logical_shape: tuple[int, ...], compute_dtype: torch.dtype
                            ) -> tuple[torch.Tensor, torch.Tensor, float] | None:
@@ -308,6 +325,22 @@ class Nvfp4Adapter:
                              "the merge recomputes a single global scale. Use routed LoRA for this weight.")
         if nv.block_size != 16:
             raise ValueError("HIP NVFP4 merge requires block_size=16.")
+
+    @staticmethod
+    def stack_key(target: torch.Tensor) -> tuple | None:
+        """Key of the grouped launches (``lm_nvfp4_merge_stack``) that merge ``target`` exactly as
+        :meth:`merge_lora_` does, or None; targets with equal keys (one scale layout) share them."""
+        nv = _require(target, Nvfp4Adapter.ATTRS, "NVFP4")
+        q, s, pts = nv.qdata, nv.scale, nv.per_tensor_scale
+        if q.device.type != "cuda" or q.dtype is not torch.uint8 or q.ndim != 2 or s.ndim != 2 \
+                or s.dtype is not torch.float8_e4m3fn or nv.block_size != 16 or q.shape[1] % 8 != 0 \
+                or not q.is_contiguous() or not s.is_contiguous() or s.device != q.device:
+            return None
+        if tuple(s.shape) != K._nvfp4_scale_shape(q.shape[0], 2 * q.shape[1], bool(nv.is_swizzled_scales)):
+            return None
+        if pts is not None and (pts.dtype is not torch.float32 or pts.numel() != 1 or pts.device != q.device):
+            return None
+        return ("nvfp4", q.device, bool(nv.is_swizzled_scales))
 
     @staticmethod
     def merge_lora_(target: torch.Tensor, b: torch.Tensor, a: torch.Tensor, strength: float, *,

@@ -29,6 +29,7 @@ from torch import nn
 
 from .registry import param_representation, select_adapter
 from .seeding import derive_seed
+from .stack import StackTarget
 
 __all__ = ["LoRA", "LoRAFactor", "LoRATransform", "ScaledLoRAFactor"]
 
@@ -157,7 +158,7 @@ class _WeightPlan:
 class LoRATransform:
     """LoRA factors applied to one base weight and optional base bias (P/lora.py:314-724)."""
 
-    __slots__ = ("_factors", "_merge_index", "_stochastic_rounding", "_target_key", "_weight_plan")
+    __slots__ = ("_factors", "_merge_index", "_staged", "_stochastic_rounding", "_target_key", "_weight_plan")
 
     def __init__(self, factors: list[ScaledLoRAFactor], *, stochastic_rounding: bool = False,
                  target_key: str = "") -> None:
@@ -168,6 +169,9 @@ class LoRATransform:
         self._target_key = target_key
         self._merge_index = 0
         self._weight_plan: _WeightPlan | None = None
+        # staged (B, A, strength) per (device, dtype, shape), valid while the
+        # host factors are unmodified (their in-place version counters)
+        self._staged: dict[tuple, tuple] = {}
 
     @property
     def merge_index(self) -> int:
@@ -262,6 +266,37 @@ class LoRATransform:
             plan.adapter.merge_lora_(data, b, a, strength, rounding_seed=seed)
         self._merge_index += 1
 
+    def stack_target(self, param: nn.Parameter | torch.Tensor) -> tuple[tuple, StackTarget] | None:
+        """This weight's merge as one target of a grouped launch, with its group key, or None.
+
+        Only weights whose adapter names a grouped kernel (``stack_key``) and
+        whose factors need no adapter-specific staging qualify; the grouped
+        kernels give the same bytes as :meth:`apply_weight` with the same
+        seed.  The caller merges the group and then calls :meth:`advance`.
+        """
+        plan = self._weight_plan
+        if plan is None:
+            raise RuntimeError("LoRA weight target must be validated before application.")
+        key_of = getattr(plan.adapter, "stack_key", None)
+        if not callable(key_of):
+            return None
+        data = param_representation(param)
+        key = key_of(data)
+        if key is None:
+            return None
+        b, a, strength, prepared = self._stage(data, plan.adapter, plan.staging_shape, plan.compute_dtype)
+        rank = a.shape[0]
+        if prepared or a.dtype not in (torch.bfloat16, torch.float16) or not 0 < rank <= 64:
+            return None
+        bucket = 16 if rank <= 16 else 32 if rank <= 32 else 64  # one rank padding per launch
+        seed = self._rounding_seed()
+        return ((*key, a.dtype, bucket, self._stochastic_rounding),
+                StackTarget(data, b, a, strength, 0 if seed is None else seed))
+
+    def advance(self) -> None:
+        """Count one merge applied outside :meth:`apply_weight` (the next merge's seed index)."""
+        self._merge_index += 1
+
     def apply_bias(self, param: torch.Tensor) -> None:
         target = param_representation(param)
         delta = torch.zeros_like(target)
@@ -290,24 +325,44 @@ class LoRATransform:
 
     def _stage_single_or_packed(self, data: torch.Tensor, shape: tuple[int, ...],
                                 compute_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor, float]:
+        """(B, A, strength) on ``data``'s device in ``compute_dtype`` (P/lora.py:595-626, 684-724).
+
+        The reference stages the factors on every validate and every apply.
+        Here they land once, straight from the (pinned) host factors, in one
+        device buffer holding A then B, and later validates and applies
+        reuse it until a host factor is modified in place.  Several factors
+        are packed along the rank with each A slice scaled by its strength in
+        ``compute_dtype`` on the device, as the reference does.
+        """
         device = data.device
-        if len(self._factors) == 1:
-            f = self._factors[0]
-            return (f.b.to(device=device, dtype=compute_dtype, non_blocking=True).contiguous(),
-                    f.a.to(device=device, dtype=compute_dtype, non_blocking=True).contiguous(), f.strength)
-        total = sum(f.a.shape[0] for f in self._factors)
-        a_packed = torch.empty((total, shape[1]), device=device, dtype=compute_dtype)
-        b_packed = torch.empty((shape[0], total), device=device, dtype=compute_dtype)
-        off = 0
-        for f in self._factors:
-            nxt = off + f.a.shape[0]
-            a_slice = a_packed[off:nxt]
-            a_slice.copy_(f.a, non_blocking=True)
-            b_packed[:, off:nxt].copy_(f.b, non_blocking=True)
-            if f.strength != 1.0:
-                a_slice.mul_(f.strength)
-            off = nxt
-        return b_packed, a_packed, 1.0
+        key = (device, compute_dtype, tuple(shape))
+        versions = tuple(v for f in self._factors for v in (f.a._version, f.b._version))
+        hit = self._staged.get(key)
+        if hit is not None and hit[0] == versions:
+            return hit[1], hit[2], hit[3]
+        factors = self._factors
+        total = sum(f.a.shape[0] for f in factors)
+        rows, cols = shape[0], shape[1]
+        buf = torch.empty(total * cols + rows * total, dtype=compute_dtype, device=device)
+        a = buf[: total * cols].view(total, cols)
+        b = buf[total * cols:].view(rows, total)
+        if len(factors) == 1:
+            f = factors[0]
+            a.copy_(f.a, non_blocking=True)
+            b.copy_(f.b, non_blocking=True)
+            strength = f.strength
+        else:
+            off = 0
+            for f in factors:
+                nxt = off + f.a.shape[0]
+                a[off:nxt].copy_(f.a, non_blocking=True)
+                b[:, off:nxt].copy_(f.b, non_blocking=True)
+                if f.strength != 1.0:
+                    a[off:nxt].mul_(f.strength)
+                off = nxt
+            strength = 1.0
+        self._staged[key] = (versions, b, a, strength)
+        return b, a, strength
 
 
 def _split_factor_tensors(state_dict: dict[str, torch.Tensor]

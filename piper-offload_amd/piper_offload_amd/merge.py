@@ -19,6 +19,7 @@ from torch import nn
 
 from .lora import LoRA, LoRATransform, ScaledLoRAFactor
 from .registry import param_tensor_id
+from .stack import StackPlan, StackTarget
 
 logger = logging.getLogger(__name__)
 
@@ -57,14 +58,41 @@ def merge_lora(model: nn.Module, loras: Sequence[tuple[LoRA, float]], *, stochas
     ops = _build_merge_ops(params, active, stochastic_rounding=stochastic_rounding)
     for op in ops:  # preflight everything before mutating anything
         op.validate()
-    for op in ops:
-        op.apply()
+    _apply_all(ops)
     modified = {param_tensor_id(op.weight) for op in ops}
     modified.update(param_tensor_id(op.bias) for op in ops if op.bias is not None)
     logger.info("merge_lora: merged %d unique parameters (%d weights, %d biases) from %d LoRA targets",
                 len(modified), len(ops), sum(op.bias is not None for op in ops),
                 sum(len(lora.targets) for lora, _s in active))
     return len(modified)
+
+
+def _apply_all(ops: list[_MergeOp]) -> None:
+    """Apply every validated op.  Weights that a grouped kernel can merge
+    (per-row INT8, NVFP4) are merged together, one grouped launch per
+    compatible group, instead of one launch each (P/merge.py:124-125 loops);
+    the rest, and all biases, are applied one by one.  Targets are distinct
+    tensors (tied aliases are rejected), so the order does not change any
+    result, and each grouped target keeps its own seed."""
+    groups: dict[tuple, list[tuple[_MergeOp, StackTarget]]] = {}
+    single: list[_MergeOp] = []
+    for op in ops:
+        st = op.transform.stack_target(op.weight)
+        if st is None:
+            single.append(op)
+        else:
+            groups.setdefault(st[0], []).append((op, st[1]))
+    for key, members in groups.items():
+        if len(members) == 1:  # one tensor: its own launch is the tuned path
+            single.append(members[0][0])
+            continue
+        StackPlan([t for _op, t in members], key[0]).merge(stochastic=key[-1])
+        for op, _t in members:
+            op.transform.advance()
+            if op.bias is not None:
+                op.transform.apply_bias(op.bias)
+    for op in single:
+        op.apply()
 
 
 def _sibling(name: str, leaf: str) -> str:

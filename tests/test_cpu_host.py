@@ -207,3 +207,44 @@ def test_reload_pipeline_rejects_unpinned_weights() -> None:
         ReloadMergePipeline([[t]])
     with pytest.raises(ValueError, match="at least one target"):
         ReloadMergePipeline([[]])
+
+
+def test_factor_staging_is_one_buffer_reused_until_a_factor_changes() -> None:
+    # one host buffer holds A then B; validate and every apply reuse it, and an
+    # in-place change of a host factor restages (P/lora.py:595-626 stages on each)
+    g = torch.Generator().manual_seed(11)
+    f = ScaledLoRAFactor(torch.randn(4, 24, generator=g), torch.randn(16, 4, generator=g), 0.75)
+    tr = LoRATransform([f], target_key="w")
+    data = torch.zeros(16, 24, dtype=torch.bfloat16)
+    b, a, s = tr.staged_update(data, torch.bfloat16)
+    assert s == 0.75 and b.dtype is torch.bfloat16 and a.dtype is torch.bfloat16
+    assert torch.equal(a, f.a.to(torch.bfloat16)) and torch.equal(b, f.b.to(torch.bfloat16))
+    assert a.is_contiguous() and b.is_contiguous()
+    assert b.data_ptr() == a.data_ptr() + a.numel() * a.element_size()
+    b2, a2, _ = tr.staged_update(data, torch.bfloat16)
+    assert a2.data_ptr() == a.data_ptr() and b2.data_ptr() == b.data_ptr()
+    f.a.mul_(2.0)
+    b3, a3, _ = tr.staged_update(data, torch.bfloat16)
+    assert torch.equal(a3, f.a.to(torch.bfloat16)) and torch.equal(b3, b)
+    # another compute dtype is its own entry
+    _b4, a4, _ = tr.staged_update(data, torch.float32)
+    assert a4.dtype is torch.float32 and torch.equal(a4, f.a)
+
+
+def test_packed_staging_folds_strength_into_a_in_the_compute_dtype() -> None:
+    # k factors: concatenated along rank, each A slice times its strength in the
+    # compute dtype, strength 1.0 (P/lora.py:684-724)
+    g = torch.Generator().manual_seed(12)
+    f1 = ScaledLoRAFactor(torch.randn(3, 40, generator=g), torch.randn(24, 3, generator=g), 0.3)
+    f2 = ScaledLoRAFactor(torch.randn(5, 40, generator=g), torch.randn(24, 5, generator=g), -1.7)
+    f3 = ScaledLoRAFactor(torch.randn(2, 40, generator=g), torch.randn(24, 2, generator=g), 1.0)
+    tr = LoRATransform([f1, f2, f3], target_key="w")
+    b, a, s = tr.staged_update(torch.zeros(24, 40, dtype=torch.bfloat16), torch.bfloat16)
+    assert s == 1.0 and a.shape == (10, 40) and b.shape == (24, 10)
+    want_a = torch.cat([f.a.to(torch.bfloat16) * f.strength if f.strength != 1.0 else f.a.to(torch.bfloat16)
+                        for f in (f1, f2, f3)])
+    assert want_a.dtype is torch.bfloat16
+    assert torch.equal(a, want_a)
+    assert torch.equal(b, torch.cat([f.b for f in (f1, f2, f3)], dim=1).to(torch.bfloat16))
+    # folding in float32 first would round differently for some elements
+    assert not torch.equal(a[3:8], (f2.a * f2.strength).to(torch.bfloat16))
