@@ -338,9 +338,9 @@ class Api(Workload):
     """The 8B-shaped INT8 stack merged through the drop-in API, ``merge_lora(model, [(lora, 1.0)])``
     (P/merge.py:54-87): a module whose 224 weights are INT8 tensors on the GPU and a LoRA whose factors
     sit in pinned host memory, so every step resolves the targets, stages each target's factors with
-    one host-to-device copy and runs one merge launch per target."""
+    one host-to-device copy and merges them with one grouped launch."""
 
-    family = "rows"
+    family = "rows_stack"
 
     def __init__(self, layers: int, stochastic: bool) -> None:
         from torch import nn
@@ -365,8 +365,8 @@ class Api(Workload):
         self.lora = LoRA.from_state_dict(sd)
         self.name = "api"
         self.config = {"workload": f"{layers}-layer 8B-shaped INT8 stack ({7 * layers} targets) merged by "
-                                   "merge_lora(model, [(lora, 1.0)]): factors in pinned host memory, one staging "
-                                   "copy and one merge launch per target, "
+                                   "merge_lora(model, [(lora, 1.0)]): factors in pinned host memory, staged once per "
+                                   "target, one grouped merge launch, "
                                    f"{'stochastic' if stochastic else 'round-to-nearest'} requant",
                        "targets": 7 * layers, "rank": rank, "algorithmic_bytes_per_step": self.bytes_per_step}
 

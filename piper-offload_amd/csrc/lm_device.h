@@ -19,6 +19,12 @@
 #include <stdint.h>
 
 #define DEV __device__ __forceinline__
+// global (HBM) address space: global_load/store with immediate offsets.
+// Vector accesses through it use clang vector types (HIP's uint2/uint4
+// classes cannot be copied from another address space).
+#define LM_GLOBAL __attribute__((address_space(1)))
+typedef uint32_t lm_u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t lm_u32x4 __attribute__((ext_vector_type(4)));
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef _Float16 v4f16 __attribute__((ext_vector_type(4)));
@@ -173,6 +179,48 @@ DEV void philox10(uint64_t ctr, uint64_t seed, uint32_t (&c)[4]) {
     k1 += 0xBB67AE85u;
   }
 }
+// Philox4x32-10 of the counter (lo, hi) with output words 0 and 2
+// complemented: the last round's three-way XOR of those words becomes an
+// XNOR (v_bitop3_b32 0x69), so the complement costs nothing.  The stochastic
+// rounding rules below consume 65535 - h = ~h (16 bits), i.e. complemented
+// words.
+DEV void philox10_n02(uint32_t lo, uint32_t hi, uint64_t seed, uint32_t (&c)[4]) {
+  c[0] = lo;
+  c[1] = hi;
+  c[2] = 0;
+  c[3] = 0;
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t pb = (uint64_t)c[2] * 0xCD9E8D57u;
+    const uint64_t pa = (uint64_t)c[0] * 0xD2511F53u;
+    if (r < 9) {
+      c[0] = __builtin_amdgcn_bitop3_b32((uint32_t)(pb >> 32), c[1], k0, 0x96);
+      c[2] = __builtin_amdgcn_bitop3_b32((uint32_t)(pa >> 32), c[3], k1, 0x96);
+    } else {
+      c[0] = __builtin_amdgcn_bitop3_b32((uint32_t)(pb >> 32), c[1], k0, 0x69);
+      c[2] = __builtin_amdgcn_bitop3_b32((uint32_t)(pa >> 32), c[3], k1, 0x69);
+    }
+    c[1] = (uint32_t)pb;
+    c[3] = (uint32_t)pa;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+}
+// The 8 complemented Philox words (~w) of the 16 offsets 8 ctr .. 8 ctr + 15
+// for an even 32-bit counter ctr (offsets below 2^35): the second block's
+// counter is ctr | 1, and the high counter word is 0.
+DEV void sr_nwords16_even(uint64_t seed, uint32_t ctr, uint32_t (&nw)[8]) {
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi) {
+    uint32_t c[4];
+    philox10_n02(ctr | (uint32_t)gi, 0u, seed, c);
+    nw[4 * gi + 0] = c[0];
+    nw[4 * gi + 1] = ~c[1];
+    nw[4 * gi + 2] = c[2];
+    nw[4 * gi + 3] = ~c[3];
+  }
+}
 // 16-bit uniform integers h for offsets idx0 .. idx0+SPAN-1 (u = h * 2^-16)
 template <int SPAN>
 DEV void sr_bits(uint64_t seed, uint64_t idx0, uint32_t (&h)[SPAN]) {
@@ -288,7 +336,18 @@ DEV uint32_t sr_e2m1_word(const float* x, const uint32_t* w) {
   return (ev & 0x0f0f0f0fu) | ((od << 4) & 0xf0f0f0f0u);
 }
 // Four fp8 codes of x[0..3] (clamped by the caller), element 2k + i drawn
-// from half i of w[k]
+// from half i of the complemented Philox word nw[k] = ~w[k]
+template <int FMT>
+DEV uint32_t sr_fp8_nword(const float* x, const uint32_t* nw) {
+  uint32_t r = 0u;
+  const uint32_t n0 = nw[0], n1 = nw[1];
+  r = cvt_sr_fp8<FMT, 0>(r, x[0], sr_seed_lo(n0));
+  r = cvt_sr_fp8<FMT, 1>(r, x[1], sr_seed_hi(n0));
+  r = cvt_sr_fp8<FMT, 2>(r, x[2], sr_seed_lo(n1));
+  r = cvt_sr_fp8<FMT, 3>(r, x[3], sr_seed_hi(n1));
+  return r;
+}
+// the same from the Philox words themselves
 template <int FMT>
 DEV uint32_t sr_fp8_word(const float* x, const uint32_t* w) {
   uint32_t r = 0u;
@@ -308,6 +367,13 @@ DEV uint32_t sr_fp8(float v, uint32_t h, float /*limit*/) { return cvt_sr_fp8<FM
 
 
 // ---- packed helpers for the fast paths -----------------------------------
+// max(acc, |a|, |b|) in one v_max3_f32 (IEEE maxNum: a NaN operand is
+// ignored, as fmaxf does)
+DEV float max3_abs(float acc, float a, float b) {
+  float r;
+  asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(acc), "v"(a), "v"(b));
+  return r;
+}
 // two fp32 -> packed bf16 pair (RNE, v_cvt_pk_bf16_f32); low half = a
 DEV float bf16_lo(uint32_t w) { return u2f(w << 16); }
 DEV float bf16_hi(uint32_t w) { return u2f(w & 0xffff0000u); }
@@ -458,6 +524,24 @@ DEV void tile_delta(const uint16_t* __restrict__ at, int64_t mt_col0, int lane, 
     d[4 * t + 1] = acc[1];
     d[4 * t + 2] = acc[2];
     d[4 * t + 3] = acc[3];
+  }
+}
+
+// load_kchunks from a global-address-space pointer (global_load with an
+// immediate offset instead of flat loads with 64-bit address arithmetic)
+template <int NKC>
+DEV void load_kchunks_g(const LM_GLOBAL uint16_t* p, v4i16 (&out)[NKC]) {
+  if constexpr (NKC == 1) {
+    const lm_u32x2 w = *(const LM_GLOBAL lm_u32x2*)p;
+    out[0] = __builtin_bit_cast(v4i16, w);
+  } else {
+#pragma unroll
+    for (int h = 0; h < NKC / 2; ++h) {
+      const lm_u32x4 w = *(const LM_GLOBAL lm_u32x4*)(p + 8 * h);
+      const lm_u32x2 lo = {w.x, w.y}, hi = {w.z, w.w};
+      out[2 * h] = __builtin_bit_cast(v4i16, lo);
+      out[2 * h + 1] = __builtin_bit_cast(v4i16, hi);
+    }
   }
 }
 

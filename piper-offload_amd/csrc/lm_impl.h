@@ -504,11 +504,13 @@ __global__ __launch_bounds__(NW * 64) void k_rows_stack(const RowStackItem* __re
 // ---- fast per-row kernels -----------------------------------------------------
 // Specialization of rows_body for the production layouts: bf16 factors,
 // N % 64 == 0, INT8 symmetric with fp32 scales or scaled FP8 (fp32 scales).
-// Merged values stay packed bf16 (v_cvt_pk_bf16_f32) from pass 1 to pass 2,
-// the row amax is a packed 16-bit max over |bits|, round-to-nearest uses the
-// 1.5*2^23 magic add, INT8 stochastic rounding works on the integer grid (an
-// exact reformulation of the reference's u < p selection) and FP8 stochastic
-// rounding uses the hardware conversions (sr_fp8_word).
+// Merged values stay packed bf16 (v_cvt_pk_bf16_f32) from pass 1 to pass 2;
+// the row amax is a running fp32 max of |merged| before the bf16 rounding
+// (rounding is monotone, so bf16(max |m|) = max |bf16(m)|), one v_max3 per
+// pair; round-to-nearest uses the 1.5*2^23 magic add; INT8 stochastic
+// rounding works on the integer grid (an exact reformulation of the
+// reference's u < p selection) and FP8 stochastic rounding uses the hardware
+// conversions (sr_fp8_nword).
 // Global inputs of one 64-column macro tile for one lane: 16 codes of its row
 // and the 4 A^T operands of its MFMAs.  Loading is split from the arithmetic
 // so that a wave can have several tiles' loads in flight.
@@ -518,31 +520,68 @@ struct FastTileIn {
   v4i16 aop[4][NKC];
 };
 
+// A lane's addresses, computed once per row group, as 32-bit offsets from the
+// wave-uniform tensor bases (the fast kernels need M N < 2^32): tile mt adds
+// 64 mt code bytes, 64 mt RPAD A^T elements and 8 mt Philox blocks, all
+// wave-uniform, so a tile's loads and store are global_load/store with a
+// scalar base, one offset register and an immediate.
+struct FastLane {
+  const LM_GLOBAL uint8_t* q;    // codes (uniform)
+  LM_GLOBAL uint8_t* out;        // output codes (uniform)
+  const LM_GLOBAL uint16_t* at;  // prepared A^T (uniform)
+  uint32_t off;                  // (clamped row) N + 16 (lane >> 4)
+  uint32_t aoff;                 // the lane's A^T operand offset in tile 0
+  uint32_t ctr;                  // Philox counter of the lane's first offset in tile 0 (even)
+};
+
 template <int NKC>
-__device__ __forceinline__ void fast_load_tile(const RowArgs& a, int64_t rowc, int mt, int lane,
-                                               FastTileIn<NKC>& t) {
+__device__ __forceinline__ FastLane fast_lane(const RowArgs& a, int64_t rowc, int lane) {
   constexpr int RPAD = NKC * 16;
   const int p = lane & 15, g = lane >> 4;
-  t.raw = *(const uint4*)((const uint8_t*)a.q + rowc * a.N + (int64_t)mt * 64 + 16 * g);
-  const int64_t colbase = (int64_t)mt * 64 + 16 * (p >> 2) + (p & 3);
-#pragma unroll
-  for (int k = 0; k < 4; ++k) load_kchunks<NKC>(a.at + (colbase + 4 * k) * RPAD + g * (NKC * 4), t.aop[k]);
+  FastLane L;
+  L.q = (const LM_GLOBAL uint8_t*)a.q;
+  L.out = (LM_GLOBAL uint8_t*)a.q_out;
+  L.at = (const LM_GLOBAL uint16_t*)a.at;
+  L.off = (uint32_t)rowc * (uint32_t)a.N + 16u * (uint32_t)g;
+  L.aoff = (uint32_t)((16 * (p >> 2) + (p & 3)) * RPAD + g * (NKC * 4));
+  // N % 64 == 0: off / 8 is even, so the lane's second Philox block (offsets
+  // +8 .. +15) is counter | 1; rows past M never store, so their counter is moot
+  L.ctr = L.off >> 3;
+  return L;
 }
 
+__device__ __forceinline__ uint4 fast_load_codes(const FastLane& L, int mt) {
+  const lm_u32x4 raw = *(const LM_GLOBAL lm_u32x4*)(L.q + (uint32_t)(mt * 64) + L.off);
+  return make_uint4(raw.x, raw.y, raw.z, raw.w);
+}
+template <int NKC>
+__device__ __forceinline__ void fast_load_aop(const FastLane& L, int mt, v4i16 (&aop)[4][NKC]) {
+  constexpr int RPAD = NKC * 16;
+  const LM_GLOBAL uint16_t* at = L.at + (uint32_t)(mt * (64 * RPAD)) + L.aoff;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, aop[k]);
+}
+template <int NKC>
+__device__ __forceinline__ void fast_load_tile(const FastLane& L, int mt, FastTileIn<NKC>& t) {
+  t.raw = fast_load_codes(L, mt);
+  fast_load_aop<NKC>(L, mt, t.aop);
+}
+
+// merged bf16 pairs of one tile into out[8]; amax = max(amax, |merged|) in fp32
 template <int KIND, int NKC>
-__device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const FastTileIn<NKC>& in,
+__device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const uint4& raw, const v4i16 (&aop)[4][NKC],
                                                  const v4i16 (&bop)[NKC], float s_in,
-                                                 uint32_t (&out)[8]) {
+                                                 uint32_t (&out)[8], float& amax) {
   float d[16];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const v4f32 acc = mfma_chain<NKC, false>(in.aop[k], bop);
+    const v4f32 acc = mfma_chain<NKC, false>(aop[k], bop);
     d[4 * k + 0] = acc[0];
     d[4 * k + 1] = acc[1];
     d[4 * k + 2] = acc[2];
     d[4 * k + 3] = acc[3];
   }
-  const uint32_t w[4] = {in.raw.x, in.raw.y, in.raw.z, in.raw.w};
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const uint32_t word = w[k >> 1];
@@ -559,6 +598,7 @@ __device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const FastTil
     const float m0 = __builtin_fmaf(d[2 * k], a.strength, bf16r(x0));
     const float m1 = __builtin_fmaf(d[2 * k + 1], a.strength, bf16r(x1));
     out[k] = pack_bf16x2(m0, m1);
+    amax = max3_abs(amax, m0, m1);
   }
 }
 
@@ -566,14 +606,11 @@ __device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const FastTil
 // the two-term reciprocal's low part would be subnormal (weights above 1e30);
 // those waves use the three-instruction quotient, exact for every normal scale.
 template <int KIND, bool SR>
-__device__ __forceinline__ void fast_quant_store(const RowArgs& a, int64_t row, bool rok, int mt, int lane,
+__device__ __forceinline__ void fast_quant_store(const RowArgs& a, const FastLane& L, bool rok, int mt,
                                                  const RowQP& qp, const uint32_t (&w)[8], bool wide) {
   if (!rok) return;
-  const int64_t N = a.N;
-  const int64_t c0 = (int64_t)mt * 64 + 16 * (lane >> 4);
-  // N % 64 == 0 and c0 % 16 == 0: the lane's 16 offsets start a Philox block
-  uint32_t rw[8];
-  if constexpr (SR) sr_words_aligned<16>(a.seed, (uint64_t)(row * N + c0), rw);
+  uint32_t nw[8];  // complemented Philox words: 65535 - h in each half
+  if constexpr (SR) sr_nwords16_even(a.seed, L.ctr + 8u * (uint32_t)mt, nw);
   uint32_t out[4];
   if constexpr (KIND == K_INT8) {
     uint32_t y[16];
@@ -609,8 +646,7 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, int64_t row, 
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const uint32_t tneg = (uint32_t)cvt_flr_neg(y16[j]);  // -ceil(Y)
-        const uint32_t nw = ~rw[j >> 1];                       // 65535 - h in each half
-        y[j] = (j & 1) ? (nw >> 16) - tneg : sub_lo16(nw, tneg);
+        y[j] = (j & 1) ? (nw[j >> 1] >> 16) - tneg : sub_lo16(nw[j >> 1], tneg);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) out[i] = pack_byte2s(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
@@ -626,34 +662,32 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, int64_t row, 
       for (int i = 0; i < 4; ++i) out[i] = pack_low_bytes(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
     }
   } else {
-    constexpr float L = FmtLimit<KIND>::v;
+    constexpr float L8 = FmtLimit<KIND>::v;
     constexpr int F = FmtLimit<KIND>::fmt;
     float x[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
-      x[j] = __builtin_amdgcn_fmed3f(div_rn(m, qp.s, qp.rcp), -L, L);
+      x[j] = __builtin_amdgcn_fmed3f(div_rn(m, qp.s, qp.rcp), -L8, L8);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if constexpr (SR) out[i] = sr_fp8_word<F>(x + 4 * i, rw + 2 * i);
+      if constexpr (SR) out[i] = sr_fp8_nword<F>(x + 4 * i, nw + 2 * i);
       else out[i] = fp8_pack4<F>(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
     }
   }
-  *(uint4*)((uint8_t*)a.q_out + row * N + c0) = make_uint4(out[0], out[1], out[2], out[3]);
+  *(LM_GLOBAL lm_u32x4*)(L.out + (uint32_t)(mt * 64) + L.off) = lm_u32x4{out[0], out[1], out[2], out[3]};
 }
 
-// Tiles whose loads a wave keeps in flight ahead of the arithmetic.  One
-// FastTileIn holds 12, 20 or 36 VGPRs for NKC 1, 2, 4; rank 16 with 4 tiles in
-// flight stays under 128 VGPRs (two 512-thread workgroups per CU), which
-// measured faster on the 8B stack than 2 or 8 tiles.
-template <int NKC>
+// Tiles of A^T operands a wave keeps in flight ahead of the arithmetic (the
+// codes of the cached tiles are all requested up front).  One tile's operands
+// hold 8, 16 or 32 VGPRs for NKC 1, 2, 4.
+template <int NKC, bool SR>
 constexpr int fast_prefetch() { return NKC == 1 ? 4 : 2; }
 
-template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC>()>
+template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>()>
 __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
-  __shared__ float sh_mx[NW][16];
-  __shared__ float sh_qp[4][16];
+  __shared__ float sh_mx[16][NW];
   constexpr int PF = PF_ < CACHE ? PF_ : CACHE;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int64_t row = row0 + rl;
@@ -661,22 +695,27 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   // rows past M load row M-1 (valid memory); their results are never stored
   const int64_t rowc = rok ? row : a.M - 1;
   const int ntiles = (int)(a.N >> 6);
+  const FastLane L = fast_lane<NKC>(a, rowc, lane);
   v4i16 bop[NKC];
   load_bop<NKC>(a.bp, row, lane, bop);
-  const float s_in = rok ? ((const float*)a.scale)[row] : 0.0f;
+  const float s_in = rok ? ((const LM_GLOBAL float*)a.scale)[row] : 0.0f;
   uint32_t cache[CACHE][8];
-  uint32_t pmax = 0u;
+  float amax = 0.0f;
   if (wave + (CACHE - 1) * NW < ntiles) {
-    // every cache slot holds a tile: branch-free, PF tiles of loads in flight
-    FastTileIn<NKC> in[CACHE];
+    // every cache slot holds a tile: branch-free.  The codes of all CACHE
+    // tiles (4 VGPRs each) are requested at once, so a wave keeps CACHE KiB of
+    // HBM reads in flight; the A^T operands (L2-resident, 4 NKC VGPRs per MFMA)
+    // run PF tiles ahead.
+    uint4 raw[CACHE];
+    v4i16 aop[PF][4][NKC];
 #pragma unroll
-    for (int i = 0; i < PF; ++i) fast_load_tile<NKC>(a, rowc, wave + i * NW, lane, in[i]);
+    for (int i = 0; i < CACHE; ++i) raw[i] = fast_load_codes(L, wave + i * NW);
+#pragma unroll
+    for (int i = 0; i < PF; ++i) fast_load_aop<NKC>(L, wave + i * NW, aop[i]);
 #pragma unroll
     for (int i = 0; i < CACHE; ++i) {
-      if (i + PF < CACHE) fast_load_tile<NKC>(a, rowc, wave + (i + PF) * NW, lane, in[i + PF]);
-      fast_merged_tile<KIND, NKC>(a, in[i], bop, s_in, cache[i]);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) pmax = pk_max_u16(pmax, cache[i][k] & 0x7fff7fffu);
+      fast_merged_tile<KIND, NKC>(a, raw[i], aop[i % PF], bop, s_in, cache[i], amax);
+      if (i + PF < CACHE) fast_load_aop<NKC>(L, wave + (i + PF) * NW, aop[i % PF]);
     }
   } else {
 #pragma unroll
@@ -684,10 +723,8 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
       const int mt = wave + i * NW;
       if (mt < ntiles) {
         FastTileIn<NKC> in;
-        fast_load_tile<NKC>(a, rowc, mt, lane, in);
-        fast_merged_tile<KIND, NKC>(a, in, bop, s_in, cache[i]);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) pmax = pk_max_u16(pmax, cache[i][k] & 0x7fff7fffu);
+        fast_load_tile<NKC>(L, mt, in);
+        fast_merged_tile<KIND, NKC>(a, in.raw, in.aop, bop, s_in, cache[i], amax);
       }
     }
   }
@@ -695,82 +732,76 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   // re-reads the final tile instead of branching)
   if (wave + CACHE * NW < ntiles) {
     FastTileIn<NKC> cur;
-    fast_load_tile<NKC>(a, rowc, wave + CACHE * NW, lane, cur);
+    fast_load_tile<NKC>(L, wave + CACHE * NW, cur);
     for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW) {
       FastTileIn<NKC> nxt;
-      fast_load_tile<NKC>(a, rowc, mt + NW < ntiles ? mt + NW : mt, lane, nxt);
+      fast_load_tile<NKC>(L, mt + NW < ntiles ? mt + NW : mt, nxt);
       uint32_t t[8];
-      fast_merged_tile<KIND, NKC>(a, cur, bop, s_in, t);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) pmax = pk_max_u16(pmax, t[k] & 0x7fff7fffu);
+      fast_merged_tile<KIND, NKC>(a, cur.raw, cur.aop, bop, s_in, t, amax);
       cur = nxt;
     }
   }
-  float vmx = __builtin_fmaxf(bf16_lo(pmax), bf16_hi(pmax));
+  float vmx = bf16r(amax);  // = max |bf16(merged)| of the lane
   vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, 16));
   vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, 32));
-  if ((lane >> 4) == 0) sh_mx[wave][rl] = vmx;
+  if ((lane >> 4) == 0) sh_mx[rl][wave] = vmx;
   __syncthreads();
-  if (threadIdx.x < 16) {
-    const int t = threadIdx.x;
-    float mx = 0.0f;
-    for (int w = 0; w < NW; ++w) mx = __builtin_fmaxf(mx, sh_mx[w][t]);
-    const int64_t r = row0 + t;
-    float stored;
-    RowQP qp;
-    if constexpr (KIND == K_INT8) {
-      int zp;
-      qp = int8_qparams<BF16, F32, false>(-mx, mx, a.qmin, a.qmax, stored, zp);
-      if (r < a.M) ((float*)a.scale_out)[r] = stored;
-      if (r < a.M && a.zp_out) a.zp_out[r] = 0;
-      if constexpr (SR) {
-        // 1/s as hi + lo: hi = RN(1/s), lo = (1 - s hi) hi (the fma residual is
-        // exact), together within ~2^-47 of 1/s; both scaled by 65536
-        const float lo = __builtin_fmaf(-qp.s, qp.rcp, 1.0f) * qp.rcp;
-        qp.inv = qp.rcp * 65536.0f;
-        qp.rcp = lo * 65536.0f;
-      }
-    } else {
-      qp = fp8_qparams<BF16, KIND>(mx, stored);
-      if (r < a.M) ((float*)a.scale_out)[r] = stored;
-    }
-    sh_qp[0][t] = qp.s;
-    sh_qp[1][t] = qp.inv;
-    sh_qp[2][t] = qp.rcp;
-    sh_qp[3][t] = qp.zp;
-  }
-  __syncthreads();
+  // Every lane derives its row's qparams from the NW wave maxima itself (the
+  // lanes of a row agree), so no second barrier and no single-wave section.
+  float mx = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) mx = __builtin_fmaxf(mx, sh_mx[rl][w]);
+  const bool writer = wave == 0 && (lane >> 4) == 0 && rok;  // one scale store per row
+  float stored;
   RowQP qp;
-  qp.s = sh_qp[0][rl];
-  qp.inv = sh_qp[1][rl];
-  qp.rcp = sh_qp[2][rl];
-  qp.zp = sh_qp[3][rl];
+  if constexpr (KIND == K_INT8) {
+    int zp;
+    qp = int8_qparams<BF16, F32, false>(-mx, mx, a.qmin, a.qmax, stored, zp);
+    if (writer) ((float*)a.scale_out)[row] = stored;
+    if (writer && a.zp_out) a.zp_out[row] = 0;
+    if constexpr (SR) {
+      // 1/s as hi + lo: hi = RN(1/s), lo = (1 - s hi) hi (the fma residual is
+      // exact), together within ~2^-47 of 1/s; both scaled by 65536
+      const float lo = __builtin_fmaf(-qp.s, qp.rcp, 1.0f) * qp.rcp;
+      qp.inv = qp.rcp * 65536.0f;
+      qp.rcp = lo * 65536.0f;
+    }
+  } else {
+    qp = fp8_qparams<BF16, KIND>(mx, stored);
+    if (writer) ((float*)a.scale_out)[row] = stored;
+  }
   const bool wide = KIND == K_INT8 && SR && __any(qp.s > 0x1p100f);
 #pragma unroll
   for (int i = 0; i < CACHE; ++i) {
     const int mt = wave + i * NW;
-    if (mt < ntiles) fast_quant_store<KIND, SR>(a, row, rok, mt, lane, qp, cache[i], wide);
+    if (mt < ntiles) fast_quant_store<KIND, SR>(a, L, rok, mt, qp, cache[i], wide);
   }
   if (wave + CACHE * NW < ntiles) {
     FastTileIn<NKC> cur;
-    fast_load_tile<NKC>(a, rowc, wave + CACHE * NW, lane, cur);
+    fast_load_tile<NKC>(L, wave + CACHE * NW, cur);
     for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW) {
       FastTileIn<NKC> nxt;
-      fast_load_tile<NKC>(a, rowc, mt + NW < ntiles ? mt + NW : mt, lane, nxt);
+      fast_load_tile<NKC>(L, mt + NW < ntiles ? mt + NW : mt, nxt);
       uint32_t t[8];
-      fast_merged_tile<KIND, NKC>(a, cur, bop, s_in, t);
-      fast_quant_store<KIND, SR>(a, row, rok, mt, lane, qp, t, wide);
+      float unused = 0.0f;
+      fast_merged_tile<KIND, NKC>(a, cur.raw, cur.aop, bop, s_in, t, unused);
+      fast_quant_store<KIND, SR>(a, L, rok, mt, qp, t, wide);
       cur = nxt;
     }
   }
 }
 
-template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC>()>
-__global__ __launch_bounds__(NW * 64) void k_rows_fast(RowArgs a) {
+// Rank 16 with the 8-tile cache fits 128 VGPRs: two 512-thread workgroups per
+// CU (4 waves per SIMD), which the bound below holds the compiler to.
+template <int NKC, int CACHE>
+constexpr int fast_min_waves() { return NKC == 1 && CACHE <= 8 ? 4 : 1; }
+
+template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>()>
+__global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_rows_fast(RowArgs a) {
   rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_>(a, (int64_t)blockIdx.x * 16);
 }
-template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC>()>
-__global__ __launch_bounds__(NW * 64) void k_rows_fast_stack(const RowStackItem* __restrict__ items, int count) {
+template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>()>
+__global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_rows_fast_stack(const RowStackItem* __restrict__ items, int count) {
   int lo = 0, hi = count - 1;
   const int64_t t = blockIdx.x;
   while (lo < hi) {
@@ -1406,31 +1437,47 @@ static int run_rows_nkc(const RowArgs& a, int nkc, int scale_dt, hipStream_t st)
 }
 
 // fast path eligibility: bf16 factors, N % 64 == 0, INT8 symmetric fp32 scales or FP8
-static inline bool rows_fast_ok(int kind, int cd, int sdt, bool asym, int nkc, int64_t N) {
-  return cd == LM_BF16 && nkc > 0 && (N % 64) == 0 && (kind != K_INT8 || (!asym && sdt == LM_F32));
+// The fast kernels address codes, A^T operands and Philox counters with 32-bit
+// offsets: M N < 2^32 (4 GiB of codes per tensor) and N RPAD < 2^32.
+static inline bool rows_fast_ok(int kind, int cd, int sdt, bool asym, int nkc, int64_t M, int64_t N) {
+  return cd == LM_BF16 && nkc > 0 && (N % 64) == 0 && (kind != K_INT8 || (!asym && sdt == LM_F32)) &&
+         M * N < (INT64_C(1) << 32) && N * 64 < (INT64_C(1) << 32);
 }
 
 // Rows with more macro tiles per wave than the register cache holds are
-// merged twice (the surplus tiles are recomputed in pass 2).  A 16-tile cache
-// removes most of that: measured on MI355X it pays for rank 64 (FP8
-// [8192, 8192] r64: RTN 0.124 -> 0.083 ms, SR 0.137 -> 0.115 ms) and for
-// round-to-nearest long rows (down_proj RTN -16%), while stochastic rounding
-// at rank <= 32 is VALU-bound and loses the occupancy it costs.
+// merged twice (the surplus tiles are recomputed in pass 2).  Two remedies,
+// measured on MI355X:
+// * rank 16 (128 VGPRs): 16-wave workgroups halve the tiles per wave at the
+//   same occupancy (4 waves per SIMD); 8B down_proj rows [4096, 14336]:
+//   RTN 1.44 -> 1.21 ms, SR 1.51 -> 1.46 ms for the 32 layers;
+// * a 16-tile cache: pays for rank 64 (FP8 [8192, 8192] r64: RTN 0.124 ->
+//   0.083 ms, SR 0.137 -> 0.115 ms) and for round-to-nearest at rank 32, while
+//   stochastic rounding at rank 32 is VALU-bound and loses the occupancy it
+//   costs (those rows recompute).
 static constexpr int ROW_DEEP_CACHE = 16;
-static inline bool rows_deep_cache(int nkc, bool sr, int64_t N) {
+static constexpr int ROW_NW_WIDE = 16;
+enum RowsMode : int { ROWS_REGULAR = 0, ROWS_WIDE = 1, ROWS_DEEP = 2 };
+static inline int rows_long_mode(int nkc, bool sr, int64_t N) {
   const int64_t tpw = (N / 64 + ROW_NW - 1) / ROW_NW;
-  return tpw > ROW_CACHE && (nkc == 4 || !sr);
+  if (tpw <= ROW_CACHE) return ROWS_REGULAR;
+  if (nkc == 1) return ROWS_WIDE;
+  return (nkc == 4 || !sr) ? ROWS_DEEP : ROWS_REGULAR;
 }
 
 template <int KIND, bool SR, int NKC>
 static int launch_rows_fast(const RowArgs& a, hipStream_t st) {
-  dim3 grid((unsigned)((a.M + 15) / 16)), block(ROW_NW * 64);
+  const dim3 grid((unsigned)((a.M + 15) / 16));
   TimedLaunch timed("rows", st);
-  if (rows_deep_cache(NKC, SR, a.N)) {
+  const int mode = rows_long_mode(NKC, SR, a.N);
+  if (mode == ROWS_WIDE) {
+    if constexpr (NKC == 1)
+      hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW_WIDE, ROW_CACHE>), grid, dim3(ROW_NW_WIDE * 64), 0, st, a);
+  } else if (mode == ROWS_DEEP) {
     if constexpr (NKC == 4 || !SR)
-      hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_DEEP_CACHE, NKC == 4 ? 1 : 2>), grid, block, 0, st, a);
+      hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_DEEP_CACHE, NKC == 4 ? 1 : 2>), grid,
+                         dim3(ROW_NW * 64), 0, st, a);
   } else {
-    hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_CACHE>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_CACHE>), grid, dim3(ROW_NW * 64), 0, st, a);
   }
   LAUNCH_CHECK();
   return LM_OK;
@@ -1438,7 +1485,7 @@ static int launch_rows_fast(const RowArgs& a, hipStream_t st) {
 
 template <int KIND, bool FROM_DENSE>
 static int run_rows(const RowArgs& a, int cd, int sdt, bool asym, bool sr, int nkc, hipStream_t st) {
-  if (!FROM_DENSE && rows_fast_ok(KIND, cd, sdt, asym, nkc, a.N)) {
+  if (!FROM_DENSE && rows_fast_ok(KIND, cd, sdt, asym, nkc, a.M, a.N)) {
     if (sr) {
       NKC_SWITCH(nkc_bucket(nkc), return (launch_rows_fast<KIND, true, NKC_>(a, st)));
     } else {

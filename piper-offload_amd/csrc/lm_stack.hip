@@ -80,11 +80,11 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
   }
   const bool sr = rounding_mode == LM_ROUND_STOCHASTIC;
   bool fast = true;
-  for (int i = 0; i < count; ++i) fast = fast && rows_fast_ok(K_INT8, cd, scale_dtype, false, nkc_max, items[i].N);
+  for (int i = 0; i < count; ++i) fast = fast && rows_fast_ok(K_INT8, cd, scale_dtype, false, nkc_max, items[i].M, items[i].N);
   // fast kernels: items whose rows want the deep register cache go to a
   // second launch; each launch numbers its 16-row groups from 0
   int n_regular = 0;
-  for (int i = 0; i < count; ++i) n_regular += (fast && rows_deep_cache(nkc_max, sr, items[i].N)) ? 0 : 1;
+  for (int i = 0; i < count; ++i) n_regular += (fast && rows_long_mode(nkc_max, sr, items[i].N) != ROWS_REGULAR) ? 0 : 1;
   int64_t tiles[2] = {0, 0};
   int slot[2] = {0, n_regular};
   for (int i = 0; rc == LM_OK && i < count; ++i) {
@@ -92,7 +92,7 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
     if (s.lora.dtype != cd) rc = fail(LM_EUNSUPPORTED, "all stack items must share one factor dtype");
     if (s.M <= 0 || s.N <= 0 || !s.q || !s.scale || !s.q_out || !s.scale_out)
       rc = fail(LM_EINVAL, "stack item %d has an invalid shape or null pointer", i);
-    const int grp = (fast && rows_deep_cache(nkc_max, sr, s.N)) ? 1 : 0;
+    const int grp = (fast && rows_long_mode(nkc_max, sr, s.N) != ROWS_REGULAR) ? 1 : 0;
     RowStackItem& r = rows[slot[grp]++];
     RowArgs& a = r.a;
     a.q = s.q;
@@ -135,9 +135,15 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
         const dim3 grid((unsigned)tiles[1]);
         const RowStackItem* d1 = d0 + n_regular;
         const int n_deep = count - n_regular;
-#define RD(SR_, PF_) NKC_SWITCH(nkc_bucket(nkc_max), if constexpr (NKC_ == 4 || !SR_) hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, ROW_DEEP_CACHE, PF_>), grid, block, 0, st, d1, n_deep))
-        if (sr) { RD(true, 1); } else if (nkc_max == 4) { RD(false, 1); } else { RD(false, 2); }
+        if (nkc_bucket(nkc_max) == 1) {  // ROWS_WIDE: 16-wave workgroups
+          const dim3 wblock(ROW_NW_WIDE * 64);
+          if (sr) hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, true, 1, ROW_NW_WIDE, ROW_CACHE>), grid, wblock, 0, st, d1, n_deep);
+          else hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, false, 1, ROW_NW_WIDE, ROW_CACHE>), grid, wblock, 0, st, d1, n_deep);
+        } else {  // ROWS_DEEP
+#define RD(SR_, PF_) NKC_SWITCH(nkc_bucket(nkc_max), if constexpr (NKC_ != 1 && (NKC_ == 4 || !SR_)) hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, ROW_DEEP_CACHE, PF_>), grid, block, 0, st, d1, n_deep))
+          if (sr) { RD(true, 1); } else if (nkc_max == 4) { RD(false, 1); } else { RD(false, 2); }
 #undef RD
+        }
       }
     } else {
       const dim3 grid((unsigned)tiles[0]);
