@@ -134,8 +134,11 @@ size_t lm_stack_workspace_extra(int32_t count);
 
 /* ---------------- INT8 (TorchAO Int8Tensor) ---------------------------
  * q: int8 [M, N]; scale: [M*N/group] in scale_dtype (LM_F32/LM_BF16);
- * zero_point: int8 [M*N/group] or NULL (symmetric).  group = N (per-row)
- * or M*N (per-tensor).  Outputs may alias inputs (in-place merge). */
+ * zero_point: int8 [M*N/group] or NULL (symmetric).  group = N (per-row),
+ * M*N (per-tensor) or g < N per-group (TorchAO block_size (1, g): 16, 32 or a
+ * multiple of 64 dividing N; qparams [M, N/g] row-major), as the Triton
+ * path's _block_numel (P/_triton_int8_lora.py:251-264).  Outputs may alias
+ * inputs (in-place merge). */
 int lm_int8_merge(const int8_t* q, const void* scale, const int8_t* zero_point, int8_t* q_out, void* scale_out,
                   int8_t* zero_point_out, int64_t M, int64_t N, int64_t group, int32_t scale_dtype, int32_t asymmetric,
                   int32_t reduce_range, const lm_lora* lora, const lm_rounding* rounding, void* workspace,
@@ -150,7 +153,8 @@ int lm_int8_dequant(const int8_t* q, const void* scale, const int8_t* zero_point
 
 /* ---------------- scaled FP8 (TorchAO Float8Tensor) -------------------
  * q: fp8 [M, N] (fp8_dtype LM_E4M3/LM_E5M2); scale: fp32 [M*N/group];
- * group = N (per-row) or M*N (per-tensor). */
+ * group = N (per-row), M*N (per-tensor) or g < N per-group (16, 32 or a
+ * multiple of 64 dividing N; P/float8_adapter.py:63-98). */
 int lm_fp8_merge(const uint8_t* q, const float* scale, uint8_t* q_out, float* scale_out, int64_t M, int64_t N,
                  int64_t group, int32_t fp8_dtype, const lm_lora* lora, const lm_rounding* rounding, void* workspace,
                  size_t workspace_bytes, void* stream);

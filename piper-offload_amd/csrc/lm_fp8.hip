@@ -1,5 +1,5 @@
 // lm_fp8.hip -- scaled FP8 (TorchAO Float8Tensor) entry points.
-#include "lm_impl.h"
+#include "lm_group.h"
 
 // ---------------------------------------------------------------------------
 // FP8
@@ -7,8 +7,11 @@
 static int check_fp8_layout(int64_t M, int64_t N, int64_t group, int32_t fmt) {
   if (M <= 0 || N <= 0) return fail(LM_EINVAL, "FP8 merge requires a non-empty weight");
   if (fmt != LM_E4M3 && fmt != LM_E5M2) return fail(LM_EUNSUPPORTED, "FP8 storage must be e4m3fn or e5m2");
-  if (group != N && group != M * N)
-    return fail(LM_EUNSUPPORTED, "FP8 supports per-row and per-tensor layouts, got group %lld", (long long)group);
+  if (group != N && group != M * N && !group_size_ok(N, group))
+    return fail(LM_EUNSUPPORTED,
+                "FP8 supports per-row, per-tensor and per-group layouts (group 16, 32 or a multiple of 64 dividing "
+                "N), got group %lld for N=%lld",
+                (long long)group, (long long)N);
   return LM_OK;
 }
 
@@ -24,7 +27,7 @@ static int fp8_common(const uint8_t* q, const float* scale, const void* dense, i
   if ((rc = setup(c, M, N, lora, ws, wsb, stream))) return rc;
   const int cd = lora ? lora->dtype : dense_dt;
   const bool sr = is_sr(rnd);
-  if (group == N) {
+  if (group == N || group != M * N) {  // per-row, or per-group
     RowArgs a;
     memset(&a, 0, sizeof a);
     a.q = q;
@@ -38,6 +41,14 @@ static int fp8_common(const uint8_t* q, const float* scale, const void* dense, i
     a.N = N;
     a.strength = lora ? lora->strength : 0.0f;
     a.seed = seed_of(rnd);
+    if (group != N) {
+      if (fmt == LM_E4M3) {
+        if (dense) return run_groups<K_E4M3, true>(a, group, cd, LM_F32, false, sr, 0, c.st);
+        return run_groups<K_E4M3, false>(a, group, cd, LM_F32, false, sr, c.nkc, c.st);
+      }
+      if (dense) return run_groups<K_E5M2, true>(a, group, cd, LM_F32, false, sr, 0, c.st);
+      return run_groups<K_E5M2, false>(a, group, cd, LM_F32, false, sr, c.nkc, c.st);
+    }
     if (fmt == LM_E4M3) {
       if (dense) return run_rows<K_E4M3, true>(a, cd, LM_F32, false, sr, 0, c.st);
       return run_rows<K_E4M3, false>(a, cd, LM_F32, false, sr, c.nkc, c.st);

@@ -947,8 +947,8 @@ __device__ __forceinline__ void blk_load_base(const BlkArgs& a, int64_t row, boo
 #pragma unroll
       for (int j = 0; j < 16; ++j) base[j] = (c0 + j < N) ? val_dt<CD>(p[j]) : 0.0f;
     }
-  } else {  // B_INT8 / B_E4M3 / B_E5M2 with per-row or per-tensor scale
-    const int64_t qi = (a.group == N) ? row : 0;
+  } else {  // B_INT8 / B_E4M3 / B_E5M2: per-row, per-tensor or per-group scale (16 | group)
+    const int64_t qi = a.group == N ? row : (a.group == a.M * N ? 0 : (row * N + c0) / a.group);
     const float s = load_scalar(a.scale, qi, a.scale_dt);
     float z = 0.0f;
     if constexpr (F == B_INT8) z = a.aux ? (float)((const int8_t*)a.aux)[qi] : 0.0f;

@@ -1,5 +1,5 @@
 // lm_int8.hip -- INT8 (TorchAO Int8Tensor) merge / requant / dequant entry points.
-#include "lm_impl.h"
+#include "lm_group.h"
 
 // ---------------------------------------------------------------------------
 // INT8
@@ -8,9 +8,11 @@ static int check_int8_layout(int64_t M, int64_t N, int64_t group, int32_t scale_
   if (M <= 0 || N <= 0) return fail(LM_EINVAL, "INT8 merge requires a non-empty weight, got [%lld, %lld]", (long long)M, (long long)N);
   if (scale_dtype != LM_F32 && scale_dtype != LM_BF16)
     return fail(LM_EUNSUPPORTED, "INT8 scales must be float32 or bfloat16, got dtype id %d", scale_dtype);
-  if (group != N && group != M * N)
-    return fail(LM_EUNSUPPORTED, "INT8 supports per-row (group=N) and per-tensor (group=M*N) layouts, got group %lld",
-                (long long)group);
+  if (group != N && group != M * N && !group_size_ok(N, group))
+    return fail(LM_EUNSUPPORTED,
+                "INT8 supports per-row (group=N), per-tensor (group=M*N) and per-group layouts (group 16, 32 or a "
+                "multiple of 64 dividing N), got group %lld for N=%lld",
+                (long long)group, (long long)N);
   return LM_OK;
 }
 
@@ -28,7 +30,7 @@ static int int8_common(const int8_t* q, const void* scale, const int8_t* zp, con
   const int cd = lora ? lora->dtype : dense_dt;
   const bool sr = is_sr(rnd);
   const int qmin = reduce_range ? -64 : -128, qmax = reduce_range ? 63 : 127;
-  if (group == N) {
+  if (group == N || group != M * N) {  // per-row, or per-group
     RowArgs a;
     memset(&a, 0, sizeof a);
     a.q = q;
@@ -46,6 +48,10 @@ static int int8_common(const int8_t* q, const void* scale, const int8_t* zp, con
     a.qmin = qmin;
     a.qmax = qmax;
     a.seed = seed_of(rnd);
+    if (group != N) {
+      if (dense) return run_groups<K_INT8, true>(a, group, cd, sdt, asym != 0, sr, 0, c.st);
+      return run_groups<K_INT8, false>(a, group, cd, sdt, asym != 0, sr, c.nkc, c.st);
+    }
     if (dense) return run_rows<K_INT8, true>(a, cd, sdt, asym != 0, sr, 0, c.st);
     return run_rows<K_INT8, false>(a, cd, sdt, asym != 0, sr, c.nkc, c.st);
   }

@@ -102,17 +102,32 @@ def _same_device(label: str, *tensors: torch.Tensor | None) -> torch.device:
 # ---------------------------------------------------------------------------
 # INT8
 # ---------------------------------------------------------------------------
+def _group_ok(cols: int, group: int) -> bool:
+    """Per-group sizes the group kernels take: 16, 32 or a multiple of 64, dividing the columns."""
+    return 0 < group < cols and cols % group == 0 and (group in (16, 32) or group % 64 == 0)
+
+
 def _int8_group(shape: tuple[int, int], block_size: tuple[int, ...]) -> int:
+    """Elements per qparam: per-tensor, per-row or per-group (1, g) layouts (P/_triton_int8_lora.py:251-264)."""
     rows, cols = shape
     block_size = tuple(block_size)
     if block_size == (rows, cols):
         return rows * cols
     if block_size == (1, cols):
         return cols
+    if len(block_size) == 2 and block_size[0] == 1 and _group_ok(cols, block_size[1]):
+        return block_size[1]
     raise ValueError(
-        "HIP INT8 merge supports two-dimensional per-tensor and per-row layouts, "
-        f"got shape {shape} with block size {block_size}."
+        "HIP INT8 merge supports two-dimensional per-tensor, per-row and per-group layouts (group 16, 32 or a "
+        f"multiple of 64 dividing the columns), got shape {shape} with block size {block_size}."
     )
+
+
+def _qparam_shape(shape: tuple[int, int], group: int) -> tuple[int, int]:
+    rows, cols = shape
+    if group == rows * cols and group != cols:
+        return (1, 1)
+    return (rows, cols // group)
 
 
 def merge_int8_lora_into(
@@ -174,7 +189,7 @@ def requantize_int8(dense: torch.Tensor, block_size: tuple[int, int], *, scale_d
     rows, cols = dense.shape
     group = _int8_group((rows, cols), block_size)
     nq = rows * cols // group
-    qshape = (rows, 1) if group == cols else (1, 1)
+    qshape = _qparam_shape((rows, cols), group)
     out_q = torch.empty((rows, cols), device=device, dtype=torch.int8)
     out_s = torch.empty(qshape, device=device, dtype=scale_dtype)
     out_z = torch.empty(qshape, device=device, dtype=torch.int8)
@@ -212,6 +227,7 @@ def dequantize_int8(qdata: torch.Tensor, scale: torch.Tensor, zero_point: torch.
 # scaled FP8
 # ---------------------------------------------------------------------------
 def _fp8_group(shape: tuple[int, int], block_size: tuple[int, ...], scale: torch.Tensor) -> int:
+    """Elements per scale: per-row, per-tensor or per-group (1, g) layouts (P/float8_adapter.py:63-98)."""
     rows, cols = shape
     block_size = tuple(block_size)
     if block_size == (1, cols):
@@ -222,9 +238,15 @@ def _fp8_group(shape: tuple[int, int], block_size: tuple[int, ...], scale: torch
         if scale.numel() != 1:
             raise ValueError("HIP per-tensor scaled-FP8 merge expects one scale.")
         return rows * cols
+    if len(block_size) == 2 and block_size[0] == 1 and _group_ok(cols, block_size[1]):
+        g = block_size[1]
+        if tuple(scale.shape) != (rows, cols // g):
+            raise ValueError(f"HIP per-group scaled-FP8 merge expects scale shape {(rows, cols // g)}, "
+                             f"got {tuple(scale.shape)}.")
+        return g
     raise ValueError(
-        "HIP scaled-FP8 merge supports per-row and per-tensor layouts, "
-        f"got block_size={block_size!r}."
+        "HIP scaled-FP8 merge supports per-row, per-tensor and per-group layouts (group 16, 32 or a multiple of 64 "
+        f"dividing the columns), got block_size={block_size!r}."
     )
 
 
@@ -266,9 +288,17 @@ def requantize_float8(dense: torch.Tensor, block_size: tuple[int, int], *, fp8_d
     device = _same_device("scaled-FP8", dense)
     dense = dense.contiguous()
     rows, cols = dense.shape
-    per_row = tuple(block_size) == (1, cols)
+    block_size = tuple(block_size)
+    if block_size == (1, cols):
+        sshape = (rows, 1)
+    elif block_size == (rows, cols):
+        sshape = (1, 1)
+    elif len(block_size) == 2 and block_size[0] == 1 and block_size[1] > 0 and cols % block_size[1] == 0:
+        sshape = (rows, cols // block_size[1])
+    else:
+        sshape = (1, 1)  # rejected by _fp8_group below
     out_q = torch.empty((rows, cols), device=device, dtype=fp8_dtype)
-    out_s = torch.empty((rows, 1) if per_row else (1, 1), device=device, dtype=torch.float32)
+    out_s = torch.empty(sshape, device=device, dtype=torch.float32)
     group = _fp8_group((rows, cols), block_size, out_s)
     rnd = L.rounding_struct(rounding_seed)
     ws_bytes = L.load_library().lm_workspace_size(rows, cols, 0)

@@ -301,3 +301,38 @@ def test_merge_dense_strength_zero_and_rank_padding() -> None:
     assert np.array_equal(O.merge_dense(bf16_np(base), bf16_np(b), bf16_np(a), 0.0), bf16_np(base))
     back = np_bf16(O.merge_dense(bf16_np(base), bf16_np(b), bf16_np(a), 1.0))
     assert back.shape == base.shape
+
+
+# ---- per-group layouts: the per-row recipe on each group ---------------------
+# A per-group quantization of [M, N] with group g is the per-row quantization
+# of the same memory viewed as [M N / g, g]: every group is one row of the
+# view and keeps its flat element offsets, so the stochastic draws are the
+# same.  This pins the oracle's per-group path to its per-row path.
+@pytest.mark.parametrize("g", [16, 32, 64, 128])
+@pytest.mark.parametrize("asym", [False, True])
+@pytest.mark.parametrize("sr", [O.SR_OFF, O.SR_PHILOX8])
+def test_int8_group_is_per_row_of_the_group_view(g, asym, sr):
+    rng = np.random.default_rng(g)
+    dense = O.f32_to_bf16((rng.standard_normal((12, 256)) * 0.02).astype(np.float32))
+    dense[3, :g] = 0
+    q, s, z = O.int8_requant(dense, g, asymmetric=asym, sr_mode=sr, seed=77)
+    view = dense.reshape(-1, g)
+    rq, rs, rz = O.int8_requant(view, g, asymmetric=asym, sr_mode=sr, seed=77)
+    assert np.array_equal(q.reshape(-1, g), rq)
+    assert np.array_equal(s, rs)
+    if asym:
+        assert np.array_equal(z, rz)
+    deq = O.int8_dequant(q, s, z if asym else None, g)
+    assert np.array_equal(deq.reshape(-1, g), O.int8_dequant(rq, rs, rz if asym else None, g))
+
+
+@pytest.mark.parametrize("g", [16, 64])
+@pytest.mark.parametrize("fmt", [O.DT_E4M3, O.DT_E5M2])
+@pytest.mark.parametrize("sr", [O.SR_OFF, O.SR_PHILOX8])
+def test_fp8_group_is_per_row_of_the_group_view(g, fmt, sr):
+    rng = np.random.default_rng(g + fmt)
+    dense = O.f32_to_bf16((rng.standard_normal((8, 128)) * 0.05).astype(np.float32))
+    q, s = O.fp8_requant(dense, g, fmt=fmt, sr_mode=sr, seed=5)
+    rq, rs = O.fp8_requant(dense.reshape(-1, g), g, fmt=fmt, sr_mode=sr, seed=5)
+    assert np.array_equal(q.reshape(-1, g), rq)
+    assert np.array_equal(s, rs)

@@ -1,4 +1,4 @@
-"""Scaled FP8 (e4m3fn / e5m2) per-row and per-tensor merge vs the oracle (same contract as INT8)."""
+"""Scaled FP8 (e4m3fn / e5m2) per-row and per-tensor merge vs the oracle (same contract as INT8; per-group layouts are in test_gpu_groups.py)."""
 
 from __future__ import annotations
 

@@ -223,9 +223,11 @@ def test_int8_rejects_bad_inputs():
     a = torch.zeros(4, 64, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(ValueError, match="do not match"):
         K.merge_int8_lora(q, s, None, (1, 64), b, a[:, :32], 1.0, asymmetric=False, reduce_range=False)
-    with pytest.raises(ValueError, match="per-tensor and per-row"):
-        K.merge_int8_lora(q, torch.ones(16, 2, device=DEV), None, (1, 32), b, a, 1.0, asymmetric=False,
+    with pytest.raises(ValueError, match="per-tensor, per-row and per-group"):  # 2-D blocks
+        K.merge_int8_lora(q, torch.ones(8, 2, device=DEV), None, (2, 32), b, a, 1.0, asymmetric=False,
                           reduce_range=False)
+    with pytest.raises(ValueError, match="scale shape"):  # a per-group layout with per-row scales
+        K.merge_int8_lora(q, s, None, (1, 32), b, a, 1.0, asymmetric=False, reduce_range=False)
     with pytest.raises(ValueError, match="int8"):
         K.merge_int8_lora(q.float(), s, None, (1, 64), b, a, 1.0, asymmetric=False, reduce_range=False)
 
