@@ -81,11 +81,12 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="int8_stack",
                    choices=["int8_stack", "nvfp4_stack", "int8", "fp8", "q8_0", "nvfp4", "mxfp4", "gguf", "reload", "h2d",
-                            "api", "copy"])
+                            "api", "routed", "copy"])
     p.add_argument("--gguf-type", default="Q4_K", choices=sorted(GGUF_TYPES),
                    help="GGUF type of --workload gguf (dequantize to bf16)")
     p.add_argument("--rounding", default="stochastic", choices=["stochastic", "nearest"])
     p.add_argument("--layers", type=int, default=32)
+    p.add_argument("--tokens", type=int, default=4096, help="tokens of --workload routed")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-oracle baseline (0: skip)")
     return p.parse_args()
 
@@ -376,6 +377,37 @@ class Api(Workload):
         merge_lora(self.model, [(self.lora, 1.0)], stochastic_rounding=self.stochastic)
 
 
+class Routed(Workload):
+    """Routed LoRA residual (P/lora.py:801-829) after a gate_proj-shaped Linear: tokens x 4096 -> 14336, rank 16,
+    bf16: out = y + ((x A^T) s) B^T, one down-projection and one up-projection launch per step."""
+
+    family = "routed"
+
+    def __init__(self, tokens: int) -> None:
+        import torch
+
+        from piper_offload_amd.routed import RoutedFactor
+
+        K, N, rank = 4096, 14336, 16
+        self.x = _normal((tokens, K), 1.0, 11)
+        self.y = _normal((tokens, N), 0.5, 12)
+        self.f = [RoutedFactor(_normal((rank, K), 1.0 / rank, 13), _normal((N, rank), 0.01, 14), 1.0)]
+        self.bytes_per_step = 2 * (tokens * K + 2 * tokens * N + rank * (K + N))
+        self.name = "routed"
+        self.config = {"workload": f"routed LoRA residual, {tokens} tokens x [4096 -> 14336] (gate_proj), rank 16, "
+                                   "bf16: reads x, y, A, B once, writes out once",
+                       "tokens": tokens, "rank": rank, "algorithmic_bytes_per_step": self.bytes_per_step}
+        torch.cuda.synchronize()
+
+    def step(self, index: int) -> None:
+        import torch
+
+        from piper_offload_amd.routed import routed_residual
+
+        with torch.no_grad():
+            self.out = routed_residual(self.x, self.f, self.y)
+
+
 class Gguf(Workload):
     """GGUF dequantize (P/gguf_dequant.py:303-331) of one gate_proj-shaped [14336, 4096] tensor to bf16."""
 
@@ -576,6 +608,8 @@ def main() -> int:
         wl = H2D(args.layers)
     elif args.workload == "api":
         wl = Api(args.layers, stochastic)
+    elif args.workload == "routed":
+        wl = Routed(args.tokens)
     else:
         wl = Single(args.workload, stochastic)
     torch.cuda.synchronize()

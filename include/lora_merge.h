@@ -216,6 +216,29 @@ int lm_gguf_dequant(const uint8_t* packed, int32_t quant_type, int64_t rows, int
 int lm_dense_merge(void* w, int64_t M, int64_t N, int64_t ldw, const lm_lora* lora, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* ---------------- routed LoRA residual --------------------------------
+ * Replaces _routed_residual (P/lora.py:801-829), the POST-hook contribution
+ * of routed mode (P/lora.py:869-930):
+ *   out = dt(y + sum_i dt(dt(dt(dt(x A_i^T) s_i) B_i^T) + dt(bias_i s_i)))
+ * with every matmul accumulated in fp32 and every step rounded to the
+ * output dtype `dtype` (LM_BF16 / LM_F16), in the reference's order (the sum
+ * over factors left to right).  x: [T, K]; y, out: [T, N] (out may alias y);
+ * a: [rank, K]; b: [N, rank]; bias: [N] or NULL; all row-major in `dtype`,
+ * 8-byte aligned, K % 4 == 0, rank 1..64, at most 8 factors and 16 rank
+ * chunks of 16 in all.  Workspace: lm_routed_workspace_size bytes, 256-byte
+ * aligned. */
+typedef struct lm_routed_factor {
+  const void* a;
+  const void* b;
+  const void* bias;
+  float strength;
+  int32_t rank;
+} lm_routed_factor;
+size_t lm_routed_workspace_size(int64_t T, int64_t K, const lm_routed_factor* factors, int32_t count);
+int lm_routed_residual(const void* x, const void* y, void* out, int64_t T, int64_t K, int64_t N, int32_t dtype,
+                       const lm_routed_factor* factors, int32_t count, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
 /* ---------------- stacks: many targets, one grouped launch ------------
  * `items` is a HOST array of `count` descriptors.  Each target gets its own
  * seed (derive_seed(param_path, merge_index)). */

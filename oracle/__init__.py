@@ -47,6 +47,7 @@ _SIGS = {
     "lmo_philox4x32": (None, [_P, ctypes.c_uint32, ctypes.c_uint32, _I, _P]),
     "lmo_uniforms": (None, [_I, _U64, _U64, _I64, _P]),
     "lmo_merge_dense": (None, [_P, _P, _I, _I64, _I64, _P, _I64, _P, _I64, _I, _I, _F, _I]),
+    "lmo_routed_residual": (None, [_P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P, _P]),
     "lmo_int8_dequant": (None, [_P, _P, _I, _P, _I64, _I64, _I64, _I, _P]),
     "lmo_int8_requant": (None, [_P, _I, _I64, _I64, _I64, _I, _I, _I, _I, _U64, _P, _P, _P]),
     "lmo_fp8_dequant": (None, [_P, _I, _P, _I64, _I64, _I64, _I, _P]),
@@ -253,6 +254,27 @@ def merge_dense(base: np.ndarray, b: np.ndarray, a: np.ndarray, strength: float,
     out = _dense_empty((M, N), cd)
     load().lmo_merge_dense(_p(base), _p(out), cd, M, N, _p(b), b.shape[1] if b.ndim == 2 else 0, _p(a), N, fdt, r,
                            float(strength), int(keep_zero_update))
+    return out
+
+
+def routed_residual(x, y, factors, *, dt=DT_BF16):
+    """out = dt(y + sum_i part_i), factors = [(a [r, K], b [N, r], bias [N] or None, strength)], all arrays of dt
+    bit patterns (uint16); the reference's _routed_residual (P/lora.py:801-829) with fp32 matmul sums."""
+    x = np.ascontiguousarray(x)
+    y = np.ascontiguousarray(y)
+    T, K = x.shape
+    N = y.shape[1]
+    nf = len(factors)
+    keep = [(np.ascontiguousarray(a), np.ascontiguousarray(b), None if bias is None else np.ascontiguousarray(bias))
+            for a, b, bias, _s in factors]
+    ptr = ctypes.c_void_p * nf
+    a_p = ptr(*[_p(a) for a, _b, _c in keep])
+    b_p = ptr(*[_p(b) for _a, b, _c in keep])
+    c_p = ptr(*[_p(c) for _a, _b, c in keep])
+    s_arr = (ctypes.c_float * nf)(*[float(f[3]) for f in factors])
+    r_arr = (ctypes.c_int32 * nf)(*[int(a.shape[0]) for a, _b, _c in keep])
+    out = np.empty_like(y)
+    load().lmo_routed_residual(_p(x), _p(y), _p(out), T, K, N, dt, nf, a_p, b_p, c_p, s_arr, r_arr)
     return out
 
 

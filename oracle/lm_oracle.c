@@ -828,3 +828,39 @@ EXPORT void lmo_sr_fp8(int fmt, const float* x, const float* u, int64_t n, float
   for (int64_t i = 0; i < n; ++i) out[i] = sr_fp8(fmt, x[i], u[i], limit);
 }
 EXPORT int lmo_version(void) { return 1; }
+
+/* ------------------------------------------------------------------ */
+/* Routed LoRA residual (P/lora.py:801-829, _routed_residual)           */
+/* ------------------------------------------------------------------ */
+/* out = dt(y + total), total = part_0, dt(total + part_i) for i > 0 in order,
+ *   part_i = dt(dt(dt(dt(x A_i^T) s_i) B_i^T)), + dt(bias_i s_i) then dt when
+ *   a bias is present,
+ * the reference's torch expression ((x @ a.T) * s) @ b.T (+ bias * s) with
+ * every op's result in the output dtype dt (bf16/fp16) and each matmul an
+ * fp32 sum in ascending k (fmaf per term).  x [T, K], y/out [T, N],
+ * a_i [r_i, K], b_i [N, r_i], bias_i [N] or NULL, all in dt. */
+EXPORT void lmo_routed_residual(const void* x, const void* y, void* out, int64_t T, int64_t K, int64_t N, int dt,
+                                int nf, const void* const* a, const void* const* b, const void* const* bias,
+                                const float* s, const int32_t* rank) {
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < T; ++t) {
+    float* total = (float*)malloc(sizeof(float) * (size_t)N);
+    float ps[64];
+    for (int i = 0; i < nf; ++i) {
+      for (int r = 0; r < rank[i]; ++r) {
+        float acc = 0.0f;
+        for (int64_t k = 0; k < K; ++k) acc = fmaf(load_dt(dt, x, t * K + k), load_dt(dt, a[i], (int64_t)r * K + k), acc);
+        ps[r] = round_dt(dt, round_dt(dt, acc) * s[i]);
+      }
+      for (int64_t n = 0; n < N; ++n) {
+        float acc = 0.0f;
+        for (int r = 0; r < rank[i]; ++r) acc = fmaf(ps[r], load_dt(dt, b[i], n * rank[i] + r), acc);
+        float part = round_dt(dt, acc);
+        if (bias[i]) part = round_dt(dt, part + round_dt(dt, load_dt(dt, bias[i], n) * s[i]));
+        total[n] = i == 0 ? part : round_dt(dt, total[n] + part);
+      }
+    }
+    for (int64_t n = 0; n < N; ++n) store_dt(dt, out, t * N + n, round_dt(dt, load_dt(dt, y, t * N + n) + total[n]));
+    free(total);
+  }
+}

@@ -8,7 +8,8 @@ Host layer over the gfx950 HIP kernels in ``libpiper_lora_merge.so``:
   P/tensor_adapter_registry.py) for INT8, scaled FP8, NVFP4, MX, GGUF and
   plain tensors;
 * ``kernels`` -- drop-in replacements for the Triton merge functions;
-* ``stack`` -- grouped multi-target merges.
+* ``stack`` -- grouped multi-target merges;
+* ``routed`` -- routed LoRA: the residual hook (P/lora.py:792-930).
 """
 
 from .adapters import Float8Adapter, GgufAdapter, Int8Adapter, MxAdapter, Nvfp4Adapter, RegularAdapter
@@ -16,6 +17,7 @@ from .formats import Float8Weight, GGUFWeight, Int8Weight, MXWeight, NVFP4Weight
 from .lora import LoRA, LoRAFactor, LoRATransform, ScaledLoRAFactor
 from .merge import merge_lora
 from .registry import param_representation, register_adapter, select_adapter
+from .routed import install_routed_residual_hook, routed_residual
 from .seeding import derive_seed
 
 __version__ = "0.1.0"
@@ -37,8 +39,10 @@ __all__ = [
     "RegularAdapter",
     "ScaledLoRAFactor",
     "derive_seed",
+    "install_routed_residual_hook",
     "merge_lora",
     "param_representation",
     "register_adapter",
+    "routed_residual",
     "select_adapter",
 ]

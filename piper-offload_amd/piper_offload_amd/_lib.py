@@ -15,7 +15,7 @@ import torch
 __all__ = [
     "LM_F32", "LM_BF16", "LM_F16", "LM_E4M3", "LM_E5M2", "LM_E2M1", "LM_E8M0",
     "LM_ROUND_NEAREST", "LM_ROUND_STOCHASTIC",
-    "LoraStruct", "RoundingStruct", "StackItem",
+    "LoraStruct", "RoundingStruct", "RoutedFactor", "StackItem",
     "check", "lib", "library_path", "torch_dtype_id", "workspace",
 ]
 
@@ -56,6 +56,12 @@ class StackItem(ctypes.Structure):
     ]
 
 
+class RoutedFactor(ctypes.Structure):
+    """Mirror of ``lm_routed_factor``."""
+
+    _fields_ = [("a", _P), ("b", _P), ("bias", _P), ("strength", ctypes.c_float), ("rank", _I32)]
+
+
 _L = ctypes.POINTER(LoraStruct)
 _R = ctypes.POINTER(RoundingStruct)
 
@@ -82,6 +88,9 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lm_dense_merge": (_I32, [_P, _I64, _I64, _I64, _L, _P, _SZ, _P]),
     "lm_int8_merge_stack": (_I32, [ctypes.POINTER(StackItem), _I32, _I32, _I32, _P, _SZ, _P]),
     "lm_nvfp4_merge_stack": (_I32, [ctypes.POINTER(StackItem), _I32, _I32, _I32, _P, _SZ, _P]),
+    "lm_routed_workspace_size": (_SZ, [_I64, _I64, ctypes.POINTER(RoutedFactor), _I32]),
+    "lm_routed_residual": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I32, ctypes.POINTER(RoutedFactor), _I32, _P, _SZ,
+                                  _P]),
     "lm_timer_enable": (_I32, [_I32]),
     "lm_timer_read": (_I32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]),
 }
