@@ -100,7 +100,8 @@ def test_int8_dequant_and_dense_merge(shape, rank):
 @pytest.mark.parametrize("shape,rank,strength", [((64, 4096), 32, 0.5), ((24, 69), 5, 0.75), ((40, 1024), 16, 1.0),
                                                  ((32, 2048), 64, 1.0), ((16, 8192), 32, 0.5),
                                                  ((40, 14336), 16, 1.0), ((17, 12288), 16, 0.5),
-                                                 ((20, 8192), 64, 0.75)])
+                                                 ((20, 8192), 64, 0.75), ((16400, 4608), 64, 1.0),
+                                                 ((16400, 1024), 16, 0.5)])
 @pytest.mark.parametrize("sr", [False, True])
 @pytest.mark.parametrize("scale_dtype", [torch.float32, torch.bfloat16])
 def test_int8_fused_equals_requant_of_gpu_dense(shape, rank, strength, sr, scale_dtype):
