@@ -221,6 +221,23 @@ DEV void sr_nwords16_even(uint64_t seed, uint32_t ctr, uint32_t (&nw)[8]) {
     nw[4 * gi + 3] = ~c[3];
   }
 }
+// The SPAN/2 complemented Philox words (~w) of offsets idx0 .. idx0+SPAN-1
+// when idx0 % SPAN == 0 (SPAN a multiple of 8): the SPAN/8 counters are
+// (idx0 >> 3) | gi with no carry.
+template <int SPAN>
+DEV void sr_nwords_aligned(uint64_t seed, uint64_t idx0, uint32_t (&nw)[SPAN / 2]) {
+  const uint64_t ctr = idx0 >> 3;
+  const uint32_t lo = (uint32_t)ctr, hi = (uint32_t)(ctr >> 32);
+#pragma unroll
+  for (int gi = 0; gi < SPAN / 8; ++gi) {
+    uint32_t c[4];
+    philox10_n02(lo | (uint32_t)gi, hi, seed, c);
+    nw[4 * gi + 0] = c[0];
+    nw[4 * gi + 1] = ~c[1];
+    nw[4 * gi + 2] = c[2];
+    nw[4 * gi + 3] = ~c[3];
+  }
+}
 // 16-bit uniform integers h for offsets idx0 .. idx0+SPAN-1 (u = h * 2^-16)
 template <int SPAN>
 DEV void sr_bits(uint64_t seed, uint64_t idx0, uint32_t (&h)[SPAN]) {
@@ -316,9 +333,22 @@ DEV uint32_t cvt_sr_fp8(uint32_t old, float x, uint32_t seed) {
 #undef LM_SR8
   return old;
 }
-// Eight e2m1 codes of x[0..7], element 2k drawn from the low half of w[k] and
-// 2k+1 from its high half (independent draws: two conversions per pair, each
-// keeping its low nibble).
+// Eight e2m1 codes of x[0..7], element 2k drawn from the low half of the
+// complemented Philox word nw[k] = ~w[k] and 2k+1 from its high half
+// (independent draws: two conversions per pair, each keeping its low nibble).
+DEV uint32_t sr_e2m1_nword(const float* x, const uint32_t* nw) {
+  uint32_t ev = 0u, od = 0u;
+  ev = cvt_sr_fp4<0>(ev, x[0], x[1], sr_seed_lo(nw[0]));
+  od = cvt_sr_fp4<0>(od, x[1], x[0], sr_seed_hi(nw[0]));
+  ev = cvt_sr_fp4<1>(ev, x[2], x[3], sr_seed_lo(nw[1]));
+  od = cvt_sr_fp4<1>(od, x[3], x[2], sr_seed_hi(nw[1]));
+  ev = cvt_sr_fp4<2>(ev, x[4], x[5], sr_seed_lo(nw[2]));
+  od = cvt_sr_fp4<2>(od, x[5], x[4], sr_seed_hi(nw[2]));
+  ev = cvt_sr_fp4<3>(ev, x[6], x[7], sr_seed_lo(nw[3]));
+  od = cvt_sr_fp4<3>(od, x[7], x[6], sr_seed_hi(nw[3]));
+  return (ev & 0x0f0f0f0fu) | ((od << 4) & 0xf0f0f0f0u);
+}
+// the same from the Philox words themselves
 DEV uint32_t sr_e2m1_word(const float* x, const uint32_t* w) {
   uint32_t ev = 0u, od = 0u;
   uint32_t nw = ~w[0];
@@ -372,6 +402,12 @@ DEV uint32_t sr_fp8(float v, uint32_t h, float /*limit*/) { return cvt_sr_fp8<FM
 DEV float max3_abs(float acc, float a, float b) {
   float r;
   asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(acc), "v"(a), "v"(b));
+  return r;
+}
+// min(acc, |a|, |b|) in one v_min3_f32
+DEV float min3_abs(float acc, float a, float b) {
+  float r;
+  asm("v_min3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(acc), "v"(a), "v"(b));
   return r;
 }
 // two fp32 -> packed bf16 pair (RNE, v_cvt_pk_bf16_f32); low half = a

@@ -124,8 +124,8 @@ DEV void mx_tile(const MxArgs& a, const MxTileIn<ELEM, NKC>& in, const v4i16 (&b
   }
   float inv;
   const uint32_t enc = mx_scale(amax, a.mode, MxTraits<ELEM>::emax, L, MxTraits<ELEM>::mbits, inv);
-  uint32_t rw[16];
-  if constexpr (SR) sr_words_aligned<32>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4)), rw);
+  uint32_t nw[16];  // complemented Philox words
+  if constexpr (SR) sr_nwords_aligned<32>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4)), nw);
   float x[32];
 #pragma unroll
   for (int j = 0; j < 32; ++j) {
@@ -137,7 +137,7 @@ DEV void mx_tile(const MxArgs& a, const MxTileIn<ELEM, NKC>& in, const v4i16 (&b
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       if constexpr (SR) {
-        words[k] = sr_e2m1_word(x + 8 * k, rw + 4 * k);
+        words[k] = sr_e2m1_nword(x + 8 * k, nw + 4 * k);
       } else {
         uint32_t wd = 0u;
         wd = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(wd, x[8 * k + 0], x[8 * k + 1], 1.0f, 0);
@@ -152,7 +152,7 @@ DEV void mx_tile(const MxArgs& a, const MxTileIn<ELEM, NKC>& in, const v4i16 (&b
     uint32_t wv[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      if constexpr (SR) wv[i] = sr_fp8_word<ELEM>(x + 4 * i, rw + 2 * i);
+      if constexpr (SR) wv[i] = sr_fp8_nword<ELEM>(x + 4 * i, nw + 2 * i);
       else wv[i] = fp8_pack4<ELEM>(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
     }
     uint4* dst = (uint4*)(qo + (int64_t)mt * 128);

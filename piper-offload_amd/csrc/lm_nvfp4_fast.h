@@ -155,7 +155,8 @@ DEV void nv_merged_block(const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float
   // LoRA row, an exact cancellation or an underflow takes the exact path).
   float dmin = __builtin_fabsf(d[0]);
 #pragma unroll
-  for (int j = 1; j < 16; ++j) dmin = __builtin_fminf(dmin, __builtin_fabsf(d[j]));
+  for (int j = 1; j < 15; j += 2) dmin = min3_abs(dmin, d[j], d[j + 1]);
+  dmin = __builtin_fminf(dmin, __builtin_fabsf(d[15]));
   if (dmin * __builtin_fabsf(strength) == 0.0f) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
@@ -195,16 +196,19 @@ static __device__ __constant__ const float kRcpE4M3[8] = {1.0f / 1.0f, 1.0f / 1.
 template <bool TWO, bool SR, int B>
 DEV void nv_quant_block(const NvArgs& a, int64_t row, int mt, int lane, float gq, float inv_g, const float* rtab,
                         const float (&m)[16], uint32_t (&words)[4], uint32_t& scb) {
-  uint32_t rw[8];
+  uint32_t nw[8];  // complemented Philox words
   if constexpr (SR)
-    sr_words_aligned<16>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4) + 16 * B), rw);
+    sr_nwords_aligned<16>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4) + 16 * B), nw);
+  // bmax over the bf16-rounded values = bf16(max |m|) (rounding is monotone)
   float mb[16];
   float bmax = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < 16; j += 2) {
     mb[j] = bf16r(m[j]);
-    bmax = __builtin_fmaxf(bmax, __builtin_fabsf(mb[j]));
+    mb[j + 1] = bf16r(m[j + 1]);
+    bmax = max3_abs(bmax, m[j], m[j + 1]);
   }
+  bmax = bf16r(bmax);
   // bmax is a bf16 value and 6 is exact in bf16: div_rn is the IEEE quotient
   float fs = div_rn(bmax, 6.0f, 1.0f / 6.0f);
   if constexpr (TWO) fs = div_markstein(fs, gq, inv_g);
@@ -222,7 +226,7 @@ DEV void nv_quant_block(const NvArgs& a, int64_t row, int mt, int lane, float gq
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     if constexpr (SR) {
-      words[2 * B + k] = sr_e2m1_word(x + 8 * k, rw + 4 * k);
+      words[2 * B + k] = sr_e2m1_nword(x + 8 * k, nw + 4 * k);
     } else {
       // dst_sel k writes byte k and keeps the others (checked on gfx950)
       uint32_t wd = 0u;
@@ -283,7 +287,7 @@ DEV void nv_amax_body(const NvArgs& a, int64_t row0, int t0, int t1) {
       float m[32];
       nv_merged<NKC, true>(cur, bop, strength, gin, m);
 #pragma unroll
-      for (int j = 0; j < 32; ++j) mx = __builtin_fmaxf(mx, __builtin_fabsf(m[j]));
+      for (int j = 0; j < 32; j += 2) mx = max3_abs(mx, m[j], m[j + 1]);
       cur = nxt;
     }
   }
