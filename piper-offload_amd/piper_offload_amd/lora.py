@@ -59,8 +59,8 @@ class LoRAFactor:
             total += self.bias.numel() * self.bias.element_size()
         return total
 
-    def scaled(self, strength: float) -> ScaledLoRAFactor:
-        return ScaledLoRAFactor(self.a, self.b, strength, self.bias)
+    def scaled(self, strength: float, staged: tuple | None = None) -> ScaledLoRAFactor:
+        return ScaledLoRAFactor(self.a, self.b, strength, self.bias, staged)
 
 
 @dataclass(slots=True, frozen=True)
@@ -71,6 +71,9 @@ class ScaledLoRAFactor:
     b: torch.Tensor
     strength: float
     bias: torch.Tensor | None = None
+    # (a, b) already on a GPU, same values and dtype as the host tensors: the
+    # staging then copies nothing (see LoRA.stage_on)
+    staged: tuple[torch.Tensor, torch.Tensor] | None = None
 
     def __post_init__(self) -> None:
         if self.a.ndim != 2 or self.b.ndim != 2 or self.a.shape[0] != self.b.shape[1]:
@@ -99,11 +102,23 @@ class ScaledLoRAFactor:
 
 
 class LoRA:
-    """Reusable immutable host-backed LoRA resource (P/lora.py:224-311)."""
+    """Reusable immutable host-backed LoRA resource (P/lora.py:224-311).
 
-    def __init__(self, targets: Mapping[str, LoRAFactor]) -> None:
+    ``from_state_dict`` with pinned host backing packs every factor into one
+    pinned arena (each tensor 256-byte aligned), so :meth:`stage_on` moves all
+    of a LoRA's factors to a GPU with one copy.
+    """
+
+    def __init__(self, targets: Mapping[str, LoRAFactor], *, arena: torch.Tensor | None = None) -> None:
         self._targets = MappingProxyType(dict(targets))
         self._cache_bytes = sum(f.cache_bytes for f in self._targets.values())
+        self._arena = arena
+
+    def stage_on(self, device: torch.device) -> _DeviceArena | None:
+        """The whole arena on ``device`` after one asynchronous copy, or None without an arena."""
+        if self._arena is None or device.type != "cuda":
+            return None
+        return _DeviceArena(self._arena, self._arena.to(device, non_blocking=True))
 
     @classmethod
     def from_state_dict(cls, state_dict: dict[str, torch.Tensor], *, dtype: torch.dtype | None = None,
@@ -132,12 +147,26 @@ class LoRA:
             _validate_factor_pair(f"{base}.weight", a, b, bias)
             if host_backing == "adopt" and dtype is not None and (a.dtype is not dtype or b.dtype is not dtype):
                 raise ValueError("adopted LoRA host backing cannot convert factor dtype without copying.")
-            if pin:
-                targets[f"{base}.weight"] = LoRAFactor(_host_copy(a, dtype, True), _host_copy(b, dtype, True),
-                                                       None if bias is None else _host_copy(bias, dtype, True))
-            else:
-                targets[f"{base}.weight"] = LoRAFactor(a, b, bias)
-        return cls(targets)
+        if not pin:
+            return cls({f"{base}.weight": LoRAFactor(a, b_t[base], bias_t.get(base)) for base, a in a_t.items()})
+        # one pinned arena holds every factor (P/lora.py:940-975 pins each tensor separately)
+        items = [(base, role, t.detach()) for base, a in a_t.items()
+                 for role, t in (("a", a), ("b", b_t[base]), ("bias", bias_t.get(base))) if t is not None]
+        sizes = [t.numel() * (dtype.itemsize if dtype is not None else t.element_size()) for _b, _r, t in items]
+        offsets, total = [], 0
+        for n in sizes:
+            offsets.append(total)
+            total += (n + 255) // 256 * 256
+        arena = torch.empty(max(total, 256), dtype=torch.uint8, pin_memory=torch.cuda.is_available())
+        placed: dict[tuple[str, str], torch.Tensor] = {}
+        for (base, role, t), off, n in zip(items, offsets, sizes):
+            dt = dtype if dtype is not None else t.dtype
+            view = arena[off:off + n].view(dt).view(t.shape)
+            view.copy_(t.to("cpu"))
+            placed[(base, role)] = view
+        for base in a_t:
+            targets[f"{base}.weight"] = LoRAFactor(placed[(base, "a")], placed[(base, "b")], placed.get((base, "bias")))
+        return cls(targets, arena=arena)
 
     @property
     def targets(self) -> Mapping[str, LoRAFactor]:
@@ -146,6 +175,23 @@ class LoRA:
     @property
     def cache_bytes(self) -> int:
         return self._cache_bytes
+
+
+class _DeviceArena:
+    """A LoRA's host arena and its copy on one GPU: device views of host factor tensors."""
+
+    __slots__ = ("dev", "host")
+
+    def __init__(self, host: torch.Tensor, dev: torch.Tensor) -> None:
+        self.host, self.dev = host, dev
+
+    def view(self, t: torch.Tensor) -> torch.Tensor | None:
+        """The device tensor holding ``t``'s values, or None when ``t`` is not in the arena."""
+        off = t.data_ptr() - self.host.data_ptr()
+        n = t.numel() * t.element_size()
+        if not t.is_contiguous() or off < 0 or off + n > self.host.numel():
+            return None
+        return self.dev[off:off + n].view(t.dtype).view(t.shape)
 
 
 @dataclass(slots=True, frozen=True)
@@ -343,20 +389,33 @@ class LoRATransform:
         factors = self._factors
         total = sum(f.a.shape[0] for f in factors)
         rows, cols = shape[0], shape[1]
+        def src(f: ScaledLoRAFactor) -> tuple[torch.Tensor, torch.Tensor]:
+            # the GPU copy made for this merge when there is one, else the host tensors
+            if f.staged is not None and f.staged[0].device == device:
+                return f.staged
+            return f.a, f.b
+
+        if len(factors) == 1 and factors[0].staged is not None and factors[0].staged[0].device == device \
+                and factors[0].a.dtype is compute_dtype and factors[0].b.dtype is compute_dtype:
+            b, a = factors[0].staged[1], factors[0].staged[0]  # already there, in the compute dtype
+            self._staged[key] = (versions, b, a, factors[0].strength)
+            return b, a, factors[0].strength
         buf = torch.empty(total * cols + rows * total, dtype=compute_dtype, device=device)
         a = buf[: total * cols].view(total, cols)
         b = buf[total * cols:].view(rows, total)
         if len(factors) == 1:
             f = factors[0]
-            a.copy_(f.a, non_blocking=True)
-            b.copy_(f.b, non_blocking=True)
+            fa, fb = src(f)
+            a.copy_(fa, non_blocking=True)
+            b.copy_(fb, non_blocking=True)
             strength = f.strength
         else:
             off = 0
             for f in factors:
                 nxt = off + f.a.shape[0]
-                a[off:nxt].copy_(f.a, non_blocking=True)
-                b[:, off:nxt].copy_(f.b, non_blocking=True)
+                fa, fb = src(f)
+                a[off:nxt].copy_(fa, non_blocking=True)
+                b[:, off:nxt].copy_(fb, non_blocking=True)
                 if f.strength != 1.0:
                     a[off:nxt].mul_(f.strength)
                 off = nxt

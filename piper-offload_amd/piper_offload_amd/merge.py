@@ -15,10 +15,11 @@ from collections.abc import Sequence
 from dataclasses import dataclass
 from typing import Any
 
+import torch
 from torch import nn
 
 from .lora import LoRA, LoRATransform, ScaledLoRAFactor
-from .registry import param_tensor_id
+from .registry import param_representation, param_tensor_id
 from .stack import StackPlan, StackTarget
 
 logger = logging.getLogger(__name__)
@@ -104,8 +105,18 @@ def _build_merge_ops(params: dict[str, nn.Parameter], loras: Sequence[tuple[LoRA
                      stochastic_rounding: bool) -> list[_MergeOp]:
     groups: dict[tuple[Any, ...], tuple[str, nn.Parameter, list[ScaledLoRAFactor]]] = {}
     for lora, strength in loras:
+        arenas: dict[torch.device, Any] = {}  # this LoRA's factors on each GPU: one copy per device
         for key, factor in lora.targets.items():
             weight = params[key]
+            device = param_representation(weight).device
+            staged = None
+            if device.type == "cuda":
+                if device not in arenas:
+                    arenas[device] = lora.stage_on(device)
+                arena = arenas[device]
+                if arena is not None:
+                    sa, sb = arena.view(factor.a), arena.view(factor.b)
+                    staged = None if sa is None or sb is None else (sa, sb)
             tid = param_tensor_id(weight)
             group = groups.get(tid)
             if group is None:
@@ -117,7 +128,7 @@ def _build_merge_ops(params: dict[str, nn.Parameter], loras: Sequence[tuple[LoRA
                     "one name for a tied weight in a single merge_lora() call; otherwise the same base weight would "
                     "receive multiple logical updates."
                 )
-            group[2].append(factor.scaled(strength))
+            group[2].append(factor.scaled(strength, staged))
     ops: list[_MergeOp] = []
     bias_owner: dict[tuple[Any, ...], str] = {}
     for key, weight, factors in groups.values():

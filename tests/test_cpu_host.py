@@ -248,3 +248,32 @@ def test_packed_staging_folds_strength_into_a_in_the_compute_dtype() -> None:
     assert torch.equal(b, torch.cat([f.b for f in (f1, f2, f3)], dim=1).to(torch.bfloat16))
     # folding in float32 first would round differently for some elements
     assert not torch.equal(a[3:8], (f2.a * f2.strength).to(torch.bfloat16))
+
+
+def test_pinned_lora_factors_share_one_arena():
+    # from_state_dict packs every factor into one host buffer (256-byte aligned),
+    # so a merge stages a whole LoRA with one copy per GPU
+    from piper_offload_amd.lora import _DeviceArena
+
+    lora = _lora({"attn": (16, 24), "mlp": (32, 24)}, 4, 13, bias=True, dtype=torch.bfloat16)
+    arena = lora._arena
+    assert arena is not None and arena.dtype is torch.uint8
+    base = arena.data_ptr()
+    for f in lora.targets.values():
+        for t in (f.a, f.b, f.bias):
+            off = t.data_ptr() - base
+            assert off % 256 == 0 and 0 <= off < arena.numel()
+    assert lora.stage_on(torch.device("cpu")) is None  # GPUs only
+    # a device arena maps every factor to the same values (a CPU copy stands in for the GPU one)
+    dev = _DeviceArena(arena, arena.clone())
+    for f in lora.targets.values():
+        for t in (f.a, f.b, f.bias):
+            v = dev.view(t)
+            assert v is not None and v.dtype is t.dtype and torch.equal(v, t) and v.data_ptr() != t.data_ptr()
+    assert dev.view(torch.zeros(4)) is None
+    # the converted dtype is what the arena holds
+    lora32 = _lora({"attn": (16, 24)}, 4, 14, dtype=torch.float32)
+    f32 = LoRA.from_state_dict({"attn.lora_A.weight": lora32.targets["attn.weight"].a,
+                                "attn.lora_B.weight": lora32.targets["attn.weight"].b}, dtype=torch.bfloat16)
+    assert f32.targets["attn.weight"].a.dtype is torch.bfloat16
+    assert torch.equal(f32.targets["attn.weight"].a, lora32.targets["attn.weight"].a.to(torch.bfloat16))
