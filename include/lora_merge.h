@@ -226,7 +226,8 @@ int lm_dense_merge(void* w, int64_t M, int64_t N, int64_t ldw, const lm_lora* lo
  * a: [rank, K]; b: [N, rank]; bias: [N] or NULL; all row-major in `dtype`,
  * 8-byte aligned, K % 4 == 0, rank 1..64, at most 8 factors and 16 rank
  * chunks of 16 in all.  Workspace: lm_routed_workspace_size bytes, 256-byte
- * aligned. */
+ * aligned; that size is 0 (and `workspace` may be NULL) for T <= 16, which
+ * runs as a single launch. */
 typedef struct lm_routed_factor {
   const void* a;
   const void* b;

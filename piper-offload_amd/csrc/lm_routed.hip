@@ -12,7 +12,8 @@
 //   total  = part_0, then dt(total + part_i)
 //   out    = dt(y + total)
 //
-// Three kernels:
+// At most 16 tokens (decode): one kernel, k_routed_small, and no workspace.
+// Otherwise three:
 // * k_routed_down: MFMA x A^T over a K split per workgroup; the partial sums
 //   of all factors' rank chunks go to an fp32 workspace [S][T][C * 16]
 //   (C = sum of ceil(r_i / 16));
@@ -287,6 +288,137 @@ __global__ __launch_bounds__(RT_NW * 64) void k_routed_up(RoutedArgs a) {
   }
 }
 
+// ---- one launch for at most 16 tokens (decode) ---------------------------------
+// Three launches cost more than their work when T is small.  Here every
+// workgroup computes the whole down projection of the one token tile (its
+// RT_SNW waves split K, one round of RT_DU loads each at K = 4096; the sums
+// meet in LDS), applies the first two roundings into LDS, then each wave
+// finishes one 64-column tile as k_routed_up does.  The wave's y values and
+// (for at most two rank chunks) B operands are requested before the down
+// projection, so their latency overlaps it.  Every workgroup recomputes the
+// down projection (x and A are read from L2 after the first).
+constexpr int RT_SNW = 16;
+
+template <bool HALF, int CMAX>
+__global__ __launch_bounds__(RT_SNW * 64) void k_routed_small(RoutedArgs a) {
+  constexpr int DT = HALF ? F16 : BF16;
+  constexpr bool PRE = CMAX <= 2;  // B operands loaded up front
+  __shared__ float sh[RT_SNW][64][4];
+  __shared__ uint32_t spw[16][RT_MAX_CHUNKS * 8];      // ps of token t: ranks 2j, 2j + 1 in word j
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15, g = lane >> 4;
+  const int64_t mt = (int64_t)blockIdx.x * RT_SNW + wave;
+  const bool tile = mt < (a.N + 63) / 64;
+  const int64_t c0 = mt * 64 + 16 * g, t = rl;
+  const bool tok = tile && t < a.T, full = (a.N & 7) == 0 && c0 + 16 <= a.N;
+  const int p = lane & 15;
+  uint4 y0 = make_uint4(0, 0, 0, 0), y1 = y0;
+  if (tok && full) {
+    const uint4* yr4 = (const uint4*)(a.y + t * a.N + c0);
+    y0 = yr4[0];
+    y1 = yr4[1];
+  }
+  v4i16 bo[PRE ? CMAX : 1][4];
+  if constexpr (PRE) {
+#pragma unroll
+    for (int c = 0; c < CMAX; ++c) {
+#pragma unroll
+      for (int k4 = 0; k4 < 4; ++k4) bo[c][k4] = (v4i16){0, 0, 0, 0};
+      if (tile && c < a.nchunks) {
+        const int i = a.cfac[c], cc = c - a.chunk0[i];
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4)
+          bo[c][k4] = load4(a.b[i], a.N, a.rank[i], mt * 64 + 16 * (p >> 2) + 4 * k4 + (p & 3), 16 * cc + 4 * g);
+      }
+    }
+  }
+  constexpr int RT_DU = 8;
+  for (int c = 0; c < a.nchunks; ++c) {
+    const int i = a.cfac[c], cc = c - a.chunk0[i];
+    v4f32 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t k0 = 32 * wave; k0 < a.K; k0 += 32 * RT_SNW * RT_DU) {
+      rt_v8i16 av[RT_DU], xv[RT_DU];
+#pragma unroll
+      for (int u = 0; u < RT_DU; ++u) {
+        const int64_t k = k0 + (int64_t)u * 32 * RT_SNW + 8 * g;
+        const bool in = k < a.K;
+        av[u] = in ? load8(a.a[i], a.rank[i], a.K, 16 * cc + rl, k) : (rt_v8i16){0, 0, 0, 0, 0, 0, 0, 0};
+        xv[u] = in ? load8(a.x, a.T, a.K, rl, k) : (rt_v8i16){0, 0, 0, 0, 0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < RT_DU; ++u) acc = mfma32<HALF>(av[u], xv[u], acc);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sh[wave][lane][j] = acc[j];
+    __syncthreads();
+    if (wave == 0) {  // lane: token rl, ranks 16 cc + 4 g + 0..3
+      uint32_t w2[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float v[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          float sum = 0.0f;
+          for (int w = 0; w < RT_SNW; ++w) sum += sh[w][lane][2 * h + e];
+          v[e] = round_dt<DT>(round_dt<DT>(sum) * a.s[i]);
+        }
+        w2[h] = (uint32_t)bits_dt<DT>(v[0]) | ((uint32_t)bits_dt<DT>(v[1]) << 16);
+      }
+      spw[rl][c * 8 + 2 * g] = w2[0];
+      spw[rl][c * 8 + 2 * g + 1] = w2[1];
+    }
+    __syncthreads();
+  }
+  if (!tile) return;
+  float total[16];
+  v4f32 acc[4];
+#pragma unroll
+  for (int c = 0; c < CMAX; ++c) {
+    if (c < a.nchunks) {
+      const int i = a.cfac[c], cc = c - a.chunk0[i];
+      if (cc == 0) {
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) acc[k4] = (v4f32){0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      const v4i16 psv = __builtin_bit_cast(v4i16, make_uint2(spw[rl][c * 8 + 2 * g], spw[rl][c * 8 + 2 * g + 1]));
+#pragma unroll
+      for (int k4 = 0; k4 < 4; ++k4) {
+        v4i16 bv;
+        if constexpr (PRE)
+          bv = bo[c][k4];
+        else
+          bv = load4(a.b[i], a.N, a.rank[i], mt * 64 + 16 * (p >> 2) + 4 * k4 + (p & 3), 16 * cc + 4 * g);
+        acc[k4] = mfma1<HALF>(bv, psv, acc[k4]);
+      }
+      if (c + 1 == a.nchunks || a.cfac[c + 1] != i) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          float part = round_dt<DT>(acc[j >> 2][j & 3]);
+          if (a.bias[i] && c0 + j < a.N)
+            part = round_dt<DT>(part + round_dt<DT>(val_dt<DT>(a.bias[i][c0 + j]) * a.s[i]));
+          total[j] = i == 0 ? part : round_dt<DT>(total[j] + part);
+        }
+      }
+    }
+  }
+  if (!tok || c0 >= a.N) return;
+  uint16_t* orow = a.out + t * a.N + c0;
+  if (full) {
+    const uint32_t yw[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+    uint32_t ow[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float lo = round_dt<DT>(val_dt<DT>(yw[k] & 0xffffu) + total[2 * k]);
+      const float hi = round_dt<DT>(val_dt<DT>(yw[k] >> 16) + total[2 * k + 1]);
+      ow[k] = (uint32_t)bits_dt<DT>(lo) | ((uint32_t)bits_dt<DT>(hi) << 16);
+    }
+    ((uint4*)orow)[0] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    ((uint4*)orow)[1] = make_uint4(ow[4], ow[5], ow[6], ow[7]);
+  } else {
+    const uint16_t* yr = a.y + t * a.N + c0;
+    for (int j = 0; j < 16 && c0 + j < a.N; ++j) orow[j] = bits_dt<DT>(round_dt<DT>(val_dt<DT>(yr[j]) + total[j]));
+  }
+}
+
 // K splits of the down projection: about 2048 workgroups in all (the kernel
 // streams x, so it needs occupancy), at least 256 columns of K per split
 int64_t routed_splits(int64_t T, int64_t K) {
@@ -300,6 +432,7 @@ int64_t routed_splits(int64_t T, int64_t K) {
 }  // namespace
 
 extern "C" size_t lm_routed_workspace_size(int64_t T, int64_t K, const lm_routed_factor* factors, int32_t count) {
+  if (T <= 16) return 0;  // the single-launch path keeps everything in LDS
   int chunks = 0;
   for (int i = 0; i < count && factors; ++i) chunks += (factors[i].rank + 15) / 16;
   const int64_t S = routed_splits(T, K);
@@ -341,7 +474,7 @@ extern "C" int lm_routed_residual(const void* x, const void* y, void* out, int64
   }
   if (T == 0) return LM_OK;
   const size_t need = lm_routed_workspace_size(T, K, factors, count);
-  if (!workspace || workspace_bytes < need)
+  if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(LM_EWORKSPACE, "routed residual workspace too small: %zu < %zu bytes", workspace_bytes, need);
   if (((uintptr_t)workspace & 255) != 0) return fail(LM_EINVAL, "workspace must be 256-byte aligned");
   const int64_t tiles = (T + 15) / 16;
@@ -372,6 +505,18 @@ extern "C" int lm_routed_residual(const void* x, const void* y, void* out, int64
   hipStream_t st = (hipStream_t)stream;
   TimedLaunch timed("routed", st);
   const dim3 block(RT_NW * 64);
+  if (T <= 16) {  // one token tile: a single launch
+    const dim3 sgrid((unsigned)((ntiles + RT_SNW - 1) / RT_SNW)), sblock(RT_SNW * 64);
+#define RT_SM(H_)                                                                                 \
+  if (chunks <= 1) hipLaunchKernelGGL((k_routed_small<H_, 1>), sgrid, sblock, 0, st, a);      \
+  else if (chunks <= 2) hipLaunchKernelGGL((k_routed_small<H_, 2>), sgrid, sblock, 0, st, a); \
+  else if (chunks <= 4) hipLaunchKernelGGL((k_routed_small<H_, 4>), sgrid, sblock, 0, st, a); \
+  else hipLaunchKernelGGL((k_routed_small<H_, RT_MAX_CHUNKS>), sgrid, sblock, 0, st, a);
+    if (dtype == LM_F16) { RT_SM(true) } else { RT_SM(false) }
+#undef RT_SM
+    LAUNCH_CHECK();
+    return LM_OK;
+  }
   const dim3 ugrid((unsigned)colgroups, (unsigned)tgroups);
 #define RT_UP(H_)                                                                                    \
   if (chunks <= 1) hipLaunchKernelGGL((k_routed_up<H_, 1>), ugrid, block, 0, st, a);                \

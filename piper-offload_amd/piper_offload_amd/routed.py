@@ -9,7 +9,8 @@ the factors there and returns ``output + residual`` with
 computed by ``lm_routed_residual``: an MFMA down projection into a small fp32
 workspace, then one kernel that applies the reference's roundings (every
 step in the output dtype, matmuls accumulated in fp32), multiplies by B and
-adds into a new output, reading and writing the ``[T, N]`` output once.
+adds into a new output, reading and writing the ``[T, N]`` output once.  At
+most 16 tokens (decode) run as a single launch with no workspace.
 
 Differences from the reference, on purpose:
 
@@ -93,9 +94,11 @@ def routed_residual(x: torch.Tensor, factors: Sequence[RoutedFactor], output: to
     handle = L.lib()
     ws_bytes = handle.lm_routed_workspace_size(t, k, arr, len(factors))
     with torch.cuda.device(device):
-        ws = L.workspace(ws_bytes, device)
+        # at most 16 tokens need no workspace (one launch, LDS only)
+        ws = L.workspace(ws_bytes, device) if ws_bytes else None
         rc = handle.lm_routed_residual(x2.data_ptr(), y2.data_ptr(), out.data_ptr(), t, k, n, L.torch_dtype_id(dtype),
-                                       arr, len(factors), L.aligned_ptr(ws), ws_bytes, L.stream_ptr(device))
+                                       arr, len(factors), None if ws is None else L.aligned_ptr(ws), ws_bytes,
+                                       L.stream_ptr(device))
     L.check(rc)
     del keep
     return out.view(output.shape)

@@ -98,6 +98,13 @@ def test_version_and_workspace_queries_need_no_gpu() -> None:
     assert 256 <= small < big
     assert h.lm_workspace_size(4096, 4096, 16) % 256 == 0
     assert h.lm_stack_workspace_extra(224) > h.lm_stack_workspace_extra(1)
+    # routed residual: at most 16 tokens run as one launch with no workspace
+    fs = (L.RoutedFactor * 2)()
+    fs[0].rank, fs[1].rank = 16, 40
+    assert h.lm_routed_workspace_size(1, 4096, fs, 2) == 0
+    assert h.lm_routed_workspace_size(16, 4096, fs, 2) == 0
+    w17 = h.lm_routed_workspace_size(17, 4096, fs, 2)
+    assert w17 >= 17 * 4 * 16 * (4 + 2) and w17 % 256 == 0
 
 
 def test_invalid_arguments_fail_loudly_before_any_device_work() -> None:

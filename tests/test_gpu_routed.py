@@ -80,6 +80,9 @@ def _check(got: torch.Tensor, x, y, fs, dtype):
     (64, 256, 384, [16, 32], True),      # two factors with biases
     (200, 1024, 2048, [64], False),      # rank 64
     (16, 4100, 96, [8, 8, 8], True),     # K not a multiple of 16, three factors
+    (8, 1024, 2048, [64, 16], True),     # one launch (T <= 16): five rank chunks
+    (3, 256, 100, [16], False),          # one launch, N not a multiple of 8
+    (17, 512, 256, [16], False),         # one token past the single-launch path
     (300, 2048, 14336 // 8, [16], False),
 ])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
