@@ -569,11 +569,21 @@ def cpu_baseline(kind: str, stochastic: bool, budget_s: float, gguf_type: str = 
             "sample": f"{what} of one {rows} x {shape_note}, {reps} repeats in {t:.1f} s"}
 
 
-def _traffic(name: str) -> int | None:
+def _traffic(name: str, kbytes: int, stochastic: bool) -> int | None:
+    """Measured HBM bytes per launch, only for the configuration they were measured on.
+
+    A record applies when its algorithmic bytes equal this run's (same shapes,
+    layers, tokens) and, where it names one, its rounding mode matches.
+    """
     path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
     try:
         with open(path) as f:
-            return int(json.load(f)["hbm_bytes_per_launch"])
+            rec = json.load(f)
+        if int(rec["algorithmic_bytes_per_launch"]) != int(kbytes):
+            return None
+        if "stochastic" in rec and bool(rec["stochastic"]) != stochastic:
+            return None
+        return int(rec["hbm_bytes_per_launch"])
     except (OSError, KeyError, ValueError):
         return None
 
@@ -662,7 +672,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": None if achieved is None else round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": _traffic(wl.name),
+            "traffic": _traffic(wl.name, kbytes, stochastic),
         },
         "cpu_baseline": cpu,
     }
