@@ -4,12 +4,15 @@
 //
 // A wave works on one 16-row x 128-column macro tile at a time (see
 // k_q8_fast for how waves pick tiles), and a lane holds row (lane & 15) and
-// the 32 columns 32*(lane >> 4) .. +31 of it -- exactly one Q8_0 block, so the block max, the new d and the codes never
-// leave the lane.  Blocks start at even byte offsets; a lane reads its block
-// through a dword-aligned 36-byte window (two 16-byte loads and one 4- or
-// 2-byte load, never past the block's last byte) and writes it back as eight
-// dword-aligned dwords plus one 2-byte store.  Every block is read and
-// written by one lane, so the merge may run in place.
+// the 32 columns 32*(lane >> 4) .. +31 of it -- exactly one Q8_0 block, so
+// the block max, the new d and the codes never leave the lane.  The tile's
+// bytes are 16 row segments of 136 bytes (rows are rowbytes apart, segments
+// 8-byte aligned).  The wave reads them as 272 consecutive 8-byte chunks
+// (17 per row, a few cache lines per instruction), stages them in its own
+// LDS slot, and each lane reads its block from there through a dword-aligned
+// 36-byte window (blocks start at even offsets).  The new blocks go back into
+// the slot and out in the same chunks, so every byte is written once and the
+// merge may run in place.
 //
 // Arithmetic (bf16 compute, as the generic block kernel):
 //   base   = bf16(bf16(d) * q)                   (P/gguf_dequant.py:57-61)
@@ -29,31 +32,51 @@ struct Q8Args {
   uint64_t seed;
 };
 
+// An item's bytes as the wave loads them: chunk c = lane + 64 i (i < 5) is
+// bytes 8 (c % 17) .. + 7 of row c / 17 of the item's 16 x 136-byte segment
+// (rows of the tile are rowbytes apart in memory); chunks 272.. do not exist.
+struct Q8Raw {
+  lm_u32x2 c[5];
+};
+constexpr int Q8_CHUNKS = 16 * 17;
+constexpr int Q8_SLOT = 64 * 5 * 8;  // LDS bytes per wave: 320 chunks (272 used)
 template <int NKC>
-struct Q8TileIn {
-  uint32_t win[9];
+struct Q8Ops {
   v4i16 aop[8][NKC];
+  v4i16 bop[NKC];
 };
 
-template <int NKC>
-DEV void q8_load_tile(const uint8_t* wbase, int sh, const uint16_t* at, int mt, Q8TileIn<NKC>& t) {
-  constexpr int RPAD = NKC * 16;
-  typedef uint32_t u4a4 __attribute__((ext_vector_type(4), aligned(4)));
-  const uint8_t* p = wbase + (int64_t)mt * 136;  // 4 blocks per macro tile
-  const u4a4 v0 = *(const u4a4*)p, v1 = *(const u4a4*)(p + 16);
-  t.win[0] = v0[0];
-  t.win[1] = v0[1];
-  t.win[2] = v0[2];
-  t.win[3] = v0[3];
-  t.win[4] = v1[0];
-  t.win[5] = v1[1];
-  t.win[6] = v1[2];
-  t.win[7] = v1[3];
-  // sh == 0: the block ends at byte 34 of the window
-  t.win[8] = sh ? *(const uint32_t*)(p + 32) : (uint32_t)*(const uint16_t*)(p + 32);
-  const uint16_t* a = at + (int64_t)mt * (128 * RPAD);
+// A lane's addresses within one item: the item's row group and tile are
+// wave-uniform (scalar bases); the lane parts are 32-bit offsets.
+struct Q8Lane {
+  uint32_t aoff;  // A^T operand offset (elements) within a tile
+  uint32_t boff;  // Bp operand offset (elements) within a row group
+};
+
+// chunk offsets of the lane within a row group; rows at or past M read row
+// M - 1 (their bytes are never stored)
+DEV void q8_chunk_offsets(int lane, int rows_left, int64_t rowbytes, uint32_t (&off)[5]) {
 #pragma unroll
-  for (int k = 0; k < 8; ++k) load_kchunks<NKC>(a + 4 * k * RPAD, t.aop[k]);
+  for (int i = 0; i < 5; ++i) {
+    const int c = lane + 64 * i < Q8_CHUNKS ? lane + 64 * i : 0;
+    const int r = c / 17;
+    const int rc = r < rows_left ? r : rows_left - 1;
+    off[i] = (uint32_t)rc * (uint32_t)rowbytes + (uint32_t)(c - 17 * r) * 8u;
+  }
+}
+
+DEV void q8_load_raw(const Q8Args& a, const uint32_t (&off)[5], int64_t rg, int mt, int64_t rowbytes, Q8Raw& t) {
+  const LM_GLOBAL uint8_t* p = (const LM_GLOBAL uint8_t*)a.q + rg * 16 * rowbytes + (uint32_t)(mt * 136);
+#pragma unroll
+  for (int i = 0; i < 5; ++i) t.c[i] = *(const LM_GLOBAL lm_u32x2*)(p + off[i]);
+}
+template <int NKC>
+DEV void q8_load_ops(const Q8Args& a, const Q8Lane& L, int64_t rg, int mt, Q8Ops<NKC>& t) {
+  constexpr int RPAD = NKC * 16;
+  const LM_GLOBAL uint16_t* at = (const LM_GLOBAL uint16_t*)a.at + (uint32_t)(mt * (128 * RPAD)) + L.aoff;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, t.aop[k]);
+  load_kchunks_g<NKC>((const LM_GLOBAL uint16_t*)a.bp + rg * (16 * RPAD) + L.boff, t.bop);
 }
 
 // roundf(x) (half away from zero) for |x| < 2^23 in two instructions: adding
@@ -66,61 +89,99 @@ DEV int round_half_away(float x) {
   return (int)(x + __builtin_copysignf(0.49999997f, x));
 }
 
+// One item: the lane's block (row `row`, columns 128 mt + 32 g ..) merged,
+// requantized and stored at `wout` (the window base of the output).
+//
+// Stochastic rounding of x = RN(m id) with the reference's rule (floor(x) or
+// floor(x) + 1, up iff h 2^-16 < frac(x); x itself when it is an integer or
+// outside (-127, 127), where the round-half-away code is +-127 since
+// |x| <= 127 (1 + 2^-22)): with Y = 65536 x clamped to [-127, 127] 65536
+// (exact: a power-of-two scaling of |x| < 2^7) and T = ceil(Y), the code is
+// (T + 65535 - h) >> 16, whose low byte is bits 16..23 of T + 65535 - h.
 template <int NKC, bool SR>
-DEV void q8_tile(const Q8Args& a, const Q8TileIn<NKC>& in, const v4i16 (&bop)[NKC], int sh, int64_t row, int mt,
-                 int lane, uint8_t* wout) {
+DEV void q8_tile(const Q8Args& a, const Q8Raw& raw, const Q8Ops<NKC>& in, uint8_t* slot, int sh, int64_t row,
+                 int mt, int lane, int rows_left, const uint32_t (&off)[5], LM_GLOBAL uint8_t* p) {
   float d[32];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    const v4f32 acc = mfma_chain<NKC, false>(in.aop[k], bop);
+    const v4f32 acc = mfma_chain<NKC, false>(in.aop[k], in.bop);
     d[4 * k + 0] = acc[0];
     d[4 * k + 1] = acc[1];
     d[4 * k + 2] = acc[2];
     d[4 * k + 3] = acc[3];
   }
-  // the block's 34 bytes from byte sh of the window: [d lo][d hi][q0..q31]
+  // stage the item's bytes in the wave's LDS slot (chunk c at byte 8 c, so
+  // row r of the segment starts at byte 136 r), then read the lane's block
+  // through its dword-aligned 36-byte window: [d lo][d hi][q0..q31] from byte sh
+#pragma unroll
+  for (int i = 0; i < 5; ++i) *(lm_u32x2*)(slot + 8 * (lane + 64 * i)) = raw.c[i];
+  const int bofs = 136 * (lane & 15) + 34 * (lane >> 4);  // the block's first byte in the slot
+  const uint32_t* wsrc = (const uint32_t*)(slot + bofs - sh);
+  uint32_t win[9];
+#pragma unroll
+  for (int k = 0; k < 9; ++k) win[k] = wsrc[k];
   uint32_t blk[9];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) blk[k] = __builtin_amdgcn_alignbyte(in.win[k + 1], in.win[k], sh);
-  blk[8] = in.win[8] >> (8 * sh);
+  for (int k = 0; k < 8; ++k) blk[k] = __builtin_amdgcn_alignbyte(win[k + 1], win[k], sh);
+  blk[8] = win[8] >> (8 * sh);
   const float dd = bf16r(f16_val(blk[0] & 0xffffu));
   float m[32];
   float amax = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    const int bi = j + 2;
-    const float base = bf16r(dd * (float)(int8_t)(blk[bi >> 2] >> (8 * (bi & 3))));
-    m[j] = bf16r(__builtin_fmaf(d[j], a.strength, base));
-    amax = __builtin_fmaxf(amax, __builtin_fabsf(m[j]));
+  for (int j = 0; j < 32; j += 2) {
+    const int b0 = j + 2, b1 = j + 3;
+    const float base0 = bf16r(dd * (float)(int8_t)(blk[b0 >> 2] >> (8 * (b0 & 3))));
+    const float base1 = bf16r(dd * (float)(int8_t)(blk[b1 >> 2] >> (8 * (b1 & 3))));
+    m[j] = bf16r(__builtin_fmaf(d[j], a.strength, base0));
+    m[j + 1] = bf16r(__builtin_fmaf(d[j + 1], a.strength, base1));
+    amax = max3_abs(amax, m[j], m[j + 1]);
   }
   const float dq = amax / 127.0f;
   const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
-  uint32_t rw[16];  // element j's 16-bit draw is half (j & 1) of rw[j >> 1]
-  if constexpr (SR) sr_words_aligned<32>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4)), rw);
   uint32_t ob[9];
   ob[0] = (uint32_t)f16_bits(dq);
+  if constexpr (SR) {
+    uint32_t nw[16];  // 65535 - h of element j in half (j & 1) of nw[j >> 1]
+    sr_nwords_aligned<32>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4)), nw);
+    uint32_t y[32];
 #pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    const float x = m[j] * id;
-    int q = round_half_away(x);
-    if constexpr (SR) q = sr_int(x, q, (j & 1) ? (rw[j >> 1] >> 16) : (rw[j >> 1] & 0xffffu), -127.0f, 127.0f);
-    const int bi = j + 2;
-    if ((bi & 3) == 0) ob[bi >> 2] = 0u;
-    ob[bi >> 2] |= ((uint32_t)q & 0xffu) << (8 * (bi & 3));
+    for (int j = 0; j < 32; ++j) {
+      const float y16 = __builtin_amdgcn_fmed3f((m[j] * id) * 65536.0f, -127.0f * 65536.0f, 127.0f * 65536.0f);
+      const uint32_t tneg = (uint32_t)cvt_flr_neg(y16);  // -ceil(Y)
+      y[j] = (j & 1) ? (nw[j >> 1] >> 16) - tneg : sub_lo16(nw[j >> 1], tneg);
+    }
+    // code j is byte 2 + j of the block: word (j + 2) >> 2
+    ob[0] |= __builtin_amdgcn_perm(y[1], y[0], 0x06020000u) & 0xffff0000u;
+#pragma unroll
+    for (int k = 1; k < 8; ++k) ob[k] = pack_byte2s(y[4 * k - 2], y[4 * k - 1], y[4 * k], y[4 * k + 1]);
+    ob[8] = __builtin_amdgcn_perm(y[31], y[30], 0x0c0c0602u);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const int q = round_half_away(m[j] * id);
+      const int bi = j + 2;
+      if ((bi & 3) == 0) ob[bi >> 2] = 0u;
+      ob[bi >> 2] |= ((uint32_t)q & 0xffu) << (8 * (bi & 3));
+    }
   }
-  typedef uint32_t u4a4 __attribute__((ext_vector_type(4), aligned(4)));
-  uint8_t* p = wout + (int64_t)mt * 136;
+  // the new block back into the slot, then the segment out in chunks
   if (sh == 0) {
-    *(u4a4*)p = (u4a4){ob[0], ob[1], ob[2], ob[3]};
-    *(u4a4*)(p + 16) = (u4a4){ob[4], ob[5], ob[6], ob[7]};
-    *(uint16_t*)(p + 32) = (uint16_t)ob[8];
-  } else {  // the block starts 2 bytes into the window: one short, then 8 aligned dwords
-    *(uint16_t*)(p + 2) = (uint16_t)ob[0];
-    uint32_t s[8];
+    uint32_t* d32 = (uint32_t*)(slot + bofs);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) s[k] = __builtin_amdgcn_alignbyte(ob[k + 1], ob[k], 2);
-    *(u4a4*)(p + 4) = (u4a4){s[0], s[1], s[2], s[3]};
-    *(u4a4*)(p + 20) = (u4a4){s[4], s[5], s[6], s[7]};
+    for (int k = 0; k < 8; ++k) d32[k] = ob[k];
+    *(uint16_t*)(slot + bofs + 32) = (uint16_t)ob[8];
+  } else {  // the block starts 2 bytes into a dword: one short, then 8 aligned dwords
+    *(uint16_t*)(slot + bofs) = (uint16_t)ob[0];
+    uint32_t* d32 = (uint32_t*)(slot + bofs + 2);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) d32[k] = __builtin_amdgcn_alignbyte(ob[k + 1], ob[k], 2);
+  }
+  (void)row;
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    const int c = lane + 64 * i;
+    if (c < Q8_CHUNKS && (rows_left == 16 || c / 17 < rows_left))
+      *(LM_GLOBAL lm_u32x2*)(p + off[i]) = *(const lm_u32x2*)(slot + 8 * c);
   }
 }
 
@@ -130,57 +191,98 @@ constexpr int Q8_NW = 4;
 // at once, and every wave walks the work items item = gwave, gwave + waves,
 // ... where item = row_group * ntiles + tile (one 16-row x 128-column tile).
 // Single tensors are too small to amortise a wave's launch over a few tiles
-// (a [13824, 5120] tensor is 34560 tiles), so waves stay resident, prefetch
-// their next item and the last round is at most one tile per wave.  Blocks are
-// independent, so no two waves need each other's results.  A lane's block
-// starts 2 * (g & 1) bytes past a dword boundary in every item (rows are
-// 136k bytes long), so its window shift is fixed.
+// (a [13824, 5120] tensor is 34560 tiles), so waves stay resident and the last
+// round is at most one tile per wave.  Blocks are independent, so no two
+// waves need each other's results.  The item's row group and tile are
+// wave-uniform and advance by the fixed stride without a division; two
+// register sets alternate so that the next item's loads are in flight while
+// the current one is merged (loads complete in order, so the wait for the
+// current item never waits for the next).  A lane's block starts 2 (g & 1)
+// bytes past a dword boundary in every item (rows are 136 k bytes long), so
+// its window shift is fixed.
+// the second bound is waves per SIMD: rank 16 fits 128 VGPRs (4 waves).
+// Five waves (96 VGPRs) spill and run slower.
 template <int NKC, bool SR>
-__global__ __launch_bounds__(Q8_NW * 64) void k_q8_fast(Q8Args a) {
+constexpr int q8_min_waves() { return NKC == 1 ? 4 : 1; }
+
+template <int NKC, bool SR>
+__global__ __launch_bounds__(Q8_NW * 64, (q8_min_waves<NKC, SR>())) void k_q8_fast(Q8Args a) {
   const int lane = threadIdx.x & 63, rl = lane & 15, g = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   constexpr int RPAD = NKC * 16;
   const int ntiles = (int)(a.N >> 7);
-  const int64_t nitems = ((a.M + 15) / 16) * (int64_t)ntiles;
+  const int64_t nrg = (a.M + 15) / 16;
   const int64_t stride = (int64_t)gridDim.x * Q8_NW;
-  int64_t item = (int64_t)blockIdx.x * Q8_NW + (threadIdx.x >> 6);
-  if (item >= nitems) return;
+  const int64_t item0 = (int64_t)blockIdx.x * Q8_NW + wv;
+  if (item0 >= nrg * ntiles) return;
+  int64_t rg = item0 / ntiles;
+  int mt = (int)(item0 - rg * ntiles);
+  const int64_t srg = stride / ntiles;
+  const int smt = (int)(stride - srg * ntiles);
+  auto advance = [&](int64_t& r, int& t) {
+    t += smt;
+    r += srg;
+    if (t >= ntiles) {
+      t -= ntiles;
+      ++r;
+    }
+  };
   const int64_t rowbytes = a.N / 32 * 34;
   const int sh = 2 * (g & 1);
   const int p = lane & 15;
-  const uint16_t* at = a.at + (int64_t)(32 * (p >> 2) + (p & 3)) * RPAD + g * (NKC * 4);
-  // per item: the lane's row, its clamp (loads stay in bounds; rows past M store nothing) and window base
-  auto locate = [&](int64_t it, int64_t& row, int& mt, int64_t& wofs) {
-    const int64_t rg = it / ntiles;
-    mt = (int)(it - rg * ntiles);
-    row = rg * 16 + rl;
-    const int64_t rowc = row < a.M ? row : a.M - 1;
-    wofs = rowc * rowbytes + (int64_t)g * 34 - sh;
+  __shared__ __attribute__((aligned(16))) uint8_t q8_lds[Q8_NW * Q8_SLOT];
+  uint8_t* slot = q8_lds + wv * Q8_SLOT;  // the wave's own: no barriers
+  Q8Lane L;
+  L.aoff = (uint32_t)((32 * (p >> 2) + (p & 3)) * RPAD + g * (NKC * 4));
+  L.boff = (uint32_t)(rl * RPAD + g * (NKC * 4));
+  uint32_t off_full[5];
+  q8_chunk_offsets(lane, 16, rowbytes, off_full);
+  // chunk offsets of row group r (only the last one can be short)
+  auto offsets = [&](int64_t r, uint32_t (&off)[5]) {
+    const int64_t left = a.M - r * 16;
+    if (left >= 16) {
+#pragma unroll
+      for (int i = 0; i < 5; ++i) off[i] = off_full[i];
+    } else {
+      q8_chunk_offsets(lane, (int)left, rowbytes, off);
+    }
   };
-  int64_t row, nrow;
-  int mt, nmt;
-  int64_t wofs, nwofs;
-  locate(item, row, mt, wofs);
-  Q8TileIn<NKC> cur;
-  v4i16 bop[NKC];
-  q8_load_tile<NKC>(a.q + wofs, sh, at, mt, cur);
-  load_bop<NKC>(a.bp, row, lane, bop);  // Bp holds ceil(M/16)*16 rows
-  for (;;) {
-    const int64_t next = item + stride;
-    const bool more = next < nitems;
-    locate(more ? next : item, nrow, nmt, nwofs);
-    Q8TileIn<NKC> nxt;
-    v4i16 nbop[NKC];
-    q8_load_tile<NKC>(a.q + nwofs, sh, at, nmt, nxt);
-    load_bop<NKC>(a.bp, nrow, lane, nbop);
-    if (row < a.M) q8_tile<NKC, SR>(a, cur, bop, sh, row, mt, lane, a.q_out + wofs);
-    if (!more) break;
-    item = next;
-    row = nrow;
-    mt = nmt;
-    wofs = nwofs;
-    cur = nxt;
-    for (int k = 0; k < NKC; ++k) bop[k] = nbop[k];
+  auto load_raw = [&](int64_t r, int tile, Q8Raw& t) {
+    uint32_t off[5];
+    offsets(r, off);
+    q8_load_raw(a, off, r, tile, rowbytes, t);
+  };
+  auto run = [&](const Q8Raw& w, const Q8Ops<NKC>& t, int64_t r, int tile) {
+    uint32_t off[5];
+    offsets(r, off);
+    LM_GLOBAL uint8_t* out = (LM_GLOBAL uint8_t*)a.q_out + r * 16 * rowbytes + (uint32_t)(tile * 136);
+    const int64_t left = a.M - r * 16;
+    q8_tile<NKC, SR>(a, w, t, slot, sh, r * 16 + rl, tile, lane, left < 16 ? (int)left : 16, off, out);
+  };
+  // the MFMA operands (L2-resident) are requested at the start of their own
+  // item, then the next item's bytes, into alternating registers (loads
+  // complete in order: waiting for the operands never waits for the next item)
+  Q8Raw w0, w1;
+  int64_t rg1 = rg;
+  int mt1 = mt;
+  advance(rg1, mt1);
+  load_raw(rg, mt, w0);
+#define Q8_STEP(WC, WN)                                   \
+  {                                                       \
+    Q8Ops<NKC> ops;                                       \
+    q8_load_ops<NKC>(a, L, rg, mt, ops);                  \
+    if (rg1 < nrg) load_raw(rg1, mt1, WN);                \
+    run(WC, ops, rg, mt);                                 \
+    if (rg1 >= nrg) break;                                \
+    rg = rg1;                                             \
+    mt = mt1;                                             \
+    advance(rg1, mt1);                                    \
   }
+  for (;;) {
+    Q8_STEP(w0, w1)
+    Q8_STEP(w1, w0)
+  }
+#undef Q8_STEP
 }
 
 // workgroups resident at once on the current device for a kernel (cached per device)

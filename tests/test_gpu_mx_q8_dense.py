@@ -111,15 +111,19 @@ def test_q8_0_merge(shape, rank, strength, sr):
     assert np.array_equal(u8_np(pd), ref)
 
 
-def test_q8_0_merge_config4_full_size():
-    # [13824, 5120] rank 16, strength 1.0, RTN
+@pytest.mark.parametrize("sr", [False, True])
+def test_q8_0_merge_config4_full_size(sr):
+    # [13824, 5120] rank 16, strength 1.0, RTN (and SR): every
+    # wave of the persistent kernel walks many items
     rows, cols = 13824, 5120
     packed = O.q8_0_requant(bf16_np(normal_bf16((rows, cols), 0.02, 11)))
     b, a = lora_factors(rows, cols, 16, 12)
     pd = torch.from_numpy(packed).to(DEV)
     dense = K.dequantize_gguf(pd, 8, lora=(b.to(DEV), a.to(DEV), 1.0))
-    out = K.merge_q8_0_lora(pd, b.to(DEV), a.to(DEV), 1.0)
-    assert np.array_equal(u8_np(out), O.q8_0_requant(bf16_np(dense)))
+    seed = derive_seed("model.layers.0.mlp.down_proj.weight", 0) if sr else None
+    out = K.merge_q8_0_lora(pd, b.to(DEV), a.to(DEV), 1.0, rounding_seed=seed)
+    ref = O.q8_0_requant(bf16_np(dense), sr_mode=O.SR_PHILOX8 if sr else O.SR_OFF, seed=seed or 0)
+    assert np.array_equal(u8_np(out), ref)
 
 
 def test_gguf_adapter_in_place():
