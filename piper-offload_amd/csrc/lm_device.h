@@ -56,6 +56,44 @@ DEV uint16_t f16_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x
 DEV float f16_val(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 DEV float f16r(float x) { return f16_val(f16_bits(x)); }
 
+// ---- cross-lane reductions, VALU only (no LDS crossbar) -------------------
+// All 64 lanes must be active.  Within a 16-lane row: DPP (quad_perm xor 1,
+// xor 2; row_half_mirror; row_mirror).  Across rows: the gfx950 lane swaps.
+// v_permlane16_swap(x, x) returns x with odd rows exchanged for even rows in
+// one output and the other way round in the second, so one of the two
+// outputs holds x[l] and the other x[l ^ 16]; v_permlane32_swap likewise
+// for l ^ 32.
+DEV float lanes_max16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(f2u(x), f2u(x), false, false);
+  return __builtin_fmaxf(u2f(r[0]), u2f(r[1]));
+}
+DEV float lanes_min16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(f2u(x), f2u(x), false, false);
+  return __builtin_fminf(u2f(r[0]), u2f(r[1]));
+}
+DEV float lanes_max32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(f2u(x), f2u(x), false, false);
+  return __builtin_fmaxf(u2f(r[0]), u2f(r[1]));
+}
+DEV float lanes_min32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(f2u(x), f2u(x), false, false);
+  return __builtin_fminf(u2f(r[0]), u2f(r[1]));
+}
+template <int CTRL>
+DEV float dpp_f32(float x) {
+  return u2f((uint32_t)__builtin_amdgcn_update_dpp((int)f2u(x), (int)f2u(x), CTRL, 0xf, 0xf, false));
+}
+// max over all 64 lanes: after xor 1 and xor 2 a quad is uniform, so the
+// half-row mirror (lane i <-> 7 - i) pairs quad 0 with quad 1 and the row
+// mirror (i <-> 15 - i) pairs the two halves
+DEV float wave_max(float x) {
+  x = __builtin_fmaxf(x, dpp_f32<0xB1>(x));   // quad_perm [1, 0, 3, 2]
+  x = __builtin_fmaxf(x, dpp_f32<0x4E>(x));   // quad_perm [2, 3, 0, 1]
+  x = __builtin_fmaxf(x, dpp_f32<0x141>(x));  // row_half_mirror
+  x = __builtin_fmaxf(x, dpp_f32<0x140>(x));  // row_mirror
+  return lanes_max32(lanes_max16(x));
+}
+
 template <int DT>
 DEV float round_dt(float x) {
   if constexpr (DT == BF16) return bf16r(x);

@@ -63,12 +63,12 @@ __global__ __launch_bounds__(GROUP_NW * 64) void k_groups(RowArgs a, int scale_d
     }
   }
   if (g >= 32) {
-    vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, 16));
-    if constexpr (KIND == K_INT8) vmn = __builtin_fminf(vmn, __shfl_xor(vmn, 16));
+    vmx = lanes_max16(vmx);
+    if constexpr (KIND == K_INT8) vmn = lanes_min16(vmn);
   }
   if (g >= 64) {
-    vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, 32));
-    if constexpr (KIND == K_INT8) vmn = __builtin_fminf(vmn, __shfl_xor(vmn, 32));
+    vmx = lanes_max32(vmx);
+    if constexpr (KIND == K_INT8) vmn = lanes_min32(vmn);
   }
   // one store per group: its first lane
   const bool writer = live && (g >= 64 ? gi == 0 : (g == 32 ? (gi & 1) == 0 : true));

@@ -411,12 +411,8 @@ __device__ __forceinline__ void rows_body(const RowArgs& a, int64_t row0, int sc
                                                                   (int64_t)mt * 64, bop, s_in, z_in, m);
     account(m);
   }
-  vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, 16));
-  vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, 32));
-  if constexpr (KIND == K_INT8) {
-    vmn = __builtin_fminf(vmn, __shfl_xor(vmn, 16));
-    vmn = __builtin_fminf(vmn, __shfl_xor(vmn, 32));
-  }
+  vmx = lanes_max32(lanes_max16(vmx));
+  if constexpr (KIND == K_INT8) vmn = lanes_min32(lanes_min16(vmn));
   if (g == 0) {
     sh_mx[wave][rl] = vmx;
     sh_mn[wave][rl] = vmn;
@@ -742,8 +738,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
     }
   }
   float vmx = bf16r(amax);  // = max |bf16(merged)| of the lane
-  vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, 16));
-  vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, 32));
+  vmx = lanes_max32(lanes_max16(vmx));
   if ((lane >> 4) == 0) sh_mx[rl][wave] = vmx;
   __syncthreads();
   // Every lane derives its row's qparams from the NW wave maxima itself (the
@@ -864,11 +859,6 @@ struct BlkTraits {
   static constexpr int SPAN = (F == B_MXFP4 || F == B_MXE4M3 || F == B_MXE5M2 || F == B_Q8_0) ? 32 : 16;
 };
 
-__device__ __forceinline__ float warp_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
 
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
@@ -1234,8 +1224,8 @@ __global__ __launch_bounds__(256) void k_blocks(BlkArgs a) {
     }
   }
   if constexpr (PASS == P_AMAX) {
-    vmx = warp_max(vmx);
-    float nmn = warp_max(-vmn);
+    vmx = wave_max(vmx);
+    float nmn = wave_max(-vmn);
     if (lane == 0) {
       sh_red[0][wave] = vmx;
       sh_red[1][wave] = nmn;

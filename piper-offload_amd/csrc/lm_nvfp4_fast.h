@@ -292,8 +292,7 @@ DEV void nv_amax_body(const NvArgs& a, int64_t row0, int t0, int t1) {
     }
   }
   mx = rok ? mx : 0.0f;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o));
+  mx = wave_max(mx);
   if (lane == 0) sh[wave] = mx;
   __syncthreads();
   if (threadIdx.x == 0) {
