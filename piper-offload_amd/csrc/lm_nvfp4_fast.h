@@ -45,12 +45,16 @@ struct NvArgs {
 };
 struct NvStackItem {
   NvArgs a;
-  int64_t tile_begin;  // prefix of 16-row groups
+  int64_t tile_begin;  // prefix of 16-row groups (quant launches)
+  int64_t pair_begin;  // prefix of 32-row units (amax launch)
 };
 
 constexpr int NV_NW = 8;
 
-// decode the two e2m1 codes of byte `b` of w to fp32 (low nibble -> .x)
+// decode the two e2m1 codes of byte `b` of w to fp32 (low nibble -> .x).
+// The conversion's own scale operand stays 1.0: with a general bf16 block
+// scale it does not give the exact product (measured: the NVFP4 parity tests
+// fail), so the block scale is a separate multiply.
 DEV v2f32 e2m1_pair(uint32_t w, int b) {
   switch (b) {
     case 0: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
@@ -106,11 +110,12 @@ DEV void nv_load_tile(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
 // "update == 0 keeps the base" rule only changes the sign of a zero, so the
 // amax pass does not need it)
 template <int NKC, bool TWO>
-DEV void nv_merged(const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float strength, float gin, float (&m)[32]) {
+DEV void nv_merged_parts(const uint4& codes, uint32_t sc, const v4i16 (&aop)[8][NKC], const v4i16 (&bop)[NKC],
+                         float strength, float gin, float (&m)[32]) {
   float d[32];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    const v4f32 acc = mfma_chain<NKC, false>(in.aop[k], bop);
+    const v4f32 acc = mfma_chain<NKC, false>(aop[k], bop);
     d[4 * k + 0] = acc[0];
     d[4 * k + 1] = acc[1];
     d[4 * k + 2] = acc[2];
@@ -119,16 +124,20 @@ DEV void nv_merged(const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float stren
   float bs[2];
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    const float v = fp8_decode<E4M3>(in.sc, b);  // e4m3 is exact in bf16
+    const float v = fp8_decode<E4M3>(sc, b);  // e4m3 is exact in bf16
     bs[b] = TWO ? bf16r(v * gin) : v;
   }
-  const uint32_t w[4] = {in.codes.x, in.codes.y, in.codes.z, in.codes.w};
+  const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
     const v2f32 pr = e2m1_pair(w[q >> 2], q & 3);
 #pragma unroll
     for (int e = 0; e < 2; ++e) m[2 * q + e] = __builtin_fmaf(d[2 * q + e], strength, bf16r(pr[e] * bs[q >> 3]));
   }
+}
+template <int NKC, bool TWO>
+DEV void nv_merged(const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float strength, float gin, float (&m)[32]) {
+  nv_merged_parts<NKC, TWO>(in.codes, in.sc, in.aop, bop, strength, gin, m);
 }
 
 // Merged values of block B (the lane's columns 16B .. 16B+15) of a tile: the
@@ -264,34 +273,68 @@ DEV void nv_quant_tile(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&b
 // ---- pass bodies -------------------------------------------------------------
 // Rows past M load row M-1 (valid memory) and store nothing.
 // Tiles [t0, t1) of rows row0 .. row0+15 (the stack passes whole rows).
+// The amax pass keeps no register cache, so a wave merges 32 rows (two
+// 16-row groups) per macro tile: both groups' MFMAs share the tile's A^T
+// fragments, which halves the operand loads (L2) per element.  Rows
+// row0 .. row0 + 31; the second group exists when row0 + 16 < M.
+template <int NKC>
+struct NvAmaxIn {
+  uint4 codes[2];
+  uint32_t sc[2];
+  v4i16 aop[8][NKC];
+};
+template <int NKC>
+DEV void nv_amax_load(const NvLane<NKC>& l0, const NvLane<NKC>& l1, int mt, NvAmaxIn<NKC>& t) {
+  constexpr int RPAD = NKC * 16;
+  t.codes[0] = *(const uint4*)(l0.q + (int64_t)mt * 64);
+  t.codes[1] = *(const uint4*)(l1.q + (int64_t)mt * 64);
+  t.sc[0] = *(const uint16_t*)(l0.sc + (int64_t)mt * l0.sc_stride);
+  t.sc[1] = *(const uint16_t*)(l1.sc + (int64_t)mt * l1.sc_stride);
+  const uint16_t* at = l0.at + (int64_t)mt * (128 * RPAD);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) load_kchunks<NKC>(at + 4 * k * RPAD, t.aop[k]);
+}
 template <int NKC>
 DEV void nv_amax_body(const NvArgs& a, int64_t row0, int t0, int t1) {
   __shared__ float sh[NV_NW];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
-  const int64_t row = row0 + rl;
-  const bool rok = row < a.M;
-  const int64_t rowc = rok ? row : a.M - 1;
+  const int64_t r0 = row0 + rl, r1 = row0 + 16 + rl;
+  const bool rok0 = r0 < a.M, rok1 = r1 < a.M;
+  const bool second = row0 + 16 < a.M;  // wave-uniform
   const int ntiles = t1;
   const float gin = *a.gin;
   const float strength = a.strength;
-  const NvLane<NKC> l = nv_lane<NKC>(a, rowc, lane);
-  v4i16 bop[NKC];
-  load_bop<NKC>(a.bp, row, lane, bop);  // Bp holds ceil(M/16)*16 rows
-  float mx = 0.0f;
-  if (t0 + wave < ntiles) {
-    NvTileIn<NKC> cur;
-    nv_load_tile<NKC>(l, t0 + wave, cur);
-    for (int mt = t0 + wave; mt < ntiles; mt += NV_NW) {
-      NvTileIn<NKC> nxt;
-      nv_load_tile<NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
-      float m[32];
-      nv_merged<NKC, true>(cur, bop, strength, gin, m);
+  // rows past M read row M - 1 (valid memory) and are left out of the max
+  const NvLane<NKC> l0 = nv_lane<NKC>(a, rok0 ? r0 : a.M - 1, lane);
+  const NvLane<NKC> l1 = nv_lane<NKC>(a, rok1 ? r1 : a.M - 1, lane);
+  v4i16 bop0[NKC], bop1[NKC];
+  load_bop<NKC>(a.bp, r0, lane, bop0);  // Bp holds ceil(M/16)*16 rows
+  if (second) {
+    load_bop<NKC>(a.bp, r1, lane, bop1);
+  } else {
 #pragma unroll
-      for (int j = 0; j < 32; j += 2) mx = max3_abs(mx, m[j], m[j + 1]);
+    for (int k = 0; k < NKC; ++k) bop1[k] = (v4i16){0, 0, 0, 0};
+  }
+  float mx0 = 0.0f, mx1 = 0.0f;
+  if (t0 + wave < ntiles) {
+    NvAmaxIn<NKC> cur;
+    nv_amax_load<NKC>(l0, l1, t0 + wave, cur);
+    for (int mt = t0 + wave; mt < ntiles; mt += NV_NW) {
+      NvAmaxIn<NKC> nxt;
+      nv_amax_load<NKC>(l0, l1, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
+      float m[32];
+      nv_merged_parts<NKC, true>(cur.codes[0], cur.sc[0], cur.aop, bop0, strength, gin, m);
+#pragma unroll
+      for (int j = 0; j < 32; j += 2) mx0 = max3_abs(mx0, m[j], m[j + 1]);
+      if (second) {
+        nv_merged_parts<NKC, true>(cur.codes[1], cur.sc[1], cur.aop, bop1, strength, gin, m);
+#pragma unroll
+        for (int j = 0; j < 32; j += 2) mx1 = max3_abs(mx1, m[j], m[j + 1]);
+      }
       cur = nxt;
     }
   }
-  mx = rok ? mx : 0.0f;
+  float mx = __builtin_fmaxf(rok0 ? mx0 : 0.0f, rok1 ? mx1 : 0.0f);
   mx = wave_max(mx);
   if (lane == 0) sh[wave] = mx;
   __syncthreads();
@@ -332,11 +375,12 @@ DEV void nv_quant_body(const NvArgs& a, int64_t row0, int t0, int t1, const floa
   }
 }
 
+template <bool PAIRS = false>
 DEV int nv_find(const NvStackItem* __restrict__ items, int count, int64_t t) {
   int lo = 0, hi = count - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (items[mid].tile_begin <= t) lo = mid;
+    if ((PAIRS ? items[mid].pair_begin : items[mid].tile_begin) <= t) lo = mid;
     else hi = mid - 1;
   }
   return lo;
@@ -345,6 +389,8 @@ DEV int nv_find(const NvStackItem* __restrict__ items, int count, int64_t t) {
 // ---- kernels: single tensor (args by value) and grouped (descriptor table) ---
 // One workgroup per 16 rows (tile_begin counts 16-row groups).
 static inline int64_t nv_units(int64_t M, int64_t /*N*/) { return (M + 15) / 16; }
+// the amax pass: one workgroup per 32 rows
+static inline int64_t nv_pairs(int64_t M) { return (M + 31) / 32; }
 
 // Single tensors: blocks are independent once the global scale is known, so a
 // workgroup owns 16 rows x NV_CHUNK macro tiles (blockIdx.y picks the chunk);
@@ -356,7 +402,7 @@ DEV int nv_chunk_end(const NvArgs& a) {
 }
 template <int NKC>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_amax(NvArgs a) {
-  nv_amax_body<NKC>(a, (int64_t)blockIdx.x * 16, (int)blockIdx.y * NV_CHUNK, nv_chunk_end(a));
+  nv_amax_body<NKC>(a, (int64_t)blockIdx.x * 32, (int)blockIdx.y * NV_CHUNK, nv_chunk_end(a));
 }
 template <int NKC, bool SR, bool TWO>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant(NvArgs a) {
@@ -367,10 +413,10 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant(NvArgs a) {
 }
 template <int NKC>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_amax_stack(const NvStackItem* __restrict__ items, int count) {
-  const int i = nv_find(items, count, blockIdx.x);
+  const int i = nv_find<true>(items, count, blockIdx.x);
   const NvArgs a = items[i].a;
   if (a.gin == nullptr) return;  // single-level item: no global scale to find
-  nv_amax_body<NKC>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16, 0, (int)(a.N >> 7));
+  nv_amax_body<NKC>(a, ((int64_t)blockIdx.x - items[i].pair_begin) * 32, 0, (int)(a.N >> 7));
 }
 // TWO: every item of the launch is two-level (the host splits a mixed stack)
 template <int NKC, bool SR, bool TWO>
@@ -401,7 +447,8 @@ static int nv_fast_run(const NvArgs& a, int nkc, bool sr, hipStream_t st) {
   const dim3 grid((unsigned)nv_units(a.M, a.N), (unsigned)(((a.N >> 7) + NV_CHUNK - 1) / NV_CHUNK)), block(NV_NW * 64);
   if (a.gin) {
     TimedLaunch timed("nvfp4", st);
-    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_amax<NKC_>), grid, block, 0, st, a));
+    const dim3 agrid((unsigned)nv_pairs(a.M), grid.y);
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_amax<NKC_>), agrid, block, 0, st, a));
     LAUNCH_CHECK();
   }
   {

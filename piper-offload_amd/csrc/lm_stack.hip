@@ -178,6 +178,7 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
   int n_two = 0;
   for (int i = 0; i < count; ++i) n_two += items[i].aux != nullptr ? 1 : 0;
   int64_t tiles[2] = {0, 0};
+  int64_t pairs = 0;  // 32-row units of the two-level items (amax launch)
   int slot[2] = {0, n_two};
   int rc = LM_OK;
   for (int i = 0; i < count && rc == LM_OK; ++i) {
@@ -203,6 +204,8 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
     a.seed = s.seed;
     it.tile_begin = tiles[grp];
     tiles[grp] += nv_units(s.M, s.N);
+    it.pair_begin = pairs;
+    if (grp == 0) pairs += nv_pairs(s.M);
     if (rc == LM_OK && swizzled) rc = zero_swizzle_pad((uint8_t*)s.scale_out, s.M, s.N / 16, st);
   }
   if (rc == LM_OK) rc = lm_stage_h2d(dev_items, h, sizeof(NvStackItem) * count, st);
@@ -211,7 +214,7 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
   const NvStackItem* d = (const NvStackItem*)dev_items;
   if (rc == LM_OK && tiles[0] > 0) {
     TimedLaunch timed("nvfp4", st);
-    const dim3 grid((unsigned)tiles[0]);
+    const dim3 grid((unsigned)pairs);
     NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_amax_stack<NKC_>), grid, block, 0, st, d, n_two));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 amax launch: %s", hipGetErrorString(e));
