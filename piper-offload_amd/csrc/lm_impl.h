@@ -681,9 +681,13 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, const FastLan
 template <int NKC, bool SR>
 constexpr int fast_prefetch() { return NKC == 1 ? 4 : 2; }
 
-template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>()>
+// LCACHE: merged tiles per wave kept in LDS after the register cache (2 KiB
+// each: [half][lane][4 words], so the two 16-byte writes of a lane are
+// consecutive across lanes); tiles beyond CACHE + LCACHE are merged twice.
+template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0>
 __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   __shared__ float sh_mx[16][NW];
+  __shared__ lm_u32x4 lcache[LCACHE > 0 ? LCACHE : 1][NW][2][64];
   constexpr int PF = PF_ < CACHE ? PF_ : CACHE;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int64_t row = row0 + rl;
@@ -724,16 +728,22 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
       }
     }
   }
-  // tiles beyond the cache: one tile of loads ahead (the last prefetch
-  // re-reads the final tile instead of branching)
+  // tiles beyond the register cache: one tile of loads ahead (the last
+  // prefetch re-reads the final tile instead of branching); the first LCACHE
+  // of them are kept in LDS
   if (wave + CACHE * NW < ntiles) {
     FastTileIn<NKC> cur;
     fast_load_tile<NKC>(L, wave + CACHE * NW, cur);
-    for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW) {
+    int l = 0;
+    for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW, ++l) {
       FastTileIn<NKC> nxt;
       fast_load_tile<NKC>(L, mt + NW < ntiles ? mt + NW : mt, nxt);
       uint32_t t[8];
       fast_merged_tile<KIND, NKC>(a, cur.raw, cur.aop, bop, s_in, t, amax);
+      if (LCACHE > 0 && l < LCACHE) {
+        lcache[l][wave][0][lane] = lm_u32x4{t[0], t[1], t[2], t[3]};
+        lcache[l][wave][1][lane] = lm_u32x4{t[4], t[5], t[6], t[7]};
+      }
       cur = nxt;
     }
   }
@@ -771,10 +781,19 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
     const int mt = wave + i * NW;
     if (mt < ntiles) fast_quant_store<KIND, SR>(a, L, rok, mt, qp, cache[i], wide);
   }
-  if (wave + CACHE * NW < ntiles) {
+#pragma unroll
+  for (int l = 0; l < LCACHE; ++l) {
+    const int mt = wave + (CACHE + l) * NW;
+    if (mt < ntiles) {
+      const lm_u32x4 lo = lcache[l][wave][0][lane], hi = lcache[l][wave][1][lane];
+      const uint32_t t[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      fast_quant_store<KIND, SR>(a, L, rok, mt, qp, t, wide);
+    }
+  }
+  if (wave + (CACHE + LCACHE) * NW < ntiles) {
     FastTileIn<NKC> cur;
-    fast_load_tile<NKC>(L, wave + CACHE * NW, cur);
-    for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW) {
+    fast_load_tile<NKC>(L, wave + (CACHE + LCACHE) * NW, cur);
+    for (int mt = wave + (CACHE + LCACHE) * NW; mt < ntiles; mt += NW) {
       FastTileIn<NKC> nxt;
       fast_load_tile<NKC>(L, mt + NW < ntiles ? mt + NW : mt, nxt);
       uint32_t t[8];
@@ -791,11 +810,11 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
 template <int NKC, int CACHE>
 constexpr int fast_min_waves() { return NKC == 1 && CACHE <= 8 ? 4 : 1; }
 
-template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>()>
+template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0>
 __global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_rows_fast(RowArgs a) {
-  rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_>(a, (int64_t)blockIdx.x * 16);
+  rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_, LCACHE>(a, (int64_t)blockIdx.x * 16);
 }
-template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>()>
+template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0>
 __global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_rows_fast_stack(const RowStackItem* __restrict__ items, int count) {
   int lo = 0, hi = count - 1;
   const int64_t t = blockIdx.x;
@@ -805,7 +824,7 @@ __global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_row
     else hi = mid - 1;
   }
   const RowArgs a = items[lo].a;
-  rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_>(a, (t - items[lo].tile_begin) * 16);
+  rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_, LCACHE>(a, (t - items[lo].tile_begin) * 16);
 }
 
 // ---------------------------------------------------------------------------
@@ -1446,6 +1465,9 @@ static inline bool rows_fast_ok(int kind, int cd, int sdt, bool asym, int nkc, i
 //   costs (those rows recompute).
 static constexpr int ROW_DEEP_CACHE = 16;
 static constexpr int ROW_NW_WIDE = 16;
+// 16-wave rows keep 4 more tiles per wave in LDS (128 KiB per workgroup, one
+// workgroup per CU)
+static constexpr int ROW_WIDE_LDS = 4;
 enum RowsMode : int { ROWS_REGULAR = 0, ROWS_WIDE = 1, ROWS_DEEP = 2 };
 static inline int rows_long_mode(int nkc, bool sr, int64_t N) {
   const int64_t tpw = (N / 64 + ROW_NW - 1) / ROW_NW;
@@ -1461,7 +1483,8 @@ static int launch_rows_fast(const RowArgs& a, hipStream_t st) {
   const int mode = rows_long_mode(NKC, SR, a.N);
   if (mode == ROWS_WIDE) {
     if constexpr (NKC == 1)
-      hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW_WIDE, ROW_CACHE>), grid, dim3(ROW_NW_WIDE * 64), 0, st, a);
+      hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<NKC, SR>(), ROW_WIDE_LDS>), grid,
+                         dim3(ROW_NW_WIDE * 64), 0, st, a);
   } else if (mode == ROWS_DEEP) {
     if constexpr (NKC == 4 || !SR)
       hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_DEEP_CACHE, NKC == 4 ? 1 : 2>), grid,

@@ -137,8 +137,12 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
         const int n_deep = count - n_regular;
         if (nkc_bucket(nkc_max) == 1) {  // ROWS_WIDE: 16-wave workgroups
           const dim3 wblock(ROW_NW_WIDE * 64);
-          if (sr) hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, true, 1, ROW_NW_WIDE, ROW_CACHE>), grid, wblock, 0, st, d1, n_deep);
-          else hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, false, 1, ROW_NW_WIDE, ROW_CACHE>), grid, wblock, 0, st, d1, n_deep);
+          if (sr)
+            hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, true, 1, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<1, true>(), ROW_WIDE_LDS>),
+                               grid, wblock, 0, st, d1, n_deep);
+          else
+            hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, false, 1, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<1, false>(), ROW_WIDE_LDS>),
+                               grid, wblock, 0, st, d1, n_deep);
         } else {  // ROWS_DEEP
 #define RD(SR_, PF_) NKC_SWITCH(nkc_bucket(nkc_max), if constexpr (NKC_ != 1 && (NKC_ == 4 || !SR_)) hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, ROW_DEEP_CACHE, PF_>), grid, block, 0, st, d1, n_deep))
           if (sr) { RD(true, 1); } else if (nkc_max == 4) { RD(false, 1); } else { RD(false, 2); }

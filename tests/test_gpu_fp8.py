@@ -37,7 +37,9 @@ def test_fp8_requant_bit_exact(shape, fp8, sr, per_tensor):
     assert np.array_equal(s.cpu().numpy().reshape(-1), os_)
 
 
-@pytest.mark.parametrize("shape,rank,strength", [((64, 8192), 64, 1.0), ((24, 69), 5, 0.75), ((32, 1024), 16, 0.5)])
+# (24, 14336) r16: 16-wave rows with tiles in registers, in LDS and merged twice
+@pytest.mark.parametrize("shape,rank,strength", [((64, 8192), 64, 1.0), ((24, 69), 5, 0.75), ((32, 1024), 16, 0.5),
+                                                 ((24, 14336), 16, 1.0)])
 @pytest.mark.parametrize("sr", [False, True])
 def test_fp8_fused_equals_requant_of_gpu_dense(shape, rank, strength, sr):
     rows, cols = shape

@@ -95,8 +95,10 @@ def test_int8_dequant_and_dense_merge(shape, rank):
 
 
 # long rows (more 64-column tiles per wave than the 8-tile register cache):
-# rank 16 takes 16-wave workgroups, rank 32 RTN and rank 64 the 16-tile cache,
-# rank 32 SR recomputes the surplus tiles
+# rank 16 takes 16-wave workgroups with 4 more tiles per wave in LDS (40 x 14336
+# also merges its last tiles twice, 17 x 12288 fills registers and LDS
+# exactly), rank 32 RTN and rank 64 the 16-tile cache, rank 32 SR recomputes
+# the surplus tiles
 @pytest.mark.parametrize("shape,rank,strength", [((64, 4096), 32, 0.5), ((24, 69), 5, 0.75), ((40, 1024), 16, 1.0),
                                                  ((32, 2048), 64, 1.0), ((16, 8192), 32, 0.5),
                                                  ((40, 14336), 16, 1.0), ((17, 12288), 16, 0.5),
