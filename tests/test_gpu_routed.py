@@ -83,6 +83,7 @@ def _check(got: torch.Tensor, x, y, fs, dtype):
     (8, 1024, 2048, [64, 16], True),     # one launch (T <= 16): five rank chunks
     (3, 256, 100, [16], False),          # one launch, N not a multiple of 8
     (17, 512, 256, [16], False),         # one token past the single-launch path
+    (40, 512, 512, [8, 12], False),      # row-streaming up kernel: ranks 8 and 12, partial token tile
     (300, 2048, 14336 // 8, [16], False),
 ])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
