@@ -808,7 +808,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
 // Rank 16 with the 8-tile cache fits 128 VGPRs: two 512-thread workgroups per
 // CU (4 waves per SIMD), which the bound below holds the compiler to.
 template <int NKC, int CACHE>
-constexpr int fast_min_waves() { return NKC == 1 && CACHE <= 8 ? 4 : 1; }
+constexpr int fast_min_waves() { return (NKC == 1 && CACHE <= 8) || (NKC == 2 && CACHE <= 4) ? 4 : 1; }
 
 template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0>
 __global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_rows_fast(RowArgs a) {
@@ -1463,6 +1463,13 @@ static inline bool rows_fast_ok(int kind, int cd, int sdt, bool asym, int nkc, i
 //   0.083 ms, SR 0.137 -> 0.115 ms) and for round-to-nearest at rank 32, while
 //   stochastic rounding at rank 32 is VALU-bound and loses the occupancy it
 //   costs (those rows recompute).
+// Rows of up to 8 tiles per wave: rank 16 caches them all in registers; rank
+// 32 keeps 4 in registers and 4 in LDS (64 KiB per workgroup), which brings
+// it to 106 VGPRs and two workgroups per CU instead of one.
+template <int NKC>
+constexpr int row_reg_cache() { return NKC == 2 ? 4 : 8; }
+template <int NKC>
+constexpr int row_lds_cache() { return NKC == 2 ? 4 : 0; }
 static constexpr int ROW_DEEP_CACHE = 16;
 static constexpr int ROW_NW_WIDE = 16;
 // 16-wave rows keep 4 more tiles per wave in LDS (128 KiB per workgroup, one
@@ -1490,7 +1497,9 @@ static int launch_rows_fast(const RowArgs& a, hipStream_t st) {
       hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_DEEP_CACHE, NKC == 4 ? 1 : 2>), grid,
                          dim3(ROW_NW * 64), 0, st, a);
   } else {
-    hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_CACHE>), grid, dim3(ROW_NW * 64), 0, st, a);
+    hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, row_reg_cache<NKC>(), fast_prefetch<NKC, SR>(),
+                                    row_lds_cache<NKC>()>),
+                       grid, dim3(ROW_NW * 64), 0, st, a);
   }
   LAUNCH_CHECK();
   return LM_OK;

@@ -127,7 +127,7 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
     if (fast) {
       if (tiles[0] > 0) {
         const dim3 grid((unsigned)tiles[0]);
-#define RF(SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, ROW_CACHE>), grid, block, 0, st, d0, n_regular))
+#define RF(SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, row_reg_cache<NKC_>(), fast_prefetch<NKC_, SR_>(), row_lds_cache<NKC_>()>), grid, block, 0, st, d0, n_regular))
         if (sr) { RF(true); } else { RF(false); }
 #undef RF
       }
