@@ -20,6 +20,8 @@
 //   requant (ggml quantize_row_q8_0_ref): d' = amax / 127, id = d' ? 1/d' : 0,
 //   q' = round-half-away(merged * id) or the stochastic choice, store fp16(d').
 #pragma once
+#include <atomic>
+
 #include "lm_impl.h"
 
 struct Q8Args {
@@ -285,21 +287,25 @@ __global__ __launch_bounds__(Q8_NW * 64, (q8_min_waves<NKC, SR>())) void k_q8_fa
 #undef Q8_STEP
 }
 
-// workgroups resident at once on the current device for a kernel (cached per device)
+// workgroups resident at once on the current device for a kernel (cached per
+// device; callers on several host threads may race to fill an entry, which
+// the atomic makes benign: they store the same value)
 template <int NKC, bool SR>
 static unsigned q8_resident_grid() {
-  static unsigned cached[64] = {0};
+  static std::atomic<unsigned> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1024;
-  if (cached[dev] == 0) {
+  unsigned v = cached[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
     int per_cu = 0, cus = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_q8_fast<NKC, SR>, Q8_NW * 64, 0) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 ||
         cus <= 0)
       return 1024;
-    cached[dev] = (unsigned)(per_cu * cus);
+    v = (unsigned)(per_cu * cus);
+    cached[dev].store(v, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return v;
 }
 
 static inline bool q8_fast_ok(int cd, int nkc, int64_t N) { return cd == LM_BF16 && nkc > 0 && (N % 128) == 0; }
