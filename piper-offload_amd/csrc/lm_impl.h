@@ -81,23 +81,28 @@ struct PrepItem {
   uint16_t* at;
   uint16_t* bp;
   uint32_t* red;
-  int64_t work_begin;  // prefix of per-item work units
+  int64_t work_begin;  // prefix of per-item work units (k_prep1: 0)
+  int64_t block_begin; // prefix of per-item k_prep_many workgroups
+  int vec_b;           // B rows load 4 ranks at once (ldb, rank % 4 == 0, 8-byte aligned)
 };
 
 __device__ __forceinline__ void prep_unit(const PrepItem& it, int64_t u) {
-  // units: [0, Npad*rpad/4) for At, then [.., + Mpad*rpad/4) for Bp, then 1 for red
+  // units: [0, Npad*rpad/4) for At, then [.., + Mpad*rpad/4) for Bp, then 1
+  // for red.  rpad is 16, 32 or 64: a unit is (column or row, g, kc) with
+  // rpad/4 units per column or row and rpad/16 chunks kc.
   const int64_t npad = (it.N + 127) / 128 * 128, mpad = (it.M + 15) / 16 * 16;
-  const int64_t n_at = npad * it.rpad / 4, n_bp = mpad * it.rpad / 4;
-  const int nkc = it.rpad / 16;
+  const int lq = it.rpad == 16 ? 2 : (it.rpad == 32 ? 3 : 4), lk = lq - 2;  // log2(rpad/4), log2(nkc)
+  const int64_t n_at = npad * it.rpad / 4, n_bp = mpad * it.rpad / 4;          // 0 without factors
+  const int nkc = it.rpad >> 4;
   if (u < n_at) {
-    // At[col][g][kc][i]: unit = (col, g, kc)
-    int64_t col = u / (it.rpad / 4);
-    int rem = (int)(u % (it.rpad / 4));
-    int g = rem / nkc, kc = rem % nkc;
+    // At[col][g][kc][i]
+    const int64_t col = u >> lq;
+    const int rem = (int)(u & ((1 << lq) - 1));
+    const int g = rem >> lk, kc = rem & (nkc - 1);
     uint16_t v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      int k = kc * 16 + 4 * g + i;
+      const int k = kc * 16 + 4 * g + i;
       v[i] = (k < it.rank && col < it.N) ? it.a[(int64_t)k * it.lda + col] : (uint16_t)0;
     }
     uint2 w = make_uint2((uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16));
@@ -106,16 +111,22 @@ __device__ __forceinline__ void prep_unit(const PrepItem& it, int64_t u) {
   }
   u -= n_at;
   if (u < n_bp) {
-    int64_t row = u / (it.rpad / 4);
-    int rem = (int)(u % (it.rpad / 4));
-    int g = rem / nkc, kc = rem % nkc;
-    uint16_t v[4];
+    const int64_t row = u >> lq;
+    const int rem = (int)(u & ((1 << lq) - 1));
+    const int g = rem >> lk, kc = rem & (nkc - 1);
+    const int k0 = kc * 16 + 4 * g;
+    uint2 w = make_uint2(0u, 0u);
+    if (it.vec_b) {
+      if (row < it.M && k0 < it.rank) w = *(const uint2*)(it.b + row * it.ldb + k0);
+    } else {
+      uint16_t v[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int k = kc * 16 + 4 * g + i;
-      v[i] = (k < it.rank && row < it.M) ? it.b[row * it.ldb + k] : (uint16_t)0;
+      for (int i = 0; i < 4; ++i) {
+        const int k = k0 + i;
+        v[i] = (k < it.rank && row < it.M) ? it.b[row * it.ldb + k] : (uint16_t)0;
+      }
+      w = make_uint2((uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16));
     }
-    uint2 w = make_uint2((uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16));
     *(uint2*)(it.bp + row * it.rpad + (g * nkc + kc) * 4) = w;
     return;
   }
@@ -125,7 +136,11 @@ __device__ __forceinline__ void prep_unit(const PrepItem& it, int64_t u) {
   }
 }
 
-static inline int64_t prep_units(const PrepItem& it) {
+// B rows can be read 4 ranks (8 bytes) at a time
+static inline int prep_vec_b(const PrepItem& it) {
+  return it.b && (it.ldb % 4) == 0 && (it.rank % 4) == 0 && ((uintptr_t)it.b & 7) == 0 ? 1 : 0;
+}
+__host__ __device__ static inline int64_t prep_units(const PrepItem& it) {
   const int64_t npad = (it.N + 127) / 128 * 128, mpad = (it.M + 15) / 16 * 16;
   return npad * it.rpad / 4 + mpad * it.rpad / 4 + 1;
 }
@@ -133,15 +148,24 @@ static inline int64_t prep_units(const PrepItem& it) {
 static __global__ __launch_bounds__(256) void k_prep1(PrepItem it, int64_t total) {
   for (int64_t u = blockIdx.x * 256ll + threadIdx.x; u < total; u += (int64_t)gridDim.x * 256) prep_unit(it, u);
 }
-static __global__ __launch_bounds__(256) void k_prep_many(const PrepItem* __restrict__ items, int count, int64_t total) {
-  for (int64_t u = blockIdx.x * 256ll + threadIdx.x; u < total; u += (int64_t)gridDim.x * 256) {
-    int lo = 0, hi = count - 1;
-    while (lo < hi) {
-      int mid = (lo + hi + 1) >> 1;
-      if (items[mid].work_begin <= u) lo = mid;
-      else hi = mid - 1;
-    }
-    prep_unit(items[lo], u - items[lo].work_begin);
+// One workgroup per PREP_PER_BLOCK units of one item: the item is found once
+// per workgroup (block_begin), not per unit.
+static constexpr int PREP_PER_BLOCK = 1024;
+static __global__ __launch_bounds__(256) void k_prep_many(const PrepItem* __restrict__ items, int count) {
+  int lo = 0, hi = count - 1;
+  const int64_t b = blockIdx.x;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (items[mid].block_begin <= b) lo = mid;
+    else hi = mid - 1;
+  }
+  const PrepItem& it = items[lo];
+  const int64_t units = prep_units(it);
+  const int64_t u0 = (b - it.block_begin) * PREP_PER_BLOCK;
+#pragma unroll
+  for (int j = 0; j < PREP_PER_BLOCK / 256; ++j) {
+    const int64_t u = u0 + j * 256 + threadIdx.x;
+    if (u < units) prep_unit(it, u);
   }
 }
 
@@ -1341,6 +1365,8 @@ static inline int setup(Ctx& c, int64_t M, int64_t N, const lm_lora* l, void* ws
   it.bp = c.bp;
   it.red = c.red;
   it.work_begin = 0;
+  it.block_begin = 0;
+  it.vec_b = prep_vec_b(it);
   return launch_prep(it, c.st);
 }
 

@@ -30,23 +30,24 @@ static int stack_layout(const lm_stack_item* items, int32_t count, void* ws, siz
     p.at = (uint16_t*)(base + cursor + w.at_off);
     p.bp = (uint16_t*)(base + cursor + w.bp_off);
     p.red = (uint32_t*)(base + cursor + w.red_off);
+    p.vec_b = prep_vec_b(p);
     cursor += w.total;
   }
   return LM_OK;
 }
 
 static int stack_prep(PrepItem* preps, int32_t count, uint8_t* dev_items, hipStream_t st) {
-  int64_t total = 0;
+  int64_t blocks = 0;
   for (int i = 0; i < count; ++i) {
-    preps[i].work_begin = total;
-    total += prep_units(preps[i]);
+    preps[i].work_begin = 0;
+    preps[i].block_begin = blocks;
+    blocks += (prep_units(preps[i]) + PREP_PER_BLOCK - 1) / PREP_PER_BLOCK;
   }
+  if (blocks > 0x7fffffff) return fail(LM_EUNSUPPORTED, "stack factors too large for one prep launch");
   int rc = lm_stage_h2d(dev_items, preps, sizeof(PrepItem) * count, st);
   if (rc != LM_OK) return rc;
-  int64_t nb = (total + 255) / 256;
-  if (nb > 8192) nb = 8192;
   TimedLaunch timed("prep", st);
-  hipLaunchKernelGGL(k_prep_many, dim3((unsigned)nb), dim3(256), 0, st, (const PrepItem*)dev_items, count, total);
+  hipLaunchKernelGGL(k_prep_many, dim3((unsigned)blocks), dim3(256), 0, st, (const PrepItem*)dev_items, count);
   LAUNCH_CHECK();
   return LM_OK;
 }
