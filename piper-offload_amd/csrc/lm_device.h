@@ -623,5 +623,12 @@ template <int NKC>
 DEV void load_bop(const uint16_t* __restrict__ bp, int64_t row, int lane, v4i16 (&bop)[NKC]) {
   load_kchunks<NKC>(bp + row * (NKC * 16) + (lane >> 4) * (NKC * 4), bop);
 }
+// the same through a global-address-space pointer: kernels whose pointers
+// come from a descriptor table in memory would otherwise use flat accesses,
+// for which the compiler waits for every outstanding load
+template <int NKC>
+DEV void load_bop_g(const uint16_t* bp, int64_t row, int lane, v4i16 (&bop)[NKC]) {
+  load_kchunks_g<NKC>((const LM_GLOBAL uint16_t*)bp + row * (NKC * 16) + (lane >> 4) * (NKC * 4), bop);
+}
 
 }  // namespace lm

@@ -103,10 +103,10 @@ __device__ __forceinline__ void prep_unit(const PrepItem& it, int64_t u) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int k = kc * 16 + 4 * g + i;
-      v[i] = (k < it.rank && col < it.N) ? it.a[(int64_t)k * it.lda + col] : (uint16_t)0;
+      v[i] = (k < it.rank && col < it.N) ? ((const LM_GLOBAL uint16_t*)it.a)[(int64_t)k * it.lda + col] : (uint16_t)0;
     }
-    uint2 w = make_uint2((uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16));
-    *(uint2*)(it.at + col * it.rpad + (g * nkc + kc) * 4) = w;
+    const lm_u32x2 w = {(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16)};
+    *(LM_GLOBAL lm_u32x2*)((LM_GLOBAL uint16_t*)it.at + col * it.rpad + (g * nkc + kc) * 4) = w;
     return;
   }
   u -= n_at;
@@ -115,24 +115,25 @@ __device__ __forceinline__ void prep_unit(const PrepItem& it, int64_t u) {
     const int rem = (int)(u & ((1 << lq) - 1));
     const int g = rem >> lk, kc = rem & (nkc - 1);
     const int k0 = kc * 16 + 4 * g;
-    uint2 w = make_uint2(0u, 0u);
+    const LM_GLOBAL uint16_t* b = (const LM_GLOBAL uint16_t*)it.b;
+    lm_u32x2 w = {0u, 0u};
     if (it.vec_b) {
-      if (row < it.M && k0 < it.rank) w = *(const uint2*)(it.b + row * it.ldb + k0);
+      if (row < it.M && k0 < it.rank) w = *(const LM_GLOBAL lm_u32x2*)(b + row * it.ldb + k0);
     } else {
       uint16_t v[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int k = k0 + i;
-        v[i] = (k < it.rank && row < it.M) ? it.b[row * it.ldb + k] : (uint16_t)0;
+        v[i] = (k < it.rank && row < it.M) ? b[row * it.ldb + k] : (uint16_t)0;
       }
-      w = make_uint2((uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16));
+      w = lm_u32x2{(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16)};
     }
-    *(uint2*)(it.bp + row * it.rpad + (g * nkc + kc) * 4) = w;
+    *(LM_GLOBAL lm_u32x2*)((LM_GLOBAL uint16_t*)it.bp + row * it.rpad + (g * nkc + kc) * 4) = w;
     return;
   }
   u -= n_bp;
   if (u == 0 && it.red) {
-    for (int i = 0; i < 64; ++i) it.red[i] = 0u;
+    for (int i = 0; i < 64; ++i) ((LM_GLOBAL uint32_t*)it.red)[i] = 0u;
   }
 }
 

@@ -76,10 +76,12 @@ struct NvTileIn {
 // scale column by 8, which is 8 bytes in the plain layout and 2 col-blocks =
 // 1024 bytes in the 128x4 swizzle (P/_triton_nvfp4_lora.py:88-104).
 template <int NKC>
+// (global-address-space pointers: the stack kernels read them from a
+// descriptor table, and flat accesses would make every wait a full one)
 struct NvLane {
-  const uint8_t* q;
-  const uint8_t* sc;
-  const uint16_t* at;
+  const LM_GLOBAL uint8_t* q;
+  const LM_GLOBAL uint8_t* sc;
+  const LM_GLOBAL uint16_t* at;
   int64_t sc_stride;
 };
 
@@ -88,22 +90,23 @@ DEV NvLane<NKC> nv_lane(const NvArgs& a, int64_t rowc, int lane) {
   constexpr int RPAD = NKC * 16;
   const int p = lane & 15, g = lane >> 4;
   NvLane<NKC> l;
-  l.q = a.q + rowc * (a.N >> 1) + 16 * g;
-  l.sc = a.scale + blocked_offset(rowc, 2 * g, a.N >> 4, a.swizzled);
+  l.q = (const LM_GLOBAL uint8_t*)a.q + rowc * (a.N >> 1) + 16 * g;
+  l.sc = (const LM_GLOBAL uint8_t*)a.scale + blocked_offset(rowc, 2 * g, a.N >> 4, a.swizzled);
   l.sc_stride = a.swizzled ? 1024 : 8;
-  l.at = a.at + (int64_t)(32 * (p >> 2) + (p & 3)) * RPAD + g * (NKC * 4);
+  l.at = (const LM_GLOBAL uint16_t*)a.at + (int64_t)(32 * (p >> 2) + (p & 3)) * RPAD + g * (NKC * 4);
   return l;
 }
 
 template <int NKC>
 DEV void nv_load_tile(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
   constexpr int RPAD = NKC * 16;
-  t.codes = *(const uint4*)(l.q + (int64_t)mt * 64);
+  const lm_u32x4 c = *(const LM_GLOBAL lm_u32x4*)(l.q + (int64_t)mt * 64);
+  t.codes = make_uint4(c.x, c.y, c.z, c.w);
   // the lane's scale column is even: both blocks' scales are adjacent bytes
-  t.sc = *(const uint16_t*)(l.sc + (int64_t)mt * l.sc_stride);
-  const uint16_t* at = l.at + (int64_t)mt * (128 * RPAD);
+  t.sc = *(const LM_GLOBAL uint16_t*)(l.sc + (int64_t)mt * l.sc_stride);
+  const LM_GLOBAL uint16_t* at = l.at + (int64_t)mt * (128 * RPAD);
 #pragma unroll
-  for (int k = 0; k < 8; ++k) load_kchunks<NKC>(at + 4 * k * RPAD, t.aop[k]);
+  for (int k = 0; k < 8; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, t.aop[k]);
 }
 
 // merged values of the lane's 32 columns, for max |merged| (the reference's
@@ -252,7 +255,8 @@ DEV void nv_quant_block(const NvArgs& a, int64_t row, int mt, int lane, float gq
 // one 2-byte scale store
 template <int NKC, bool TWO, bool SR>
 DEV void nv_quant_tile(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float gin, int64_t row,
-                       int mt, int lane, float gq, float inv_g, const float* rtab, uint8_t* qo, uint8_t* so,
+                       int mt, int lane, float gq, float inv_g, const float* rtab, LM_GLOBAL uint8_t* qo,
+                       LM_GLOBAL uint8_t* so,
                        int64_t so_stride) {
   uint32_t words[4];
   uint32_t scb = 0;
@@ -266,8 +270,8 @@ DEV void nv_quant_tile(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&b
     nv_merged_block<NKC, TWO, 1>(in, bop, a.strength, gin, m);
     nv_quant_block<TWO, SR, 1>(a, row, mt, lane, gq, inv_g, rtab, m, words, scb);
   }
-  *(uint4*)(qo + (int64_t)mt * 64) = make_uint4(words[0], words[1], words[2], words[3]);
-  *(uint16_t*)(so + (int64_t)mt * so_stride) = (uint16_t)scb;
+  *(LM_GLOBAL lm_u32x4*)(qo + (int64_t)mt * 64) = lm_u32x4{words[0], words[1], words[2], words[3]};
+  *(LM_GLOBAL uint16_t*)(so + (int64_t)mt * so_stride) = (uint16_t)scb;
 }
 
 // ---- pass bodies -------------------------------------------------------------
@@ -286,13 +290,15 @@ struct NvAmaxIn {
 template <int NKC>
 DEV void nv_amax_load(const NvLane<NKC>& l0, const NvLane<NKC>& l1, int mt, NvAmaxIn<NKC>& t) {
   constexpr int RPAD = NKC * 16;
-  t.codes[0] = *(const uint4*)(l0.q + (int64_t)mt * 64);
-  t.codes[1] = *(const uint4*)(l1.q + (int64_t)mt * 64);
-  t.sc[0] = *(const uint16_t*)(l0.sc + (int64_t)mt * l0.sc_stride);
-  t.sc[1] = *(const uint16_t*)(l1.sc + (int64_t)mt * l1.sc_stride);
-  const uint16_t* at = l0.at + (int64_t)mt * (128 * RPAD);
+  const lm_u32x4 c0 = *(const LM_GLOBAL lm_u32x4*)(l0.q + (int64_t)mt * 64);
+  const lm_u32x4 c1 = *(const LM_GLOBAL lm_u32x4*)(l1.q + (int64_t)mt * 64);
+  t.codes[0] = make_uint4(c0.x, c0.y, c0.z, c0.w);
+  t.codes[1] = make_uint4(c1.x, c1.y, c1.z, c1.w);
+  t.sc[0] = *(const LM_GLOBAL uint16_t*)(l0.sc + (int64_t)mt * l0.sc_stride);
+  t.sc[1] = *(const LM_GLOBAL uint16_t*)(l1.sc + (int64_t)mt * l1.sc_stride);
+  const LM_GLOBAL uint16_t* at = l0.at + (int64_t)mt * (128 * RPAD);
 #pragma unroll
-  for (int k = 0; k < 8; ++k) load_kchunks<NKC>(at + 4 * k * RPAD, t.aop[k]);
+  for (int k = 0; k < 8; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, t.aop[k]);
 }
 template <int NKC>
 DEV void nv_amax_body(const NvArgs& a, int64_t row0, int t0, int t1) {
@@ -302,15 +308,15 @@ DEV void nv_amax_body(const NvArgs& a, int64_t row0, int t0, int t1) {
   const bool rok0 = r0 < a.M, rok1 = r1 < a.M;
   const bool second = row0 + 16 < a.M;  // wave-uniform
   const int ntiles = t1;
-  const float gin = *a.gin;
+  const float gin = *(const LM_GLOBAL float*)a.gin;
   const float strength = a.strength;
   // rows past M read row M - 1 (valid memory) and are left out of the max
   const NvLane<NKC> l0 = nv_lane<NKC>(a, rok0 ? r0 : a.M - 1, lane);
   const NvLane<NKC> l1 = nv_lane<NKC>(a, rok1 ? r1 : a.M - 1, lane);
   v4i16 bop0[NKC], bop1[NKC];
-  load_bop<NKC>(a.bp, r0, lane, bop0);  // Bp holds ceil(M/16)*16 rows
+  load_bop_g<NKC>(a.bp, r0, lane, bop0);  // Bp holds ceil(M/16)*16 rows
   if (second) {
-    load_bop<NKC>(a.bp, r1, lane, bop1);
+    load_bop_g<NKC>(a.bp, r1, lane, bop1);
   } else {
 #pragma unroll
     for (int k = 0; k < NKC; ++k) bop1[k] = (v4i16){0, 0, 0, 0};
@@ -353,17 +359,17 @@ DEV void nv_quant_body(const NvArgs& a, int64_t row0, int t0, int t1, const floa
   const bool rok = row < a.M;
   const int64_t rowc = rok ? row : a.M - 1;
   const int ntiles = t1;
-  const float gin = TWO ? *a.gin : 1.0f;
+  const float gin = TWO ? *(const LM_GLOBAL float*)a.gin : 1.0f;
   float gq = 1.0f, inv_g = 1.0f;
   if constexpr (TWO) {
-    gq = __builtin_fmaxf(u2f(*a.red) / 2688.0f, kEps);
+    gq = __builtin_fmaxf(u2f(*(const LM_GLOBAL uint32_t*)a.red) / 2688.0f, kEps);
     inv_g = 1.0f / gq;
   }
   const NvLane<NKC> l = nv_lane<NKC>(a, rowc, lane);
-  uint8_t* qo = a.q_out + rowc * (a.N >> 1) + 16 * (lane >> 4);
-  uint8_t* so = a.scale_out + blocked_offset(rowc, 2 * (lane >> 4), a.N >> 4, a.swizzled);
+  LM_GLOBAL uint8_t* qo = (LM_GLOBAL uint8_t*)a.q_out + rowc * (a.N >> 1) + 16 * (lane >> 4);
+  LM_GLOBAL uint8_t* so = (LM_GLOBAL uint8_t*)a.scale_out + blocked_offset(rowc, 2 * (lane >> 4), a.N >> 4, a.swizzled);
   v4i16 bop[NKC];
-  load_bop<NKC>(a.bp, row, lane, bop);
+  load_bop_g<NKC>(a.bp, row, lane, bop);
   if (t0 + wave >= ntiles) return;
   NvTileIn<NKC> cur;
   nv_load_tile<NKC>(l, t0 + wave, cur);
