@@ -279,7 +279,10 @@ DEV void nv_quant_tile(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&b
 // Tiles [t0, t1) of rows row0 .. row0+15 (the stack passes whole rows).
 // The amax pass keeps no register cache, so a wave merges 32 rows (two
 // 16-row groups) per macro tile: both groups' MFMAs share the tile's A^T
-// fragments, which halves the operand loads (L2) per element.  Rows
+// fragments, which halves the operand loads (L2) per element.  The pass is
+// bound by the texture-address unit (TA_BUSY ~85%, VALU ~63%) through its
+// code and scale loads, whose every instruction touches 16 rows: four
+// groups per wave, sharing the A^T loads further, measured the same.  Rows
 // row0 .. row0 + 31; the second group exists when row0 + 16 < M.
 template <int NKC>
 struct NvAmaxIn {
