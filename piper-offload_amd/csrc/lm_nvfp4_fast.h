@@ -304,7 +304,7 @@ DEV void nv_amax_load(const NvLane<NKC>& l0, const NvLane<NKC>& l1, int mt, NvAm
   for (int k = 0; k < 8; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, t.aop[k]);
 }
 template <int NKC>
-DEV void nv_amax_body(const NvArgs& a, int64_t row0, int t0, int t1) {
+DEV void nv_amax_body_direct(const NvArgs& a, int64_t row0, int t0, int t1) {
   __shared__ float sh[NV_NW];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int64_t r0 = row0 + rl, r1 = row0 + 16 + rl;
@@ -353,6 +353,133 @@ DEV void nv_amax_body(const NvArgs& a, int64_t row0, int t0, int t1) {
     for (int w = 1; w < NV_NW; ++w) r = __builtin_fmaxf(r, sh[w]);
     atomicMax(a.red, f2u(bf16r(r)));
   }
+}
+
+// Plain (unswizzled) scales: the workgroup stages each step's codes and
+// scales through LDS.  A step is the 8 consecutive macro tiles its waves
+// take (wave w: tile ts + w) of the 32 rows.  The codes arrive as 512-byte
+// row segments (two rows per wave instruction) and the scales as 64-byte row
+// segments, one instruction for the whole step.  Loaded per lane, every
+// code and scale instruction touched 16 rows, which kept the
+// texture-address unit busy.  The next step's bytes are requested into
+// registers while the current one is merged.  Row pitches are padded (528
+// and 68 bytes) so that the lanes' LDS reads of one row group do not share
+// banks.
+constexpr int NV_CPITCH = 528, NV_SPITCH = 68;
+template <int NKC>
+DEV void nv_amax_body_lds(const NvArgs& a, int64_t row0, int t0, int t1) {
+  constexpr int RPAD = NKC * 16;
+  __shared__ float sh[NV_NW];
+  __shared__ __attribute__((aligned(16))) uint8_t lcodes[32 * NV_CPITCH];
+  __shared__ __attribute__((aligned(16))) uint8_t lsc[32 * NV_SPITCH];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, rl = lane & 15, g = lane >> 4;
+  const int ntiles = t1;
+  const int steps = (ntiles - t0 + NV_NW - 1) / NV_NW;  // workgroup-uniform
+  const int64_t half = a.N >> 1, scols = a.N >> 4;
+  const float gin = *(const LM_GLOBAL float*)a.gin;
+  const float strength = a.strength;
+  const bool second = row0 + 16 < a.M;  // workgroup-uniform
+  // staging: thread tid loads code chunks q = tid, tid + 512 (row q >> 5,
+  // 16-byte chunk q & 31 of the row's 512-byte step segment); threads 0..255
+  // load the scales of row tid >> 3, tile tid & 7 (8 bytes)
+  const LM_GLOBAL uint8_t* qb = (const LM_GLOBAL uint8_t*)a.q;
+  const LM_GLOBAL uint8_t* sb = (const LM_GLOBAL uint8_t*)a.scale;
+  auto rowc = [&](int r) { const int64_t row = row0 + r; return row < a.M ? row : a.M - 1; };
+  lm_u32x4 sc0, sc1;
+  lm_u32x2 ss;
+  auto stage = [&](int ts) {
+    const int qa = tid, qq = tid + 512;
+    const int ta = ts + ((qa & 31) >> 2), tq = ts + ((qq & 31) >> 2);
+    const int tca = ta < ntiles ? ta : ntiles - 1, tcq = tq < ntiles ? tq : ntiles - 1;
+    sc0 = *(const LM_GLOBAL lm_u32x4*)(qb + rowc(qa >> 5) * half + (int64_t)tca * 64 + (qa & 3) * 16);
+    sc1 = *(const LM_GLOBAL lm_u32x4*)(qb + rowc(qq >> 5) * half + (int64_t)tcq * 64 + (qq & 3) * 16);
+    if (tid < 256) {
+      const int tt = ts + (tid & 7), tc = tt < ntiles ? tt : ntiles - 1;
+      ss = *(const LM_GLOBAL lm_u32x2*)(sb + rowc(tid >> 3) * scols + (int64_t)tc * 8);
+    }
+  };
+  auto publish = [&]() {
+    *(lm_u32x4*)(lcodes + (tid >> 5) * NV_CPITCH + (tid & 31) * 16) = sc0;
+    *(lm_u32x4*)(lcodes + ((tid + 512) >> 5) * NV_CPITCH + (tid & 31) * 16) = sc1;
+    if (tid < 256) {
+      uint32_t* d = (uint32_t*)(lsc + (tid >> 3) * NV_SPITCH + (tid & 7) * 8);
+      d[0] = ss.x;
+      d[1] = ss.y;
+    }
+  };
+  // per wave: its tile's A^T fragments (from L2), one step ahead
+  const int p = lane & 15;
+  const LM_GLOBAL uint16_t* atl = (const LM_GLOBAL uint16_t*)a.at + (int64_t)(32 * (p >> 2) + (p & 3)) * RPAD + g * (NKC * 4);
+  auto load_aop = [&](int ts, v4i16 (&aop)[8][NKC]) {
+    const int mt = ts + wave, mtc = mt < ntiles ? mt : ntiles - 1;
+    const LM_GLOBAL uint16_t* at = atl + (int64_t)mtc * (128 * RPAD);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, aop[k]);
+  };
+  v4i16 bop0[NKC], bop1[NKC];
+  load_bop_g<NKC>(a.bp, row0 + rl, lane, bop0);  // Bp holds ceil(M/16)*16 rows
+  if (second) {
+    load_bop_g<NKC>(a.bp, row0 + 16 + rl, lane, bop1);
+  } else {
+#pragma unroll
+    for (int k = 0; k < NKC; ++k) bop1[k] = (v4i16){0, 0, 0, 0};
+  }
+  float mx0 = 0.0f, mx1 = 0.0f;
+  v4i16 aop[8][NKC];
+  stage(t0);
+  load_aop(t0, aop);
+  publish();
+  __syncthreads();
+  for (int s = 0; s < steps; ++s) {
+    const int ts = t0 + s * NV_NW;
+    if (s + 1 < steps) stage(ts + NV_NW);
+    v4i16 nxt[8][NKC];
+    load_aop(ts + NV_NW, nxt);
+    if (ts + wave < ntiles) {
+      const int cofs = wave * 64 + 16 * g, sofs = wave * 8 + 2 * g;
+      float m[32];
+      {
+        const lm_u32x4 c = *(const lm_u32x4*)(lcodes + rl * NV_CPITCH + cofs);
+        const uint32_t scv = *(const uint16_t*)(lsc + rl * NV_SPITCH + sofs);
+        nv_merged_parts<NKC, true>(make_uint4(c.x, c.y, c.z, c.w), scv, aop, bop0, strength, gin, m);
+#pragma unroll
+        for (int j = 0; j < 32; j += 2) mx0 = max3_abs(mx0, m[j], m[j + 1]);
+      }
+      if (second) {
+        const lm_u32x4 c = *(const lm_u32x4*)(lcodes + (16 + rl) * NV_CPITCH + cofs);
+        const uint32_t scv = *(const uint16_t*)(lsc + (16 + rl) * NV_SPITCH + sofs);
+        nv_merged_parts<NKC, true>(make_uint4(c.x, c.y, c.z, c.w), scv, aop, bop1, strength, gin, m);
+#pragma unroll
+        for (int j = 0; j < 32; j += 2) mx1 = max3_abs(mx1, m[j], m[j + 1]);
+      }
+    }
+    __syncthreads();  // every wave has read this step's LDS
+    if (s + 1 < steps) publish();
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int c = 0; c < NKC; ++c) aop[k][c] = nxt[k][c];
+  }
+  const bool rok0 = row0 + rl < a.M, rok1 = row0 + 16 + rl < a.M;
+  float mx = __builtin_fmaxf(rok0 ? mx0 : 0.0f, rok1 ? mx1 : 0.0f);
+  mx = wave_max(mx);
+  if (lane == 0) sh[wave] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float r = sh[0];
+#pragma unroll
+    for (int w = 1; w < NV_NW; ++w) r = __builtin_fmaxf(r, sh[w]);
+    atomicMax(a.red, f2u(bf16r(r)));
+  }
+}
+// (the staged loads need 16-byte aligned codes and 8-byte aligned scales)
+template <int NKC>
+DEV void nv_amax_body(const NvArgs& a, int64_t row0, int t0, int t1) {
+  if (a.swizzled || (((uintptr_t)a.q) & 15) != 0 || (((uintptr_t)a.scale) & 7) != 0)
+    nv_amax_body_direct<NKC>(a, row0, t0, t1);
+  else
+    nv_amax_body_lds<NKC>(a, row0, t0, t1);
 }
 
 template <int NKC, bool TWO, bool SR>
