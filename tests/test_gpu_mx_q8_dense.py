@@ -84,10 +84,13 @@ def test_mx_zero_update_is_identity_and_code0_subnormal():
 
 
 # N % 128 == 0 with bf16 factors takes the one-block-per-lane kernel (k_q8_fast);
-# the other shapes take the generic block kernel
+# the other shapes take the generic block kernel.  Rank <= 16 with an even
+# number of 16-row groups rounds to nearest two groups per item ((30, 256):
+# a short last group; (47, 384): three groups, one per item).
 @pytest.mark.parametrize("shape,rank,strength", [
     ((13824 // 64, 5120), 16, 1.0), ((48, 96), 5, 1.0), ((33, 64), 16, 1.0),
-    ((37, 384), 32, 0.5), ((40, 256), 64, -1.25), ((17, 128), 16, 2.0)])
+    ((37, 384), 32, 0.5), ((40, 256), 64, -1.25), ((17, 128), 16, 2.0),
+    ((30, 256), 12, 1.0), ((47, 384), 16, 0.75)])
 @pytest.mark.parametrize("sr", [False, True])
 def test_q8_0_merge(shape, rank, strength, sr):
     rows, cols = shape
