@@ -592,7 +592,8 @@ def main() -> int:
     args = _parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the merge shards by weight and by row "
-              "with no exchange except one scalar max for two-level scales -- see DESIGN.md", file=sys.stderr)
+              "with no exchange except one scalar max for two-level scales; run it on one GPU per shard",
+              file=sys.stderr)
         return 2
     import torch
 
