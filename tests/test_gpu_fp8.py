@@ -96,3 +96,26 @@ def test_fp8_negative_zero_keeps_sign_and_zero_rows_get_eps():
     q, s = K.requantize_float8(dense.to(DEV), (1, 64), rounding_seed=derive_seed("negzero", 0))
     assert u8_np(q)[0, 0] == 0x80
     assert float(s[0, 0]) == torch.finfo(torch.float32).eps
+
+
+def test_fp8_config3_full_size():
+    """Config 3: W [8192, 8192] e4m3, r=64, strength 1.0, stochastic and nearest.
+    The fused merge's codes and scales are compared with the oracle's requant of
+    the GPU dense merge; the dense merge itself with the oracle on a row sample
+    (the oracle's full GEMM is slow on the CPU)."""
+    rows, cols, rank = 8192, 8192, 64
+    w = normal_bf16((rows, cols), 0.02, 5)
+    q, s = fp8_initial(w)
+    b, a = lora_factors(rows, cols, rank, 6)
+    qd, sd, bd, ad = q.to(DEV), s.to(DEV), b.to(DEV), a.to(DEV)
+    dense = K.dequantize_float8(qd, sd, (1, cols), lora=(bd, ad, 1.0))
+    dense_np = bf16_np(dense)
+    for seed in (derive_seed("model.layers.0.self_attn.o_proj.weight", 0), None):
+        oq, os_ = K.merge_float8_lora(qd, sd, (1, cols), bd, ad, 1.0, rounding_seed=seed)
+        rq, rs = O.fp8_requant(dense_np, cols, sr_mode=O.SR_PHILOX8 if seed else O.SR_OFF, seed=seed or 0)
+        assert np.array_equal(u8_np(oq), rq)
+        assert np.array_equal(os_.cpu().numpy().reshape(-1), rs)
+    idx = np.arange(0, rows, 101)
+    obase = O.fp8_dequant(u8_np(q)[idx], s.numpy()[idx], cols)
+    omerged = O.merge_dense(obase, bf16_np(b)[idx], bf16_np(a), 1.0)
+    assert_merged_close(dense_np[idx], omerged, obase)
