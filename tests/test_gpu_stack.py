@@ -35,7 +35,10 @@ def _int8_targets(shapes, rank, seed0):  # noqa: ANN001, ANN202
 
 @pytest.mark.parametrize("shapes", [[(64, 256), (40, 512), (128, 128), (16, 64)],   # fast kernel (N % 64 == 0)
                                     [(64, 256), (40, 14336), (16, 8192), (24, 4096)],  # + long rows (second launch)
-                                    [(64, 256), (24, 96)]])                          # generic kernel
+                                    [(64, 256), (24, 96)],                           # generic kernel
+                                    # one 8B layer at full size: q, k, v, o, gate, up, down
+                                    [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096),
+                                     (14336, 4096), (4096, 14336)]])
 @pytest.mark.parametrize("sr", [False, True])
 def test_int8_stack_equals_per_target_merges(shapes, sr):
     tg = _int8_targets(shapes, 16, 10)
