@@ -66,7 +66,10 @@ def _nvfp4_weight(rows, cols, seed, two_level, swizzled):  # noqa: ANN001, ANN20
 
 
 @pytest.mark.parametrize("shapes", [[(64, 256), (40, 512), (16, 128), (128, 1024)],  # fast kernels (N % 128 == 0)
-                                    [(32, 256), (16, 96)]])                          # per-target block kernels
+                                    [(32, 256), (16, 96)],                           # per-target block kernels
+                                    # one 8B layer at full size: q, k, v, o, gate, up, down
+                                    [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096),
+                                     (14336, 4096), (4096, 14336)]])
 @pytest.mark.parametrize("swizzled", [False, True])
 @pytest.mark.parametrize("sr", [False, True])
 def test_nvfp4_stack_equals_per_target_merges(shapes, swizzled, sr):
