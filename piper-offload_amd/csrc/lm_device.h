@@ -435,18 +435,31 @@ DEV uint32_t sr_fp8(float v, uint32_t h, float /*limit*/) { return cvt_sr_fp8<FM
 
 
 // ---- packed helpers for the fast paths -----------------------------------
+// Inline asm and the MFMA wait states.  gfx950 needs software wait states
+// between an MFMA and a VALU instruction that reads or overwrites its
+// destination, or overwrites its accumulator input, while it is in flight.
+// The compiler pads only the instructions it emits itself, never inline asm.
+// So every asm helper below (a) takes no MFMA result as an input (callers pass
+// values of ordinary arithmetic) and (b) writes only a register tied to one
+// of its inputs ("+v"): that register holds a live value the compiler itself
+// produced, so it is never the destination or accumulator input of an MFMA
+// in flight.  An untied output may be allocated over the accumulator input
+// of an MFMA just issued, and an asm v_min3_f32 that read MFMA results saw
+// stale registers depending on timing.  The compiled kernels are checked for
+// both by csrc/check_asm_hazards.py (make check-asm).
+//
 // max(acc, |a|, |b|) in one v_max3_f32 (IEEE maxNum: a NaN operand is
-// ignored, as fmaxf does)
+// ignored, as fmaxf does).  Written as asm because the builtin form makes the
+// compiler add canonicalizing maxima of loop-carried values (+2-4% VALU
+// instructions in the per-row kernels).
 DEV float max3_abs(float acc, float a, float b) {
-  float r;
-  asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(acc), "v"(a), "v"(b));
-  return r;
+  asm("v_max3_f32 %0, %0, |%1|, |%2|" : "+v"(acc) : "v"(a), "v"(b));
+  return acc;
 }
 // min(acc, |a|, |b|) in one v_min3_f32
 DEV float min3_abs(float acc, float a, float b) {
-  float r;
-  asm("v_min3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(acc), "v"(a), "v"(b));
-  return r;
+  asm("v_min3_f32 %0, %0, |%1|, |%2|" : "+v"(acc) : "v"(a), "v"(b));
+  return acc;
 }
 // two fp32 -> packed bf16 pair (RNE, v_cvt_pk_bf16_f32); low half = a
 DEV float bf16_lo(uint32_t w) { return u2f(w << 16); }
@@ -479,16 +492,14 @@ DEV uint32_t pack_byte2s(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
 // lower + (u < frac) for all finite y; an integer y stays y.
 // floor(-x) as int32 in one v_cvt_flr_i32_f32 (= -ceil(x)); |x| < 2^31
 DEV int cvt_flr_neg(float x) {
-  int r;
-  asm("v_cvt_flr_i32_f32_e64 %0, -%1" : "=v"(r) : "v"(x));
-  return r;
+  asm("v_cvt_flr_i32_f32_e64 %0, -%0" : "+v"(x));  // output tied to the input
+  return (int)f2u(x);
 }
 // (w & 0xffff) - t in one SDWA subtract (word 0 of w)
 DEV uint32_t sub_lo16(uint32_t w, uint32_t t) {
-  uint32_t r;
-  asm("v_sub_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD"
-      : "=v"(r) : "v"(w), "v"(t));
-  return r;
+  asm("v_sub_u32_sdwa %0, %1, %0 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD"
+      : "+v"(t) : "v"(w));  // output tied to t
+  return t;
 }
 DEV int sr_grid(float y16, uint32_t h) {
   int fneg = (int)__builtin_floorf(-y16);  // floor(-y16) = -ceil(y16)

@@ -52,8 +52,8 @@ __constant__ int8_t kIq4Values[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 
 // left to the optimizer, fp16(d * q) becomes v_fma_mixlo_f16(d, q, +0), and
 // the +0 addend turns a -0 product into +0 where torch's fp16 multiply keeps -0.
 DEV float f16r(float x) {
-  uint32_t h;
-  asm("v_cvt_f16_f32 %0, %1" : "=v"(h) : "v"(x));
+  uint32_t h = __builtin_bit_cast(uint32_t, x);
+  asm("v_cvt_f16_f32 %0, %0" : "+v"(h));  // output tied to the input
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 

@@ -161,32 +161,28 @@ DEV void nv_merged_block(const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float
   const float v = fp8_decode<E4M3>(in.sc, B);  // e4m3 is exact in bf16
   const float bs = TWO ? bf16r(v * gin) : v;
   const uint32_t w[2] = {B == 0 ? in.codes.x : in.codes.z, B == 0 ? in.codes.y : in.codes.w};
-  // "update == 0 keeps the base" (P/_triton_nvfp4_lora.py:183-186) can only
-  // matter where d * strength == 0; every such product is bounded below by
-  // min|d| * |strength|, so a block with a non-zero bound skips it (a zero
-  // LoRA row, an exact cancellation or an underflow takes the exact path).
-  float dmin = __builtin_fabsf(d[0]);
+  float base[16];
 #pragma unroll
-  for (int j = 1; j < 15; j += 2) dmin = min3_abs(dmin, d[j], d[j + 1]);
-  dmin = __builtin_fminf(dmin, __builtin_fabsf(d[15]));
-  if (dmin * __builtin_fabsf(strength) == 0.0f) {
+  for (int q = 0; q < 8; ++q) {
+    const v2f32 pr = e2m1_pair(w[q >> 2], q & 3);
+    base[2 * q] = bf16r(pr[0] * bs);
+    base[2 * q + 1] = bf16r(pr[1] * bs);
+  }
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const v2f32 pr = e2m1_pair(w[q >> 2], q & 3);
+  for (int j = 0; j < 16; ++j) m[j] = __builtin_fmaf(d[j], strength, base[j]);
+  // "update == 0 keeps the base" (P/_triton_nvfp4_lora.py:183-186).  Where
+  // d * strength == 0 the fma gives base + (+-0), which is the base itself
+  // unless the base is a zero, and then the fma's result is a zero too.  So
+  // the rule can change a value only where that value is +-0: a block whose
+  // merged values are all non-zero is final, and a block with a zero re-applies
+  // the rule element by element.
+  float mmin = __builtin_fabsf(m[0]);
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int j = 2 * q + e;
-        const float base = bf16r(pr[e] * bs);
-        m[j] = (d[j] * strength == 0.0f) ? base : __builtin_fmaf(d[j], strength, base);
-      }
-    }
-  } else {
+  for (int j = 1; j < 15; j += 2) mmin = min3_abs(mmin, m[j], m[j + 1]);
+  mmin = __builtin_fminf(mmin, __builtin_fabsf(m[15]));
+  if (mmin == 0.0f) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const v2f32 pr = e2m1_pair(w[q >> 2], q & 3);
-#pragma unroll
-      for (int e = 0; e < 2; ++e) m[2 * q + e] = __builtin_fmaf(d[2 * q + e], strength, bf16r(pr[e] * bs));
-    }
+    for (int j = 0; j < 16; ++j) m[j] = (d[j] * strength == 0.0f) ? base[j] : m[j];
   }
 }
 

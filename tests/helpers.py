@@ -131,3 +131,18 @@ def gguf_blocks(quant_type: int, nblocks: int, seed: int) -> np.ndarray:
     for off in GGUF_F16_FIELDS[quant_type]:
         raw[:, off:off + 2] = random_f16_bits(nblocks, rng).view(np.uint8).reshape(nblocks, 2)
     return raw.reshape(-1)
+
+
+def mismatch_report(got: np.ndarray, want: np.ndarray, what: str, cols_per_tile: int) -> str:
+    """'' when equal; otherwise the count and the first mismatching (row, column, tile) positions."""
+    got = np.asarray(got)
+    want = np.asarray(want)
+    if got.shape != want.shape:
+        return f"{what}: shape {got.shape} != {want.shape}"
+    bad = np.argwhere(got != want) if got.ndim > 1 else np.argwhere((got != want).reshape(-1, 1))
+    if bad.size == 0:
+        return ""
+    first = ", ".join(
+        f"(row {int(r)}, col {int(c)}, tile {int(c) // cols_per_tile}: {got[r, c] if got.ndim > 1 else got[r]} "
+        f"!= {want[r, c] if got.ndim > 1 else want[r]})" for r, c in bad[:6])
+    return f"{what}: {len(bad)} of {want.size} differ; first {first}"

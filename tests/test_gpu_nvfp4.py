@@ -138,3 +138,36 @@ def test_nvfp4_zero_update_rows_keep_signed_zero_codes(two_level, sr):
                                    seed=seed or 0)
     assert np.array_equal(u8_np(oq), rq)
     assert np.array_equal(u8_np(os_), rs)
+
+
+@pytest.mark.parametrize("two_level", [True, False])
+@pytest.mark.parametrize("sr", [False, True])
+def test_nvfp4_isolated_zero_updates_keep_signed_zero_codes(two_level, sr):
+    # One column per 16-element block gets an exactly zero update (its A
+    # column is zero) while the other 15 do not, so only the per-element rule
+    # keeps -0.0 (code 8) there (P/_triton_nvfp4_lora.py:183-186).  This is
+    # the pattern of the two elements (737, 3340) and (6519, 2489) of the
+    # 8B layer's up_proj whose codes once differed between launches.
+    rows, cols, rank = 1024, 4096, 16
+    w = normal_bf16((rows, cols), 0.02, 31)
+    q, s, pts = _encode(w, two_level, False)
+    b, a = lora_factors(rows, cols, rank, 32)
+    a[:, 5::16] = 0.0
+    codes = np.stack([u8_np(q) & 15, u8_np(q) >> 4], axis=-1).reshape(rows, cols)
+    assert (codes[:, 5::16] == 8).sum() > 100  # many -0 bases under a zero update
+    qd, sd, bd, ad = q.to(DEV), s.to(DEV), b.to(DEV), a.to(DEV)
+    ptsd = None if pts is None else pts.to(DEV)
+    dense = K.dequantize_nvfp4(qd, sd, ptsd, lora=(bd, ad, 2.0))
+    seed = derive_seed("nvfp4.isolated_zero", 0) if sr else None
+    rq, rs, rpts = O.nvfp4_requant(bf16_np(dense), two_level=two_level, sr_mode=O.SR_PHILOX8 if sr else O.SR_OFF,
+                                   seed=seed or 0)
+    oq, os_, opts = K.merge_nvfp4_lora(qd, sd, ptsd, 16, False, bd, ad, 2.0, rounding_seed=seed)
+    assert np.array_equal(u8_np(oq), rq)
+    assert np.array_equal(u8_np(os_), rs)
+    from piper_offload_amd.stack import StackTarget, merge_nvfp4_stack
+
+    t = StackTarget(NVFP4Weight(qd.clone(), sd.clone(), None if ptsd is None else ptsd.clone(), 16, torch.bfloat16,
+                                False), bd, ad, 2.0, seed or 0)
+    merge_nvfp4_stack([t], stochastic=sr)
+    assert np.array_equal(u8_np(t.weight.qdata), rq)
+    assert np.array_equal(u8_np(t.weight.scale), rs)
