@@ -107,21 +107,43 @@ class Int8Adapter:
         return tuple(t.qdata.shape)
 
     @staticmethod
-    def _stored_coordinates(qt: Any, a: torch.Tensor, strength: float) -> tuple[torch.Tensor, float]:  # noqa: ANN401
-        """Fold ``act_pre_scale`` into A (P/int8_adapter.py:59-141)."""
+    def _pre_scale(qt: Any) -> torch.Tensor | None:  # noqa: ANN401
+        """``act_pre_scale`` as [1, 1] or [1, in_features], or None (P/int8_adapter.py:59-100).
+
+        TorchAO multiplies the activation by it before the matmul, so a merge
+        divides A by it along the input dimension; only layouts whose meaning
+        does not depend on the activation's rank are accepted."""
         pre = getattr(qt, "act_pre_scale", None)
         if pre is None:
-            return a, strength
+            return None
+        if not pre.dtype.is_floating_point:
+            raise ValueError(f"TorchAO INT8 act_pre_scale must be floating-point for LoRA merge, got {pre.dtype}.")
+        if pre.device != qt.qdata.device:
+            raise ValueError("TorchAO INT8 act_pre_scale must be on the weight device for LoRA merge, got "
+                             f"{pre.device} and {qt.qdata.device}.")
         cols = qt.qdata.shape[-1]
         if pre.numel() == 1:
             norm = pre.reshape(1, 1)
         elif pre.ndim >= 1 and pre.shape[-1] == cols and all(s == 1 for s in pre.shape[:-1]):
             norm = pre.reshape(1, cols)
         else:
-            raise ValueError("TorchAO INT8 act_pre_scale must be a scalar or one value per input feature "
-                             f"with only singleton leading dimensions for LoRA merge; got {tuple(pre.shape)}.")
-        if not bool(torch.isfinite(norm).all()) or bool((norm == 0).any()):
-            raise ValueError("TorchAO INT8 act_pre_scale must contain only finite non-zero values for LoRA merge.")
+            raise ValueError("TorchAO INT8 act_pre_scale must be a scalar or one value per input feature with only "
+                             f"singleton leading dimensions for LoRA merge; got shape {tuple(pre.shape)} for {cols} "
+                             "input features.")
+        if not bool(torch.isfinite(norm).all()):
+            raise ValueError("TorchAO INT8 act_pre_scale must contain only finite values for LoRA merge.")
+        if bool((norm == 0).any()):
+            raise ValueError("TorchAO INT8 act_pre_scale must contain only non-zero values for LoRA merge.")
+        return norm
+
+    @staticmethod
+    def _stored_coordinates(qt: Any, a: torch.Tensor, strength: float) -> tuple[torch.Tensor, float]:  # noqa: ANN401
+        """A in stored-weight coordinates: (strength * A) / act_pre_scale, unit strength (P/int8_adapter.py:103-141)."""
+        norm = Int8Adapter._pre_scale(qt)
+        if norm is None:
+            return a, strength
+        # strength is folded in before the division, in float64, so that a tiny
+        # strength keeps A / p finite when p alone would overflow it
         stored = a.to(torch.float64).mul(strength).div(norm.to(device=a.device, dtype=torch.float64)).to(a.dtype)
         if not bool(torch.isfinite(stored).all()):
             raise ValueError("TorchAO INT8 act_pre_scale produces non-finite stored-coordinate LoRA factors.")
@@ -174,15 +196,14 @@ class Int8Adapter:
                            ) -> tuple[torch.Tensor, torch.Tensor, float] | None:
         """Transform each logical A before packing when ``act_pre_scale`` is set (P/int8_adapter.py:302-347)."""
         qt = _require(target, Int8Adapter.ATTRS, "INT8")
-        if getattr(qt, "act_pre_scale", None) is None:
+        norm = Int8Adapter._pre_scale(qt)
+        if norm is None:
             return None
         total = sum(a.shape[0] for _s, a, _b in factors)
         dev = qt.qdata.device
         a_packed = torch.empty((total, logical_shape[1]), device=dev, dtype=compute_dtype)
         b_packed = torch.empty((logical_shape[0], total), device=dev, dtype=compute_dtype)
-        pre = qt.act_pre_scale
-        cols = qt.qdata.shape[-1]
-        pre = (pre.reshape(1, 1) if pre.numel() == 1 else pre.reshape(1, cols)).to(device=dev, dtype=torch.float64)
+        pre = norm.to(device=dev, dtype=torch.float64)
         off = 0
         for strength, a, b in factors:
             nxt = off + a.shape[0]

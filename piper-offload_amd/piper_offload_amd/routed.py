@@ -1,8 +1,8 @@
 """Routed LoRA: the LoRA contribution added after a Linear instead of merged into it.
 
-Mirror of the reference's routed mode (P/lora.py:792-930).  A forward PRE
-hook on the parent module notes the input's device and a POST hook stages
-the factors there and returns ``output + residual`` with
+The reference's routed mode (P/lora.py:792-930).  A forward hook on the
+parent module stages the factors on the input's device (cached) and returns
+``output + residual`` with
 
     residual = sum_i ((x @ A_i.T) * s_i) @ B_i.T (+ bias_i * s_i)
 
@@ -16,7 +16,8 @@ Differences from the reference, on purpose:
 
 * staged factors are kept per device and dtype while the host factors are
   unmodified (their in-place version counters), instead of copied on every
-  invocation;
+  invocation, so one post-forward hook replaces the reference's pre/post
+  pair;
 * the kernel is inference-only (no autograd) and takes bfloat16 / float16
   outputs; other cases raise instead of running elsewhere.
 """
@@ -104,21 +105,6 @@ def routed_residual(x: torch.Tensor, factors: Sequence[RoutedFactor], output: to
     return out.view(output.shape)
 
 
-def _linear_input(inputs: tuple[Any, ...], kwargs: dict[str, Any]) -> torch.Tensor:
-    """The Linear input from positional or keyword arguments (P/lora.py:832-848)."""
-    if inputs:
-        x = inputs[0]
-    else:
-        try:
-            x = kwargs["input"]
-        except KeyError as exc:
-            raise TypeError("Routed LoRA expected the Linear input as either the first positional argument or the "
-                            "'input' keyword") from exc
-    if not isinstance(x, torch.Tensor):
-        raise TypeError(f"Routed LoRA requires the Linear input to be a torch.Tensor; got {type(x).__name__}")
-    return x
-
-
 class _Stager:
     """Device copies of host factors per (device, dtype), valid while the host tensors are unmodified."""
 
@@ -141,49 +127,51 @@ class _Stager:
         return staged
 
 
-def install_routed_residual_hook(parent: nn.Module, factors: Sequence[ScaledLoRAFactor]) -> Callable[[], None]:
-    """Stage factors in a PRE hook and add their residual in a POST hook (P/lora.py:869-930).
+class _RoutedHook:
+    """A forward hook that returns ``output + routed residual`` for the module it is on.
 
-    Returns an idempotent callable that removes both hooks.  One hook pair
-    covers every LoRA targeting this parent.
+    The reference stages the factors in a pre-forward hook for every
+    invocation and adds the residual in a post-forward hook that must run even
+    when the forward raises (to drop the staged copies).  Here the staged
+    copies are cached per (device, dtype) by ``_Stager``, so one post-forward
+    hook does both and there is no per-invocation state to clean up.
+    """
+
+    def __init__(self, parent: nn.Module, factors: Sequence[ScaledLoRAFactor]) -> None:
+        self.stager = _Stager(factors)
+        self.handle = parent.register_forward_hook(self, with_kwargs=True)
+
+    @staticmethod
+    def _input(args: tuple[Any, ...], kwargs: dict[str, Any]) -> torch.Tensor:
+        """``Linear.forward``'s input, given by position or as the keyword ``input``."""
+        if args:
+            x = args[0]
+        elif "input" in kwargs:
+            x = kwargs["input"]
+        else:
+            raise TypeError("Routed LoRA expected the Linear input as either the first positional argument or the "
+                            "'input' keyword")
+        if isinstance(x, torch.Tensor):
+            return x
+        raise TypeError(f"Routed LoRA requires the Linear input to be a torch.Tensor; got {type(x).__name__}")
+
+    def __call__(self, _module: nn.Module, args: tuple[Any, ...], kwargs: dict[str, Any], output: object) -> object:
+        if not isinstance(output, torch.Tensor):
+            return output
+        x = self._input(args, kwargs)
+        return routed_residual(x, self.stager.stage(x.device, output.dtype), output)
+
+    def remove(self) -> None:
+        self.handle.remove()  # a removed handle ignores further removals
+        self.stager.cache.clear()
+
+
+def install_routed_residual_hook(parent: nn.Module, factors: Sequence[ScaledLoRAFactor]) -> Callable[[], None]:
+    """Add the routed residual of ``factors`` to every output of ``parent`` (interface of P/lora.py:869-930).
+
+    Returns an idempotent callable that removes the hook.  One hook covers
+    every LoRA targeting this parent.
     """
     if not factors:
         raise ValueError("Routed LoRA hook requires at least one factor")
-    stager = _Stager(factors)
-    staged_factors: list[torch.device] = []
-
-    def pre_hook(_module: nn.Module, inputs: tuple[Any, ...], kwargs: dict[str, Any]) -> None:
-        # the staging itself waits for the output dtype (POST); the device
-        # copies are cached, so only a first call or a changed factor copies
-        x = _linear_input(inputs, kwargs)
-        staged_factors.append(x.device)
-
-    def post_hook(_module: nn.Module, inputs: tuple[Any, ...], kwargs: dict[str, Any], output: object) -> object:
-        # always_call=True also reaches this hook when the Linear or an earlier
-        # hook raised: then there may be no staged entry or tensor output
-        device = staged_factors.pop() if staged_factors else None
-        if device is None or not isinstance(output, torch.Tensor):
-            return output
-        x = _linear_input(inputs, kwargs)
-        return routed_residual(x, stager.stage(device, output.dtype), output)
-
-    pre_handle = parent.register_forward_pre_hook(pre_hook, with_kwargs=True)
-    try:
-        post_handle = parent.register_forward_hook(post_hook, with_kwargs=True, always_call=True)
-    except BaseException:
-        pre_handle.remove()
-        raise
-    removed = False
-
-    def remove_hooks() -> None:
-        nonlocal removed
-        if removed:
-            return
-        post_handle.remove()
-        pre_handle.remove()
-        staged_factors.clear()
-        stager.cache.clear()
-        removed = True
-
-    return remove_hooks
-
+    return _RoutedHook(parent, factors).remove

@@ -8,8 +8,10 @@ target's seed ``derive_seed(target_key, 0)`` (P/lora.py:356-359); weights a
 grouped kernel can merge (per-row INT8, NVFP4) go through one grouped launch
 per compatible group.  Every weight must end up byte-identical to the
 one-by-one adapter merge of the same weight with factors packed
-independently here, and the kernels behind those adapter merges are checked
-against the oracle in the per-format tests.
+independently here, and equal the oracle: its requant of the GPU dense merge
+of the original weight with those factors and seed (codes and scales bit for
+bit), or for the plain bf16 weight the oracle's dense merge within the
+floating-point contract.
 """
 
 from __future__ import annotations
@@ -20,7 +22,7 @@ import torch
 from torch import nn
 
 import oracle as O
-from helpers import bf16_np, fp8_initial, int8_initial, normal_bf16, u8_np
+from helpers import assert_merged_close, bf16_np, fp8_initial, int8_initial, mismatch_report, normal_bf16, u8_np
 
 pytestmark = pytest.mark.gpu
 
@@ -86,6 +88,40 @@ def _bytes(p: torch.Tensor) -> list[np.ndarray]:
     return [u8_np(p.detach())]
 
 
+def _oracle_errors(key: str, got: torch.Tensor, fresh: torch.Tensor, b: torch.Tensor, a: torch.Tensor,
+                   strength: float, seed: int | None) -> list[str]:
+    """Compare one merged weight with the oracle; fresh is the same weight before the merge."""
+    sr = O.SR_PHILOX8 if seed is not None else O.SR_OFF
+    seed = seed or 0
+    g, f = param_representation(got), param_representation(fresh)
+    lora = (b, a, strength)
+    if isinstance(f, Int8Weight):
+        cols = f.qdata.shape[1]
+        dense = K.dequantize_int8(f.qdata, f.scale, None, (1, cols), lora=lora)
+        rq, rs, _ = O.int8_requant(bf16_np(dense), cols, sr_mode=sr, seed=seed)
+        pairs = [(g.qdata.cpu().numpy(), rq), (g.scale.cpu().numpy().reshape(-1), rs)]
+    elif isinstance(f, Float8Weight):
+        cols = f.qdata.shape[1]
+        dense = K.dequantize_float8(f.qdata, f.scale, tuple(f.block_size), lora=lora)
+        rq, rs = O.fp8_requant(bf16_np(dense), cols, sr_mode=sr, seed=seed)
+        pairs = [(u8_np(g.qdata), rq), (g.scale.cpu().numpy().reshape(-1), rs)]
+    elif isinstance(f, NVFP4Weight):
+        dense = K.dequantize_nvfp4(f.qdata, f.scale, f.per_tensor_scale, lora=lora)
+        rq, rs, rp = O.nvfp4_requant(bf16_np(dense), two_level=f.per_tensor_scale is not None, sr_mode=sr, seed=seed)
+        pairs = [(u8_np(g.qdata), rq), (u8_np(g.scale), rs)]
+        if rp is not None:
+            pairs.append((g.per_tensor_scale.cpu().numpy().reshape(-1), rp))
+    elif isinstance(f, GGUFWeight):
+        packed = f.as_subclass(torch.Tensor)
+        dense = K.dequantize_gguf(packed, 8, lora=lora)
+        pairs = [(u8_np(g.as_subclass(torch.Tensor)), O.q8_0_requant(bf16_np(dense), sr_mode=sr, seed=seed))]
+    else:  # plain bf16: the oracle's dense merge, within the floating-point contract
+        base = bf16_np(f.detach())
+        assert_merged_close(bf16_np(g.detach()), O.merge_dense(base, bf16_np(b), bf16_np(a), strength), base)
+        return []
+    return [f"{key}: {m}" for m in (mismatch_report(x, y, "vs oracle", 64) for x, y in pairs) if m]
+
+
 @pytest.mark.parametrize("stochastic", [False, True])
 def test_merge_lora_equals_adapter_merges_with_packed_factors(stochastic):
     l1 = _lora(list(_SHAPES), 16, 10)
@@ -93,6 +129,7 @@ def test_merge_lora_equals_adapter_merges_with_packed_factors(stochastic):
     l2 = _lora(["q.weight", "o.weight", "up.weight", "dn.weight", "d.weight"], 8, 11)
     strengths = (0.5, -1.25)
     expected_model = _model()
+    packed = {}
     for key in _SHAPES:
         facs = [(lora.targets[key], s) for lora, s in zip((l1, l2), strengths) if key in lora.targets]
         if len(facs) == 1:
@@ -103,6 +140,7 @@ def test_merge_lora_equals_adapter_merges_with_packed_factors(stochastic):
             b = torch.cat([f.b.to(DEV) for f, _s in facs], dim=1).contiguous()
             strength = 1.0
         assert a.dtype is torch.bfloat16
+        packed[key] = (b, a, strength)
         data = param_representation(dict(expected_model.named_parameters())[key])
         _ADAPTERS[key].merge_lora_(data, b, a, strength,
                                    rounding_seed=derive_seed(key, 0) if stochastic else None)
@@ -114,6 +152,14 @@ def test_merge_lora_equals_adapter_merges_with_packed_factors(stochastic):
     for key in _SHAPES:
         for x, y in zip(_bytes(got[key]), _bytes(want[key])):
             assert np.array_equal(x, y), key
+    # and every weight equals the oracle
+    fresh_params = dict(_model().named_parameters())
+    errors = []
+    for key in _SHAPES:
+        b, a, strength = packed[key]
+        errors += _oracle_errors(key, got[key], fresh_params[key], b, a, strength,
+                                 derive_seed(key, 0) if stochastic else None)
+    assert not errors, "\n".join(errors)
     # the grouped path was taken for the INT8 and NVFP4 pairs
     keys = {}
     for key in ("q.weight", "o.weight", "up.weight", "dn.weight"):

@@ -255,3 +255,27 @@ def test_int8_config2_full_size_properties():
     obase = O.int8_dequant(q.numpy()[idx], s.numpy()[idx], None, cols)
     omerged = O.merge_dense(obase, bf16_np(b)[idx], bf16_np(a), 0.5)
     assert_merged_close(dense_np[idx], omerged, obase)
+
+
+@pytest.mark.parametrize("pre_shape", [(), (512,), (1, 1, 512)])
+@pytest.mark.parametrize("sr", [False, True])
+def test_int8_act_pre_scale_merge_equals_the_oracle(pre_shape, sr):
+    # TorchAO applies act_pre_scale p to the activation, so the merge adds
+    # B @ ((strength * A) / p) to the stored weight, the fold done in float64
+    # and rounded to the factor dtype (P/int8_adapter.py:103-141); the adapter's
+    # result must equal the oracle requant of the dense merge with that factor
+    rows, cols, rank, strength = 64, 512, 16, 0.75
+    q, s = int8_initial(normal_bf16((rows, cols), 0.02, 71))
+    b, a = lora_factors(rows, cols, rank, 72)
+    pre = torch.linspace(0.5, 2.0, cols).reshape(pre_shape) if pre_shape else torch.tensor(1.5)
+    stored = (a.double() * strength / pre.reshape(1, -1).double()).to(torch.bfloat16)
+    qd, sd, bd = q.to(DEV), s.to(DEV), b.to(DEV)
+    dense = K.dequantize_int8(qd, sd, None, (1, cols), lora=(bd, stored.to(DEV), 1.0))
+    seed = derive_seed("int8.act_pre_scale", 0) if sr else None
+    rq, rs, _ = O.int8_requant(bf16_np(dense), cols, sr_mode=O.SR_PHILOX8 if sr else O.SR_OFF, seed=seed or 0)
+    w = Int8Weight(qd.clone(), sd.clone(), (1, cols), torch.bfloat16, act_pre_scale=pre.to(DEV))
+    Int8Adapter.validate_lora_merge(w, bd, a.to(DEV), strength)
+    Int8Adapter.merge_lora_(w, bd, a.to(DEV), strength, rounding_seed=seed)
+    assert np.array_equal(w.qdata.cpu().numpy(), rq)
+    assert np.array_equal(w.scale.cpu().numpy().reshape(-1), rs)
+    assert Int8Adapter.stack_key(w) is None  # the grouped launch would skip the pre-scale: kept out of it

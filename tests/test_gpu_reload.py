@@ -1,6 +1,8 @@
 """Merge on reload (P/model_offloader.py:245-288 post-copy hooks) through
-ReloadMergePipeline: every reload re-merges the pristine stored weights, and
-the result equals a grouped stack merge of copies of them with the same seeds."""
+ReloadMergePipeline: every reload re-merges the pristine stored weights.  Each
+reloaded weight equals the oracle's requant of the GPU dense merge of the
+stored weight with seed derive_seed(path, merge_index), and a grouped stack
+merge of copies of the stored weights with the same seeds."""
 
 from __future__ import annotations
 
@@ -8,11 +10,13 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import int8_initial, lora_factors, normal_bf16
+import oracle as O
+from helpers import bf16_np, int8_initial, lora_factors, mismatch_report, normal_bf16
 
 pytestmark = pytest.mark.gpu
 
 R = pytest.importorskip("piper_offload_amd.reload")
+K = pytest.importorskip("piper_offload_amd.kernels")
 from piper_offload_amd import Int8Weight, derive_seed  # noqa: E402
 from piper_offload_amd.stack import StackTarget, merge_int8_stack  # noqa: E402
 
@@ -40,11 +44,28 @@ def _expected(layer: list[R.HostInt8Target], merge_index: int, stochastic: bool)
     return ws
 
 
-def _check(got: R.Reloaded, want: list[Int8Weight]) -> None:
+def _oracle(layer: list[R.HostInt8Target], merge_index: int, stochastic: bool) -> list[tuple]:
+    """Per target: the oracle's requant of the GPU dense merge of the stored weight."""
+    out = []
+    for t in layer:
+        cols = t.qdata.shape[1]
+        dense = K.dequantize_int8(t.qdata.to(DEV), t.scale.to(DEV), None, (1, cols), lora=(t.b, t.a, t.strength))
+        seed = derive_seed(t.path, merge_index)
+        rq, rs, _ = O.int8_requant(bf16_np(dense), cols, sr_mode=O.SR_PHILOX8 if stochastic else O.SR_OFF,
+                                   seed=seed if stochastic else 0)
+        out.append((rq, rs))
+    return out
+
+
+def _check(got: R.Reloaded, want: list[Int8Weight], oracle: list[tuple] | None = None) -> None:
     got.wait()
     for g, w in zip(got.weights, want):
         assert torch.equal(g.qdata, w.qdata)
         assert torch.equal(g.scale, w.scale)
+    for i, (g, (rq, rs)) in enumerate(zip(got.weights, oracle or [])):
+        m = mismatch_report(g.qdata.cpu().numpy(), rq, f"target {i} codes vs oracle", 64)
+        assert not m, m
+        assert np.array_equal(g.scale.cpu().numpy().reshape(-1), rs), f"target {i} scales vs oracle"
 
 
 @pytest.mark.parametrize("stochastic", [True, False])
@@ -54,11 +75,11 @@ def test_reloads_equal_stack_merges_of_the_stored_weights(stochastic: bool) -> N
     order = [(0, 0), (1, 0), (2, 0), (0, 1), (1, 1), (0, 2)]
     for layer, mi in order:
         got = pipe.reload(layer, mi)
-        _check(got, _expected(layers[layer], mi, stochastic))
+        _check(got, _expected(layers[layer], mi, stochastic), _oracle(layers[layer], mi, stochastic))
         pipe.release(got)
     # the stored weights are untouched
     again = pipe.reload(0, 1)
-    _check(again, _expected(layers[0], 1, stochastic))
+    _check(again, _expected(layers[0], 1, stochastic), _oracle(layers[0], 1, stochastic))
 
 
 def test_two_reloads_in_flight_keep_their_own_slots() -> None:
