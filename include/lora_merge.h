@@ -143,6 +143,20 @@ int lm_int8_merge(const int8_t* q, const void* scale, const int8_t* zero_point, 
                   int8_t* zero_point_out, int64_t M, int64_t N, int64_t group, int32_t scale_dtype, int32_t asymmetric,
                   int32_t reduce_range, const lm_lora* lora, const lm_rounding* rounding, void* workspace,
                   size_t workspace_bytes, void* stream);
+/* lm_int8_merge without a workspace argument: NO counterpart in the reference.
+ * It is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The call
+ * allocates nothing: its scratch is a static device array of
+ * LM_NOALLOC_SCRATCH_BYTES that each GPU holds until the process ends.  A
+ * shape whose lm_workspace_size(M, N, rank) exceeds that fails with
+ * LM_EWORKSPACE before any device work.  All calls on one GPU share its
+ * array: calls that overlap on one GPU (several streams or threads) race.
+ * Results equal lm_int8_merge's bit for bit. */
+#define LM_NOALLOC_SCRATCH_BYTES (8u << 20)
+int lm_int8_merge_noalloc(const int8_t* q, const void* scale, const int8_t* zero_point, int8_t* q_out,
+                          void* scale_out, int8_t* zero_point_out, int64_t M, int64_t N, int64_t group,
+                          int32_t scale_dtype, int32_t asymmetric, int32_t reduce_range, const lm_lora* lora,
+                          const lm_rounding* rounding, void* stream);
 int lm_int8_requant(const void* dense, int32_t dense_dtype, int8_t* q_out, void* scale_out, int8_t* zero_point_out,
                     int64_t M, int64_t N, int64_t group, int32_t scale_dtype, int32_t asymmetric, int32_t reduce_range,
                     const lm_rounding* rounding, void* workspace, size_t workspace_bytes, void* stream);

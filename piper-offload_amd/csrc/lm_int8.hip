@@ -120,3 +120,62 @@ extern "C" int lm_int8_dequant(const int8_t* q, const void* scale, const int8_t*
   return run_blocks<B_INT8, P_TODENSE>(a, cd, c.nkc, false, false, c.st);
 }
 
+
+// ---------------------------------------------------------------------------
+// lm_int8_merge_noalloc: lm_int8_merge with its workspace in a static device
+// array, for callers that cannot allocate (code under HIP graph capture, tight
+// serving loops).  Each GPU holds its own copy of `scratch` from module load to
+// process exit.  Host code never passes the array's name to a kernel or a copy
+// (it is a host-side stand-in, not a device address): the address comes from
+// hipGetSymbolAddress, taken once per device with that device current on the
+// first call there, and kept per device.  Every call on a GPU shares that
+// GPU's array; the factor-relayout kernel rewrites the whole region a call
+// reads (the transposed A, the packed B and the cleared reduction slots), so
+// nothing of an earlier call survives into a later one.  Calls that overlap
+// on one GPU (several streams or threads) race on the array.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[LM_NOALLOC_SCRATCH_BYTES];
+
+#include <mutex>
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};
+}  // namespace
+
+static int scratch_of_current_device(void** out) {
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kScratchDevices)
+    return fail(LM_EUNSUPPORTED, "lm_int8_merge_noalloc supports device ordinals below %d, got %d", kScratchDevices, dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(LM_EHIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return LM_OK;
+}
+
+extern "C" int lm_int8_merge_noalloc(const int8_t* q, const void* scale, const int8_t* zero_point, int8_t* q_out,
+                                     void* scale_out, int8_t* zero_point_out, int64_t M, int64_t N, int64_t group,
+                                     int32_t scale_dtype, int32_t asymmetric, int32_t reduce_range, const lm_lora* lora,
+                                     const lm_rounding* rounding, void* stream) {
+  int rc;
+  if (!lora) return fail(LM_EINVAL, "lm_int8_merge_noalloc requires LoRA factors");
+  if ((rc = check_int8_layout(M, N, group, scale_dtype))) return rc;
+  if ((rc = check_lora(lora, M, N))) return rc;
+  const size_t need = lm_workspace_size(M, N, lora->rank);
+  if (need > (size_t)LM_NOALLOC_SCRATCH_BYTES)
+    return fail(LM_EWORKSPACE,
+                "lm_int8_merge_noalloc: a [%lld, %lld] rank-%d merge needs %zu bytes of scratch, above the %zu-byte "
+                "static array; use lm_int8_merge with a caller workspace",
+                (long long)M, (long long)N, (int)lora->rank, need, (size_t)LM_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if ((rc = scratch_of_current_device(&ws))) return rc;
+  return lm_int8_merge(q, scale, zero_point, q_out, scale_out, zero_point_out, M, N, group, scale_dtype, asymmetric,
+                       reduce_range, lora, rounding, ws, (size_t)LM_NOALLOC_SCRATCH_BYTES, stream);
+}
