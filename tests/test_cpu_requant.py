@@ -336,3 +336,47 @@ def test_fp8_group_is_per_row_of_the_group_view(g, fmt, sr):
     rq, rs = O.fp8_requant(dense.reshape(-1, g), g, fmt=fmt, sr_mode=sr, seed=5)
     assert np.array_equal(q.reshape(-1, g), rq)
     assert np.array_equal(s, rs)
+
+
+def _to_blocked(scales: torch.Tensor) -> torch.Tensor:
+    """TorchAO's 128x4 block-scaling layout (torchao 0.18.0, ``to_blocked``; the layout cuBLAS
+    documents for block-scaled GEMMs), written as tensor reshapes: pad rows to 128 and columns to 4,
+    cut into 128x4 tiles in row-major tile order, then inside a tile store element (32 g + l, c) at
+    16 l + 4 g + c.  The flat result is the memory of the [ceil(M/128) * 32, ceil(C/4) * 16] scale
+    tensor."""
+    rows, cols = scales.shape
+    rb, cb = -(-rows // 128), -(-cols // 4)
+    padded = torch.zeros((rb * 128, cb * 4), dtype=scales.dtype)
+    padded[:rows, :cols] = scales
+    tiles = padded.view(rb, 128, cb, 4).permute(0, 2, 1, 3)            # [rb, cb, 128, 4]
+    inner = tiles.reshape(rb * cb, 4, 32, 4).transpose(1, 2)            # [tile, l, g, c]
+    return inner.reshape(-1).reshape(rb * 32, cb * 16)
+
+
+@pytest.mark.parametrize("rows,cols", [(128, 64), (256, 512), (300, 208), (17, 48), (1000, 4096)])
+def test_nvfp4_swizzled_scales_are_torchao_to_blocked_of_the_plain_ones(rows: int, cols: int) -> None:
+    # the same weight encoded with plain and with swizzled scales: equal codes, and the swizzled
+    # scale array is the block layout of the plain one (P/_triton_nvfp4_lora.py:88-104); a swapped
+    # row-lane / row-group stride, or a wrong tile order, fails here (bijectivity alone does not)
+    dense = bf16_np(_dense(rows, cols, 40 + rows))
+    q0, s0, p0 = O.nvfp4_requant(dense, two_level=True, swizzled=False)
+    q1, s1, p1 = O.nvfp4_requant(dense, two_level=True, swizzled=True)
+    assert np.array_equal(q0, q1) and np.array_equal(p0, p1)
+    want = _to_blocked(torch.from_numpy(s0)).numpy()
+    assert s1.shape == want.shape
+    assert np.array_equal(s1, want)
+    # and the offset function agrees element by element
+    for r in range(0, rows, max(1, rows // 37)):
+        for c in range(0, cols // 16, max(1, cols // 16 // 11)):
+            assert s1.reshape(-1)[O.blocked_scale_offset(r, c, cols // 16, True)] == s0[r, c]
+
+
+@pytest.mark.parametrize("fmt", [O.DT_E2M1, O.DT_E4M3])
+@pytest.mark.parametrize("rows,cols", [(128, 128), (300, 640), (33, 256)])
+def test_mx_swizzled_scales_are_torchao_to_blocked_of_the_plain_ones(fmt: int, rows: int, cols: int) -> None:
+    # MX's e8m0 block-32 scales use the same layout (P/_triton_mx_lora.py:97-112)
+    dense = bf16_np(_dense(rows, cols, 60 + rows))
+    q0, s0 = O.mx_requant(dense, fmt, swizzled=False)
+    q1, s1 = O.mx_requant(dense, fmt, swizzled=True)
+    assert np.array_equal(q0, q1)
+    assert np.array_equal(s1, _to_blocked(torch.from_numpy(s0)).numpy())
