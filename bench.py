@@ -13,8 +13,9 @@ whole stack once, in place, through the grouped HIP kernel.
 ``value`` is algorithmic GB/s: per target 2*M*N (codes in + out) + 8*M
 (fp32 scales in + out) + 2*r*(M+N) (bf16 factors), over the step time.  The
 ``roofline`` block uses the dominant kernel's own HIP-event time; the
-``cpu_baseline`` block times the CPU oracle (a C restatement of the same
-merge) on a bounded sample of the same workload.
+``cpu_baseline`` block times the reference's portable merge (dequantize,
+addmm_, requantize) in torch CPU ops on the host cores, on a bounded sample of
+the same workload.
 
     python bench.py [--steps K] [--warmup W]
                     [--workload int8_stack|nvfp4_stack|int8|fp8|q8_0|nvfp4|mxfp4|gguf|reload|h2d|copy]
@@ -509,64 +510,103 @@ class Single(Workload):
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the oracle (C restatement, OpenMP) on a bounded sample
+# CPU baseline: the reference's portable path in torch CPU ops, bounded sample
 # ---------------------------------------------------------------------------
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(kind: str, stochastic: bool, budget_s: float, gguf_type: str = "Q4_K") -> dict | None:
+    """Time the CPU path on the host cores, on a bounded sample of the workload.
+
+    INT8 workloads run the reference's portable merge (dequantize, addmm_,
+    requantize; oracle/portable.py) with torch CPU ops on every core of this
+    process's affinity, as BASELINE.md prescribes: one warm-up, then repeats
+    until the budget is spent (at least 5), and the median repeat is reported.
+    GGUF runs the oracle's dequantize (C, OpenMP).
+    """
     if budget_s <= 0:
         return None
-    import numpy as np
+    import statistics
+
+    import torch
 
     cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
     os.environ.setdefault("OMP_NUM_THREADS", str(cores))
-    import oracle as O
+    from piper_offload_amd import derive_seed
 
-    rng = np.random.default_rng(0)
-    if kind in ("int8_stack", "int8"):
-        cols, rank, strength = 4096, (16 if kind == "int8_stack" else 32), (1.0 if kind == "int8_stack" else 0.5)
-        def make(rows):  # noqa: ANN001, ANN202
-            w = (rng.standard_normal((rows, cols), dtype=np.float32) * 0.02)
-            s = np.maximum(np.abs(w).max(1) / 127.0, np.float32(1.1920929e-07)).astype(np.float32)
-            q = np.clip(np.round(w / s[:, None]), -128, 127).astype(np.int8)
-            a = O.f32_to_bf16(rng.standard_normal((rank, cols), dtype=np.float32) / rank)
-            b = O.f32_to_bf16(rng.standard_normal((rows, rank), dtype=np.float32) * 0.01)
-            return q, s, a, b
-        def run(data):  # noqa: ANN001, ANN202
-            q, s, a, b = data
-            base = O.int8_dequant(q, s, None, cols)
-            merged = O.merge_dense(base, b, a, strength)
-            O.int8_requant(merged, cols, sr_mode=O.SR_PHILOX8 if stochastic else O.SR_OFF, seed=12345)
-        def nbytes(rows):  # noqa: ANN001, ANN202
-            return _int8_bytes(rows, cols, rank)
-        shape_note = f"{cols} gate_proj-shaped INT8 tensor (rank {rank})"
-        what = f"oracle dequant + fp32 B@A + requant ({'SR' if stochastic else 'RTN'})"
+    path = "model.layers.0.mlp.gate_proj.weight"
+    rows, cols = 14336, 4096
+    if kind in ("int8_stack", "int8", "api", "reload"):
+        from oracle import portable as P
+
+        rank, strength = (32, 0.5) if kind == "int8" else (16, 1.0)
+        g = torch.Generator(device="cpu").manual_seed(derive_seed(path, 0) % (1 << 63))
+        w = torch.randn((rows, cols), generator=g) * 0.02
+        scale = (w.abs().amax(dim=1, keepdim=True) / 127.0).clamp_min(torch.finfo(torch.float32).eps)
+        q = torch.round(w / scale).clamp_(-128, 127).to(torch.int8)
+        del w
+        a = (torch.randn((rank, cols), generator=g) / rank).to(torch.bfloat16)
+        b = (torch.randn((rows, rank), generator=g) * 0.01).to(torch.bfloat16)
+        seeds = iter(range(1 << 30))
+
+        def run() -> None:
+            P.int8_merge(q, scale, b, a, strength,
+                         rounding_seed=derive_seed(path, next(seeds)) if stochastic else None)
+
+        nbytes = _int8_bytes(rows, cols, rank)
+        what = (f"reference portable path in torch CPU ops (dequantize, addmm_, requantize, "
+                f"{'stochastic' if stochastic else 'round-to-nearest'}) of one {rows} x {cols} gate_proj-shaped "
+                f"INT8 tensor, rank {rank}")
     elif kind == "gguf":
-        qtype, cols = GGUF_TYPES[gguf_type], 4096
-        def make(rows):  # noqa: ANN001, ANN202
-            return _gguf_bytes(qtype, rows, cols, 1)
-        def run(data):  # noqa: ANN001, ANN202
-            O.gguf_dequant(data, qtype, cd=O.DT_BF16)
+        import oracle as O
+
+        qtype = GGUF_TYPES[gguf_type]
+        data = _gguf_bytes(qtype, rows, cols, 1)
         from piper_offload_amd.gguf_dequant import GGML_QUANT_SIZES
 
         bs, ts = GGML_QUANT_SIZES[qtype]
-        def nbytes(rows):  # noqa: ANN001, ANN202
-            return rows * cols * 2 + rows * cols // bs * ts
-        shape_note = f"{cols} GGUF {gguf_type} tensor"
-        what = "oracle GGUF dequantize to bf16"
+
+        def run() -> None:
+            O.gguf_dequant(data, qtype, cd=O.DT_BF16)
+
+        nbytes = rows * cols * 2 + rows * cols // bs * ts
+        what = f"oracle GGUF dequantize (C, OpenMP) of one {rows} x {cols} {gguf_type} tensor to bf16"
     else:
         return None
-    # the sample is one full gate_proj-shaped tensor, merged repeatedly until
-    # the budget is spent (at least twice); throughput over every repeat
-    rows = 14336
-    data = make(rows)
-    run(data)  # first touch of the buffers and the thread pool
-    reps, t0 = 0, time.perf_counter()
-    while reps < 2 or time.perf_counter() - t0 < budget_s:
-        run(data)
-        reps += 1
-    t = time.perf_counter() - t0
-    return {"value": round(nbytes(rows) * reps / t / 1e9, 3), "unit": "GB/s",
-            "cores": int(os.environ.get("OMP_NUM_THREADS", cores)), "kind": "port",
-            "sample": f"{what} of one {rows} x {shape_note}, {reps} repeats in {t:.1f} s"}
+    run()  # warm-up: first touch of the buffers and the thread pool
+    times: list[float] = []
+    t_start = time.perf_counter()
+    while len(times) < 5 or time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "cpu": _cpu_model(), "ms_per_merge": round(med * 1e3, 1),
+            "sample": f"{what}: median of {len(times)} repeats after one warm-up ({sum(times):.1f} s)"}
+
+
+def _limiter(name: str, stochastic: bool) -> dict | None:
+    """What the counters say limits the dominant kernel below its roofline, from the
+    committed counter summary of this workload (profiles/<name>_counters.json)."""
+    path = os.path.join(ROOT, "profiles", f"{name}_counters.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+        if "stochastic" in rec and bool(rec["stochastic"]) != stochastic:
+            return None
+        return {"limiter": rec["limiter"], "evidence": rec["evidence"], "source": f"profiles/{name}_counters.json"}
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def _traffic(name: str, kbytes: int, stochastic: bool) -> int | None:
@@ -666,8 +706,13 @@ def main() -> int:
         "data": "synthetic",
         "config": wl.config,
         "hbm_peak_fraction": round(value / HBM_PEAK_GBS, 4),
+        # bound: the roofline the kernel is measured against (HBM: the merge's
+        # arithmetic intensity, 2r flops per 2 bytes, is far below the MFMA
+        # ridge of 2.5 PFLOP/s / 8 TB/s); limiter: what the counters say stops
+        # it short of that roofline
         "roofline": {
             "bound": "hbm",
+            **(_limiter(wl.name, stochastic) or {}),
             "kernel": wl.family,
             "achieved": None if achieved is None else round(achieved, 2),
             "peak": HBM_PEAK_GBS,

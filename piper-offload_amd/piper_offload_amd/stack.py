@@ -73,6 +73,11 @@ class StackPlan:
     targets' storage and factors must stay alive and keep their addresses for
     the plan's lifetime; their contents may change between merges (that is
     the point: each merge updates the weights in place).
+
+    Every merge reuses one workspace (the factor layouts and the descriptor
+    table).  A merge therefore makes its stream wait for the previous merge's
+    completion event, so merges issued on different streams run one after the
+    other instead of overwriting buffers an earlier launch still reads.
     """
 
     def __init__(self, targets: Sequence[StackTarget], kind: str) -> None:
@@ -100,6 +105,7 @@ class StackPlan:
         with torch.cuda.device(self.device):
             self._ws = L.workspace(self._ws_bytes, self.device)
         self._ws_ptr = L.aligned_ptr(self._ws)
+        self._last: torch.cuda.Event | None = None  # completion of the previous merge
 
     def merge(self, seeds: Sequence[int] | None = None, *, stochastic: bool = True) -> None:
         """Merge every target once; ``seeds`` (one per target) replace the targets' seeds."""
@@ -111,16 +117,22 @@ class StackPlan:
         lib = L.lib()
         mode = L.LM_ROUND_STOCHASTIC if stochastic else L.LM_ROUND_NEAREST
         with torch.cuda.device(self.device):
-            stream = L.stream_ptr(self.device)
+            current = torch.cuda.current_stream(self.device)
+            if self._last is not None:
+                current.wait_event(self._last)
+            stream = current.cuda_stream
             if self.kind == "int8":
                 rc = lib.lm_int8_merge_stack(self._arr, len(self.targets), L.torch_dtype_id(self._scale_dtype), mode,
                                              self._ws_ptr, self._ws_bytes, stream)
             else:
                 rc = lib.lm_nvfp4_merge_stack(self._arr, len(self.targets), int(self._swizzled), mode,
                                               self._ws_ptr, self._ws_bytes, stream)
-            # the workspace is reused by the next merge on this stream: keep the
-            # caching allocator from handing it to another stream meanwhile
-            self._ws.record_stream(torch.cuda.current_stream(self.device))
+            # the caching allocator must not hand the workspace to another stream
+            # while this merge may still read it
+            self._ws.record_stream(current)
+            if rc == L.LM_OK:
+                self._last = torch.cuda.Event()
+                self._last.record(current)
         L.check(rc)
 
 

@@ -303,3 +303,30 @@ def test_config5_nvfp4_stack_224_targets(sr):
                     errors.append(f"{paths[i]} vs oracle: {m}")
         del dense, pq, ps
     assert not errors, "\n".join(errors[:20])
+
+
+def test_stack_plan_merges_on_two_streams_run_in_order():
+    # one plan, one workspace: a merge issued on a second stream must wait for
+    # the first one (its completion event), or it would overwrite the factor
+    # layouts and descriptors the first launch still reads
+    tg = _int8_targets([(4096, 4096), (1024, 4096)], 16, 80)
+    targets = [StackTarget(Int8Weight(q.clone().to(DEV), s.clone().to(DEV), (1, q.shape[1]), torch.bfloat16),
+                           b, a, strength, 0) for q, s, b, a, strength, _ in tg]
+    plan = StackPlan(targets, "int8")
+    side = torch.cuda.Stream()
+    seeds = [[derive_seed(f"two.{i}", step) for i in range(len(targets))] for step in range(2)]
+    plan.merge(seeds[0])  # default stream
+    with torch.cuda.stream(side):
+        plan.merge(seeds[1])  # no host synchronization in between
+    torch.cuda.synchronize()
+    current = [(q, s) for q, s, *_ in tg]
+    for step in range(2):
+        nxt = []
+        for (cq, cs), (_, _, b, a, strength, _), seed in zip(current, tg, seeds[step]):
+            rq, rs = _int8_oracle(cq, cs, b, a, strength, seed, True)
+            nxt.append((torch.from_numpy(rq), torch.from_numpy(rs).reshape(-1, 1)))
+        current = nxt
+    for i, (t, (rq, rs)) in enumerate(zip(targets, current)):
+        m = mismatch_report(t.weight.qdata.cpu().numpy(), rq.numpy(), f"item {i} codes", 64)
+        assert not m, m
+        assert torch.equal(t.weight.scale.cpu().reshape(-1), rs.reshape(-1))
