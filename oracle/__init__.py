@@ -70,6 +70,8 @@ _SIGS = {
     "lmo_e8m0_to_f32": (None, [_P, _P, _I64]),
     "lmo_mx_scale": (None, [_P, _I64, _I, _I, _P, _P]),
     "lmo_sr_int": (None, [_P, _P, _P, _I64, _I, _I, _P]),
+    "lmo_sr_int13": (None, [_P, _P, _P, _P, _I64, _I, _I, _P]),
+    "lmo_sr_h16": (None, [ctypes.c_uint64, ctypes.c_uint64, _I64, _P]),
     "lmo_sr_e2m1": (None, [_P, _P, _P, _I64, _P]),
     "lmo_sr_fp8": (None, [_I, _P, _P, _I64, _F, _P]),
     "lmo_version": (_I, []),
@@ -216,6 +218,24 @@ def sr_int(x, det, u, qmin, qmax):
     u = np.ascontiguousarray(u, np.float32)
     out = np.empty(x.shape, np.int32)
     load().lmo_sr_int(_p(x), _p(det), _p(u), x.size, qmin, qmax, _p(out))
+    return out
+
+
+def sr_int13(v, rcp, zp, h, qmin, qmax):
+    """Integer stochastic rounding of v / s + zp on the 13-bit grid (rcp = RN(1 / s), h = 16-bit draws)."""
+    v = np.ascontiguousarray(v, np.float32)
+    rcp = np.ascontiguousarray(np.broadcast_to(np.asarray(rcp, np.float32), v.shape))
+    zp = np.ascontiguousarray(np.broadcast_to(np.asarray(zp, np.float32), v.shape))
+    h = np.ascontiguousarray(np.broadcast_to(np.asarray(h, np.uint32), v.shape))
+    out = np.empty(v.shape, np.int32)
+    load().lmo_sr_int13(_p(v), _p(rcp), _p(zp), _p(h), v.size, qmin, qmax, _p(out))
+    return out
+
+
+def sr_h16(seed: int, start: int, n: int) -> np.ndarray:
+    """The 16-bit Philox draws of offsets start .. start + n - 1 (uniform = h * 2^-16)."""
+    out = np.empty(n, np.uint32)
+    load().lmo_sr_h16(seed, start, n, _p(out))
     return out
 
 

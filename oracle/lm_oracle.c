@@ -223,6 +223,44 @@ static inline int sr_int(float x, int det, float u, int qmin, int qmax) {
   float rounded = lower + ((u < p) ? 1.0f : 0.0f);
   return (interior && p > 0.0f) ? (int)rounded : det;
 }
+/* 16-bit Philox draw h of the element at offset idx (SR_PHILOX8 layout; the
+ * uniform of sr_uniform is h * 2^-16). */
+static inline uint32_t sr_h16(uint64_t seed, uint64_t idx) {
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+  uint64_t g = idx >> 3;
+  uint32_t c[4] = {(uint32_t)g, (uint32_t)(g >> 32), 0, 0};
+  philox4x32(c, k0, k1, 10);
+  int j = (int)(idx & 7);
+  uint32_t w = c[j >> 1];
+  return (j & 1) ? (w >> 16) : (w & 0xffffu);
+}
+/* Integer stochastic rounding (INT8, Q8_0) in the form the HIP kernels run on
+ * gfx950's v_cvt_sr_f16_f32 (the selection rule of
+ * P/_triton_stochastic_quantization.py:25-40, u < p):
+ *   t = clamp(RN(v * rcp + (1536 + zp)), 1536 + qmin, 1536 + qmax)
+ *   code = floor(t) - 1536 + [u < frac(t)],  u = (h >> 3) * 2^-13.
+ * rcp = RN(1 / s).  t lies in [1024, 2048), where fp32 keeps 13 fraction bits,
+ * so frac(t) is p = frac(v / s + zp) rounded to 13 bits and u is the draw
+ * truncated to 13 bits.  Exact integers and clamped values keep their code.
+ * The clamp is v_med3_f32's: a NaN t gives 1536 + qmin.  (The instruction's
+ * rule, measured on MI355X over every 13-bit fraction and 13-bit random
+ * field: round up iff (R >> 19) + frac * 2^13 >= 2^13; the kernels pass
+ * R = (65535 - h) << 16, i.e. R >> 19 = 8191 - (h >> 3).) */
+static inline int sr_int13(float v, float rcp, float zp, int qmin, int qmax, uint32_t h) {
+  float lo = 1536.0f + (float)qmin, hi = 1536.0f + (float)qmax;
+  float t = fmaf(v, rcp, 1536.0f + zp);
+  t = isnan(t) ? lo : fminf(fmaxf(t, lo), hi);
+  float fl = floorf(t);
+  uint32_t frac13 = (uint32_t)((t - fl) * 8192.0f);
+  return (int)fl - 1536 + (((h >> 3) < frac13) ? 1 : 0);
+}
+EXPORT void lmo_sr_int13(const float* v, const float* rcp, const float* zp, const uint32_t* h, int64_t n, int qmin,
+                         int qmax, int32_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = sr_int13(v[i], rcp[i], zp[i], qmin, qmax, h[i]);
+}
+EXPORT void lmo_sr_h16(uint64_t seed, uint64_t start, int64_t n, uint32_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = sr_h16(seed, start + (uint64_t)i);
+}
 /* The up-probability p = (|x| - lo) / (hi - lo) of the 4- and 8-bit float
  * formats is exact in fp32 (the grid steps are powers of two).  It is used
  * truncated to W fraction bits, W = 23 - (target mantissa bits): 22 for e2m1,
@@ -348,7 +386,9 @@ EXPORT void lmo_int8_requant(const void* dense, int cd, int64_t M, int64_t N, in
       float scaled = round_dt(scale_dt, v * inv);
       int qv = isnan(scaled) ? 0 : (int)nearbyintf(scaled);
       qv += zp;
-      if (sr_mode != SR_OFF) {
+      if (sr_mode == SR_PHILOX8) {
+        qv = sr_int13(v, 1.0f / s, (float)zp, qmin, qmax, sr_h16(seed, (uint64_t)f));
+      } else if (sr_mode != SR_OFF) {
         float x = v / s + (float)zp;
         qv = sr_int(x, qv, sr_uniform(sr_mode, seed, (uint64_t)f), qmin, qmax);
       }
@@ -582,7 +622,7 @@ EXPORT void lmo_q8_0_dequant(const uint8_t* packed, int64_t M, int64_t N, int cd
 }
 /* requant: ggml quantize_row_q8_0_ref (MIT): d = amax/127, id = d ? 1/d : 0,
  * q = roundf(x*id) (half away from zero), store fp16(d). SR (an extension: the
- * reference routes GGUF only) selects floor/ceil of x*id with P(up) = frac. */
+ * reference routes GGUF only) is the integer rule sr_int13 with rcp = id. */
 EXPORT void lmo_q8_0_requant(const void* dense, int cd, int64_t M, int64_t N, int sr_mode, uint64_t seed,
                              uint8_t* packed_out) {
   int64_t nb = N / 32, rowbytes = nb * 34;
@@ -602,7 +642,9 @@ EXPORT void lmo_q8_0_requant(const void* dense, int cd, int64_t M, int64_t N, in
       for (int t = 0; t < 32; ++t) {
         float x = v[t] * id;
         int qv = (int)roundf(x);
-        if (sr_mode != SR_OFF) qv = sr_int(x, qv, sr_uniform(sr_mode, seed, (uint64_t)(i * N + b * 32 + t)), -127, 127);
+        if (sr_mode == SR_PHILOX8) qv = sr_int13(v[t], id, 0.0f, -127, 127, sr_h16(seed, (uint64_t)(i * N + b * 32 + t)));
+        else if (sr_mode != SR_OFF)
+          qv = sr_int(x, qv, sr_uniform(sr_mode, seed, (uint64_t)(i * N + b * 32 + t)), -127, 127);
         blk[2 + t] = (uint8_t)(int8_t)qv;
       }
     }

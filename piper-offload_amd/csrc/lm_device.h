@@ -310,18 +310,8 @@ DEV void sr_words_aligned(uint64_t seed, uint64_t idx0, uint32_t (&w)[SPAN / 2])
   }
 }
 // u < p with u = h * 2^-16 (exact: both sides scaled by 2^16)
-DEV bool sr_up(uint32_t h, float p) { return (float)h < p * 65536.0f; }
 
 // ---- stochastic selections (P/_triton_stochastic_quantization.py) --------
-// :25-40
-DEV int sr_int(float x, int det, uint32_t h, float qmin, float qmax) {
-  bool interior = (x > qmin) && (x < qmax);
-  float safe = interior ? x : 0.0f;
-  float lower = __builtin_floorf(safe);
-  float p = safe - lower;
-  float rounded = lower + (sr_up(h, p) ? 1.0f : 0.0f);
-  return (interior && p > 0.0f) ? (int)rounded : det;
-}
 // ---- stochastic 4- and 8-bit float conversions (gfx950 hardware) ----------
 // v_cvt_scalef32_sr_{pk_fp4,fp8,bf8}_f32 (scale 1.0) round x onto the target
 // grid with a 32-bit random operand R: with W = 23 - (target mantissa bits)
@@ -477,33 +467,33 @@ DEV uint32_t pack_low_bytes(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) 
   uint32_t hi = __builtin_amdgcn_perm(w3, w2, 0x0c0c0400u);
   return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
-// byte 2 of four 32-bit words -> one word (byte k from w_k)
-DEV uint32_t pack_byte2s(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
-  uint32_t lo = __builtin_amdgcn_perm(w1, w0, 0x0c0c0602u);
-  uint32_t hi = __builtin_amdgcn_perm(w3, w2, 0x0c0c0602u);
-  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-}
 
-// Stochastic rounding of y >= 0 (or any sign) onto the integer grid with the
-// reference's rule  up <=> u < frac(y),  u = h * 2^-16  (h a 16-bit uniform):
-// with X = ceil(65536 * y),  result = floor((X + 65535 - h) / 65536).
-// y16 = 65536 * y must be exactly representable (|y| < 2^7 for fp32 inputs
-// of 24-bit precision keeps every step exact).  Equivalent to
-// lower + (u < frac) for all finite y; an integer y stays y.
-// floor(-x) as int32 in one v_cvt_flr_i32_f32 (= -ceil(x)); |x| < 2^31
-DEV int cvt_flr_neg(float x) {
-  asm("v_cvt_flr_i32_f32_e64 %0, -%0" : "+v"(x));  // output tied to the input
-  return (int)f2u(x);
+// ---- integer stochastic rounding on gfx950's v_cvt_sr_f16_f32 -------------
+// INT8 and Q8_0 codes round v / s + zp stochastically (the selection of
+// P/_triton_stochastic_quantization.py:25-40, u < p) through the hardware's
+// stochastic conversion to f16.  The caller forms
+//   t = med3(fma(v, RN(1/s), 1536 + zp), 1536 + qmin, 1536 + qmax):
+// fp32 in [1024, 2048) keeps 13 fraction bits and f16 has spacing 1 there, so
+// the conversion picks floor(t) or floor(t) + 1.  Its rule, measured on
+// MI355X over every 13-bit fraction and every 13-bit random field: round up
+// iff (R >> 19) + frac(t) 2^13 >= 2^13.  With R = (65535 - h) << 16, h the
+// element's 16-bit Philox draw, that is u < frac(t) with u = (h >> 3) 2^-13.
+// The code is floor(t) + up - 1536, whose two's-complement low byte is the
+// low byte of the f16 result (f16 bits of 1536 + c are 0x6600 + c).
+typedef _Float16 lm_v2f16 __attribute__((ext_vector_type(2)));
+// two codes: t0 with random operand r0 in byte 0, t1 with r1 in byte 2 (the
+// conversions overwrite both halves of `old`, which only gives a register)
+DEV uint32_t sr_i8_pair(uint32_t old, float t0, float t1, uint32_t r0, uint32_t r1) {
+  lm_v2f16 o = __builtin_bit_cast(lm_v2f16, old);
+  o = __builtin_amdgcn_cvt_sr_f16_f32(o, t0, r0, false);
+  o = __builtin_amdgcn_cvt_sr_f16_f32(o, t1, r1, true);
+  return __builtin_bit_cast(uint32_t, o);
 }
-// (w & 0xffff) - t in one SDWA subtract (word 0 of w)
-DEV uint32_t sub_lo16(uint32_t w, uint32_t t) {
-  asm("v_sub_u32_sdwa %0, %1, %0 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD"
-      : "+v"(t) : "v"(w));  // output tied to t
-  return t;
-}
-DEV int sr_grid(float y16, uint32_t h) {
-  int fneg = (int)__builtin_floorf(-y16);  // floor(-y16) = -ceil(y16)
-  return ((int)(65535u - h) - fneg) >> 16;
+// the four codes of two pairs (bytes 0 and 2 of each) as one word
+DEV uint32_t pack_sr_i8(uint32_t p01, uint32_t p23) { return __builtin_amdgcn_perm(p23, p01, 0x06040200u); }
+// t of the rule above
+DEV float sr_i8_t(float v, float rcp, float base, float lo, float hi) {
+  return __builtin_amdgcn_fmed3f(__builtin_fmaf(v, rcp, base), lo, hi);
 }
 
 // ---- blocked (swizzled) scale offsets: P/_triton_nvfp4_lora.py:88-104,

@@ -341,18 +341,25 @@ __device__ __forceinline__ void row_quant_store(const RowArgs& a, int64_t row, b
   if constexpr (SR) sr_bits<16>(a.seed, (uint64_t)(row * N + c0), h);
   uint32_t w[4];
   if constexpr (KIND == K_INT8) {
-    const float qmin = (float)a.qmin, qmax = (float)a.qmax;
     int codes[16];
+    if constexpr (SR) {
+      // integer stochastic rounding on the 13-bit grid (sr_i8_pair)
+      const float lo = 1536.0f + (float)a.qmin, hi = 1536.0f + (float)a.qmax, base = 1536.0f + qp.zp;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      float x = round_dt<SDT>(m[j] * qp.inv);
-      int q = (int)__builtin_rintf(x) + (int)qp.zp;
-      if constexpr (SR) {
-        float xs = div_rn(m[j], qp.s, qp.rcp) + qp.zp;
-        q = sr_int(xs, q, h[j], qmin, qmax);
+      for (int j = 0; j < 16; j += 2) {
+        const uint32_t pr = sr_i8_pair(h[j], sr_i8_t(m[j], qp.rcp, base, lo, hi),
+                                       sr_i8_t(m[j + 1], qp.rcp, base, lo, hi), (65535u - h[j]) << 16,
+                                       (65535u - h[j + 1]) << 16);
+        codes[j] = (int)(int8_t)(pr & 0xffu);
+        codes[j + 1] = (int)(int8_t)((pr >> 16) & 0xffu);
       }
-      q = q < a.qmin ? a.qmin : (q > a.qmax ? a.qmax : q);
-      codes[j] = q;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float x = round_dt<SDT>(m[j] * qp.inv);
+        int q = (int)__builtin_rintf(x) + (int)qp.zp;
+        codes[j] = q < a.qmin ? a.qmin : (q > a.qmax ? a.qmax : q);
+      }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -623,12 +630,9 @@ __device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const uint4& 
   }
 }
 
-// `wide` (wave-uniform): some row of the wave has a scale above 2^100, where
-// the two-term reciprocal's low part would be subnormal (weights above 1e30);
-// those waves use the three-instruction quotient, exact for every normal scale.
 template <int KIND, bool SR>
 __device__ __forceinline__ void fast_quant_store(const RowArgs& a, const FastLane& L, bool rok, int mt,
-                                                 const RowQP& qp, const uint32_t (&w)[8], bool wide) {
+                                                 const RowQP& qp, const uint32_t (&w)[8]) {
   if (!rok) return;
   uint32_t nw[8];  // complemented Philox words: 65535 - h in each half
   if constexpr (SR) sr_nwords16_even(a.seed, L.ctr + 8u * (uint32_t)mt, nw);
@@ -636,41 +640,19 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, const FastLan
   if constexpr (KIND == K_INT8) {
     uint32_t y[16];
     if constexpr (SR) {
-      // Stochastic rounding of y = RN(m / s): q = floor(y) + [h * 2^-16 < frac(y)].
-      // With Y = 65536 y (exact) and T = ceil(Y), q = (T + 65535 - h) >> 16.
-      // Y is first clamped to [qmin, qmax] * 65536, which yields the bound for
-      // exactly the inputs the reference keeps at their (clamped) RTN code.
-      // The code byte is bit 16..23 of T + 65535 - h, picked by v_perm.
-      // RN(m / s) = RN(m hi + RN(m lo)) with 1/s = hi + lo (qp.inv, qp.rcp,
-      // scaled by 65536): m and s are bf16 values (8-bit significands), so m/s
-      // is representable or at least 2^-33 (relative) away from a rounding
-      // midpoint, far more than the ~2^-47 error of the two-term product.
-      const float lo16 = (float)a.qmin * 65536.0f, hi16 = (float)a.qmax * 65536.0f;
-      float y16[16];
-      if (!wide) {
+      // integer stochastic rounding on the 13-bit grid (sr_i8_pair): the
+      // complemented Philox word nw[i] holds 65535 - h of elements 2i (low
+      // half) and 2i + 1 (high half), which are the random operands' top bits
+      const float lo = 1536.0f + (float)a.qmin, hi = 1536.0f + (float)a.qmax;
+      uint32_t pr[8];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
-          y16[j] = __builtin_amdgcn_fmed3f(__builtin_fmaf(m, qp.inv, m * qp.rcp), lo16, hi16);
-        }
-      } else {
-        // q0 = m 65536 RN(1/s), e = m - q0 s / 65536 (exact), Y = q0 + e 65536 RN(1/s)
-        const float rs = qp.s * (1.0f / 65536.0f);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
-          const float q0 = m * qp.inv;
-          const float e = __builtin_fmaf(-q0, rs, m);
-          y16[j] = __builtin_amdgcn_fmed3f(__builtin_fmaf(e, qp.inv, q0), lo16, hi16);
-        }
+      for (int i = 0; i < 8; ++i) {
+        const float t0 = sr_i8_t(bf16_lo(w[i]), qp.rcp, 1536.0f, lo, hi);
+        const float t1 = sr_i8_t(bf16_hi(w[i]), qp.rcp, 1536.0f, lo, hi);
+        pr[i] = sr_i8_pair(w[i], t0, t1, nw[i] << 16, nw[i]);
       }
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint32_t tneg = (uint32_t)cvt_flr_neg(y16[j]);  // -ceil(Y)
-        y[j] = (j & 1) ? (nw[j >> 1] >> 16) - tneg : sub_lo16(nw[j >> 1], tneg);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) out[i] = pack_byte2s(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+      for (int i = 0; i < 4; ++i) out[i] = pack_sr_i8(pr[2 * i], pr[2 * i + 1]);
     } else {
       const float qmin = (float)a.qmin, qmax = (float)a.qmax;
 #pragma unroll
@@ -789,22 +771,14 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
     qp = int8_qparams<BF16, F32, false>(-mx, mx, a.qmin, a.qmax, stored, zp);
     if (writer) ((float*)a.scale_out)[row] = stored;
     if (writer && a.zp_out) a.zp_out[row] = 0;
-    if constexpr (SR) {
-      // 1/s as hi + lo: hi = RN(1/s), lo = (1 - s hi) hi (the fma residual is
-      // exact), together within ~2^-47 of 1/s; both scaled by 65536
-      const float lo = __builtin_fmaf(-qp.s, qp.rcp, 1.0f) * qp.rcp;
-      qp.inv = qp.rcp * 65536.0f;
-      qp.rcp = lo * 65536.0f;
-    }
   } else {
     qp = fp8_qparams<BF16, KIND>(mx, stored);
     if (writer) ((float*)a.scale_out)[row] = stored;
   }
-  const bool wide = KIND == K_INT8 && SR && __any(qp.s > 0x1p100f);
 #pragma unroll
   for (int i = 0; i < CACHE; ++i) {
     const int mt = wave + i * NW;
-    if (mt < ntiles) fast_quant_store<KIND, SR>(a, L, rok, mt, qp, cache[i], wide);
+    if (mt < ntiles) fast_quant_store<KIND, SR>(a, L, rok, mt, qp, cache[i]);
   }
 #pragma unroll
   for (int l = 0; l < LCACHE; ++l) {
@@ -812,7 +786,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
     if (mt < ntiles) {
       const lm_u32x4 lo = lcache[l][wave][0][lane], hi = lcache[l][wave][1][lane];
       const uint32_t t[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-      fast_quant_store<KIND, SR>(a, L, rok, mt, qp, t, wide);
+      fast_quant_store<KIND, SR>(a, L, rok, mt, qp, t);
     }
   }
   if (wave + (CACHE + LCACHE) * NW < ntiles) {
@@ -824,7 +798,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
       uint32_t t[8];
       float unused = 0.0f;
       fast_merged_tile<KIND, NKC>(a, cur.raw, cur.aop, bop, s_in, t, unused);
-      fast_quant_store<KIND, SR>(a, L, rok, mt, qp, t, wide);
+      fast_quant_store<KIND, SR>(a, L, rok, mt, qp, t);
       cur = nxt;
     }
   }
@@ -1107,9 +1081,12 @@ __device__ __forceinline__ void blk_store(const BlkArgs& a, int64_t row, int64_t
     blk[0] = (uint32_t)f16_bits(d);
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
-      float x = m[j] * id;
-      int q = (int)__builtin_roundf(x);
-      if constexpr (SR) q = sr_int(x, q, h[j], -127.0f, 127.0f);
+      int q = (int)__builtin_roundf(m[j] * id);
+      if constexpr (SR) {  // integer stochastic rounding on the 13-bit grid (sr_i8_pair)
+        const uint32_t pr = sr_i8_pair(h[j], sr_i8_t(m[j], id, 1536.0f, 1409.0f, 1663.0f), 1536.0f,
+                                       (65535u - h[j]) << 16, 0u);
+        q = (int)(int8_t)(pr & 0xffu);
+      }
       int bi = j + 2;
       if ((bi & 3) == 0) blk[bi >> 2] = 0u;
       blk[bi >> 2] |= ((uint32_t)q & 0xffu) << (8 * (bi & 3));

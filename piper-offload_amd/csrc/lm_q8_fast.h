@@ -145,18 +145,18 @@ DEV void q8_tile(const Q8Args& a, const Q8Raw& raw, const Q8Ops<NKC>& in, uint8_
   if constexpr (SR) {
     uint32_t nw[16];  // 65535 - h of element j in half (j & 1) of nw[j >> 1]
     sr_nwords_aligned<32>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4)), nw);
-    uint32_t y[32];
+    // integer stochastic rounding on the 13-bit grid (sr_i8_pair); pair i
+    // holds codes 2i and 2i + 1 in bytes 0 and 2
+    uint32_t pr[16];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      const float y16 = __builtin_amdgcn_fmed3f((m[j] * id) * 65536.0f, -127.0f * 65536.0f, 127.0f * 65536.0f);
-      const uint32_t tneg = (uint32_t)cvt_flr_neg(y16);  // -ceil(Y)
-      y[j] = (j & 1) ? (nw[j >> 1] >> 16) - tneg : sub_lo16(nw[j >> 1], tneg);
-    }
+    for (int i = 0; i < 16; ++i)
+      pr[i] = sr_i8_pair(nw[i], sr_i8_t(m[2 * i], id, 1536.0f, 1409.0f, 1663.0f),
+                         sr_i8_t(m[2 * i + 1], id, 1536.0f, 1409.0f, 1663.0f), nw[i] << 16, nw[i]);
     // code j is byte 2 + j of the block: word (j + 2) >> 2
-    ob[0] |= __builtin_amdgcn_perm(y[1], y[0], 0x06020000u) & 0xffff0000u;
+    ob[0] |= __builtin_amdgcn_perm(pr[0], pr[0], 0x06040c0cu);
 #pragma unroll
-    for (int k = 1; k < 8; ++k) ob[k] = pack_byte2s(y[4 * k - 2], y[4 * k - 1], y[4 * k], y[4 * k + 1]);
-    ob[8] = __builtin_amdgcn_perm(y[31], y[30], 0x0c0c0602u);
+    for (int k = 1; k < 8; ++k) ob[k] = pack_sr_i8(pr[2 * k - 1], pr[2 * k]);
+    ob[8] = __builtin_amdgcn_perm(pr[15], pr[15], 0x0c0c0200u);
   } else {
 #pragma unroll
     for (int j = 0; j < 32; ++j) {

@@ -106,3 +106,46 @@ def test_requant_streams_are_independent_of_target_and_merge_index() -> None:
     assert np.array_equal(q_again, runs[("a.weight", 0)])  # replay
     assert not np.array_equal(runs[("a.weight", 0)], runs[("a.weight", 1)])
     assert not np.array_equal(runs[("a.weight", 0)], runs[("b.weight", 0)])
+
+
+# ---- the integer rule on the 13-bit grid (INT8, Q8_0; gfx950 v_cvt_sr_f16_f32) ----
+def test_sr_int13_is_the_reference_rule_with_13_bit_u_and_p() -> None:
+    # on values with 13 fraction bits and s = 1, sr_int13 is the reference's
+    # selection (P/_triton_stochastic_quantization.py:25-40) with u = (h >> 3) 2^-13
+    rng = np.random.default_rng(3)
+    n = 200_000
+    y = (rng.integers(-130 * 8192, 130 * 8192, n) / 8192.0).astype(np.float32)
+    h = rng.integers(0, 65536, n).astype(np.uint32)
+    got = O.sr_int13(y, 1.0, 0.0, h, -128, 127)
+    det = np.clip(np.rint(y), -128, 127).astype(np.int32)
+    want = np.clip(O.sr_int(y, det, (h >> 3).astype(np.float32) / 8192.0, -128, 127), -128, 127)
+    assert np.array_equal(got, want)
+
+
+def test_sr_int13_up_probability_is_exactly_the_13_bit_fraction() -> None:
+    # over every 16-bit draw, the up-count of a fraction F * 2^-13 is exactly 8 F
+    h = np.arange(65536, dtype=np.uint32)
+    for frac13 in (0, 1, 2, 1000, 4096, 8191):
+        v = np.full(h.size, 3.0 + frac13 / 8192.0, np.float32)
+        up = O.sr_int13(v, 1.0, 0.0, h, -128, 127) - 3
+        assert set(np.unique(up).tolist()) <= {0, 1}
+        assert int(up.sum()) == 8 * frac13
+
+
+def test_sr_int13_neighbours_unbiased_and_clamped() -> None:
+    rng = np.random.default_rng(5)
+    n = 1_000_000
+    s = np.float32(0.00037)
+    v = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    rcp = np.float32(1.0) / s
+    h = O.sr_h16(O.derive_seed("sr13", 0), 0, n)
+    q = O.sr_int13(v, rcp, 0.0, h, -128, 127)
+    y = np.clip(v.astype(np.float64) / np.float64(s), -128, 127)
+    assert np.all((q == np.floor(y)) | (q == np.ceil(y)))
+    assert abs(float(np.mean(q - y))) < 2e-3
+    assert O.sr_int13(np.float32([1e30, -1e30, np.nan]), 1.0, 0.0, 12345, -128, 127).tolist() == [127, -128, -128]
+    assert O.sr_int13(np.float32([5.0, -7.0]), 1.0, 0.0, 0, -128, 127).tolist() == [5, -7]  # integers stay
+    # reduce_range and a zero point shift the grid, not the rule
+    # (h = 0 is u = 0: any fraction rounds up; h = 65535 is u = 8191 / 8192: only a fraction above it does)
+    assert O.sr_int13(np.float32([70.0, 10.25]), 1.0, np.float32([0.0, 3.0]), 0, -64, 63).tolist() == [63, 14]
+    assert O.sr_int13(np.float32([70.0, 10.25]), 1.0, np.float32([0.0, 3.0]), 65535, -64, 63).tolist() == [63, 13]
