@@ -25,8 +25,18 @@ kernels use, so a clean result needs no per-instruction table.  Branches are
 read in layout order; the asm helpers are straight-line code inside unrolled
 loop bodies, so the windows that matter are not split by a back edge.
 
+It also checks every vector-memory store of 12 or 16 bytes, compiler-emitted
+or not: no instruction may overwrite the store's data registers fewer than
+``STORE_NEED`` wait states after it.  Measured on gfx950, a VALU write to a
+data register of a 16-byte buffer store in the very next instruction corrupts
+what the store writes (the last lanes of each row of 16), and the compiler
+does not pad it.  (8-byte stores followed at once by such a write exist in
+kernels whose outputs are checked bit for bit, and never differed.)  A store
+that needs a guard gets one in the source: an ``s_nop 1`` in inline asm that
+takes the data registers as inputs, placed after the store.
+
 Exit status 1 and one line per finding when any asm instruction is inside an
-MFMA's window.
+MFMA's window or a store's data is overwritten too early.
 """
 
 from __future__ import annotations
@@ -36,6 +46,8 @@ import sys
 from pathlib import Path
 
 NEED = 19
+STORE_NEED = 2
+WIDE_STORE = re.compile(r"^(global|buffer|flat|scratch)_store_(dwordx[34]|b96|b128)\b")
 REG = re.compile(r"\bv\[(\d+):(\d+)\]|\bv(\d+)\b")
 FUNC = re.compile(r"^([A-Za-z_][\w.$]*):")
 NO_VGPR_DEF = ("v_cmp", "v_cmpx", "v_readlane", "v_readfirstlane")
@@ -54,13 +66,14 @@ def _regs(text: str) -> set[int]:
 def scan(path: Path) -> list[str]:
     findings: list[str] = []
     func, window, ws, in_asm = "?", [], 0, False
+    stores: list[dict] = []  # recent wide stores: data registers and issue position
     with open(path) as fh:
         for line in fh:
             line = line.rstrip("\n")
             st = line.strip()
             m = FUNC.match(line)
             if m:
-                func, window, ws = m.group(1), [], 0
+                func, window, ws, stores = m.group(1), [], 0, []
                 continue
             if st == ";;#ASMSTART":
                 in_asm = True
@@ -73,9 +86,20 @@ def scan(path: Path) -> list[str]:
                 continue
             op = s.split()[0]
             ws += int(s.split()[1], 0) + 1 if op == "s_nop" else 1
+            parts = s.split(None, 1)[1].split(",") if " " in s else [""]
+            # register defined by this instruction (VALU result or load destination)
+            if op.startswith(("v_", "global_load", "buffer_load", "flat_load", "scratch_load", "ds_read", "ds_load")):
+                written = set() if op.startswith(NO_VGPR_DEF) or " lds" in s else _regs(parts[0])
+                stores = [t for t in stores if ws - t["ws"] - 1 < STORE_NEED]
+                for t in stores:
+                    if written & t["data"]:
+                        findings.append(f"{path.name}: {func}: '{s}' overwrites the data of '{t['text']}' "
+                                        f"{ws - t['ws'] - 1} wait states after it")
+            if WIDE_STORE.match(op):
+                data = _regs(parts[0] if op.startswith("buffer") else (parts[1] if len(parts) > 1 else ""))
+                stores.append({"ws": ws, "data": data, "text": s})
             if not op.startswith("v_"):
                 continue
-            parts = s.split(None, 1)[1].split(",") if " " in s else [""]
             dst = set() if op.startswith(NO_VGPR_DEF) else _regs(parts[0])
             src = _regs(",".join(parts[1:]))
             if in_asm:
@@ -102,7 +126,8 @@ def main(argv: list[str]) -> int:
     findings = [f for p in paths for f in scan(p)]
     for f in findings:
         print(f)
-    print(f"check_asm_hazards: {len(paths)} files, {len(findings)} asm instructions inside an MFMA window")
+    print(f"check_asm_hazards: {len(paths)} files, {len(findings)} findings (asm inside an MFMA window, "
+          "store data overwritten early)")
     return 1 if findings else 0
 
 

@@ -62,6 +62,9 @@ def _int8_oracle(q: torch.Tensor, s: torch.Tensor, b, a, strength, seed, sr):  #
 @pytest.mark.parametrize("shapes", [[(64, 256), (40, 512), (128, 128), (16, 64)],   # fast kernel (N % 64 == 0)
                                     [(64, 256), (40, 14336), (16, 8192), (24, 4096)],  # + long rows (second launch)
                                     [(64, 256), (24, 96)],                           # generic kernel
+                                    # rows all 4096 wide (every tile in the register cache) with ragged
+                                    # last groups, more 16-row groups than workgroups resident at once
+                                    [(24, 4096), (8200, 4096), (40, 4096), (1000, 4096)],
                                     LAYER])                                          # one 8B layer at full size
 @pytest.mark.parametrize("sr", [False, True])
 def test_int8_stack_and_per_target_merges_equal_the_oracle(shapes, sr):
