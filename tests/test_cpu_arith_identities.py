@@ -1,7 +1,6 @@
-"""Exhaustive CPU checks of fp32 identities the HIP kernels use (tests/arith/identities.c):
-the two-instruction round-half-away of k_q8_fast and the two-instruction INT8
-stochastic-rounding quotient of k_rows_fast.  Each walks every input of its
-domain (2.5e9 floats, 4.6e8 bf16 pairs), about 10-15 s each."""
+"""Exhaustive CPU check of an fp32 identity the HIP kernels use (tests/arith/identities.c):
+the two-instruction round-half-away of k_q8_fast, over every input of its
+domain (2.5e9 floats, about 10-15 s)."""
 
 from __future__ import annotations
 
@@ -25,7 +24,7 @@ def binary(tmp_path_factory) -> str:
     return out
 
 
-@pytest.mark.parametrize("identity", ["round", "quotient"])
+@pytest.mark.parametrize("identity", ["round"])
 def test_identity_holds_on_its_whole_domain(binary: str, identity: str) -> None:
     r = subprocess.run([binary, identity], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
