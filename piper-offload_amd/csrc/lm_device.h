@@ -154,6 +154,13 @@ DEV float fp8_decode(uint32_t word, int byte) {
     }
   }
 }
+// bytes 2 HI and 2 HI + 1 of a word as fp32, in one v_cvt_pk_f32_fp8 / _bf8
+// (the same exact conversion as fp8_decode)
+template <int FMT, bool HI>
+DEV v2f32 fp8_decode_pair(uint32_t word) {
+  if constexpr (FMT == E4M3) return __builtin_amdgcn_cvt_pk_f32_fp8(word, HI);
+  else return __builtin_amdgcn_cvt_pk_f32_bf8(word, HI);
+}
 // pack 4 values (already clamped to the finite range) to 4 fp8 codes, RNE
 template <int FMT>
 DEV uint32_t fp8_pack4(float a, float b, float c, float d) {

@@ -23,10 +23,13 @@ static int fp8_common(const uint8_t* q, const float* scale, const void* dense, i
   if ((rc = check_lora(lora, M, N))) return rc;
   if ((rc = check_rounding(rnd))) return rc;
   if (!q_out || !scale_out) return fail(LM_EINVAL, "FP8 outputs must be non-null");
-  Ctx c;
-  if ((rc = setup(c, M, N, lora, ws, wsb, stream))) return rc;
   const int cd = lora ? lora->dtype : dense_dt;
   const bool sr = is_sr(rnd);
+  const bool split = !dense && group == N && lora &&
+                     rows_split_wanted(fmt == LM_E4M3 ? K_E4M3 : K_E5M2, cd, LM_F32, false, sr,
+                                       rpad_of(lora->rank) / 16, M, N);
+  Ctx c;
+  if ((rc = setup(c, M, N, lora, ws, wsb, stream, split))) return rc;
   if (group == N || group != M * N) {  // per-row, or per-group
     RowArgs a;
     memset(&a, 0, sizeof a);
@@ -41,6 +44,7 @@ static int fp8_common(const uint8_t* q, const float* scale, const void* dense, i
     a.N = N;
     a.strength = lora ? lora->strength : 0.0f;
     a.seed = seed_of(rnd);
+    a.red = split ? c.red : nullptr;
     if (group != N) {
       if (fmt == LM_E4M3) {
         if (dense) return run_groups<K_E4M3, true>(a, group, cd, LM_F32, false, sr, 0, c.st);

@@ -11,6 +11,10 @@
 //                 columns, keep merged bf16 values of up to CACHE macro tiles
 //                 in registers, reduce the row amax/min through LDS, then
 //                 quantize (recomputing tiles that did not fit the cache).
+//   k_rows_split: per-row INT8 / FP8 rows too long for a workgroup's
+//                 registers at rank above 32: an amax pass into per-row
+//                 workspace slots, then a pass that merges again and
+//                 quantizes, each over freely tiled 64-column tiles.
 //   k_blocks    : block-local formats (NVFP4 block 16, MX block 32, GGUF
 //                 Q8_0 block 32), dense bf16 weights, dequantize-to-dense,
 //                 and the two passes of per-tensor / two-level formats.
@@ -56,16 +60,20 @@ static inline int rpad_of(int rank) { return rank <= 0 ? 0 : (rank <= 16 ? 16 : 
 static inline int64_t npad_of(int64_t N) { return (N + 127) / 128 * 128; }
 static inline int64_t mpad_of(int64_t M) { return (M + 15) / 16 * 16; }
 
+// reduction slots: 64 words for the block formats' per-tensor passes, then
+// (for the two-pass long-row kernels) Mpad words of row amax bits and Mpad
+// copies of the input row scales
 struct WsLayout {
   size_t at_off, bp_off, red_off, total;
 };
+static inline int64_t red_words(int64_t M) { return 64 + 2 * mpad_of(M); }
 static WsLayout ws_layout(int64_t M, int64_t N, int rank) {
   WsLayout w;
   int rp = rpad_of(rank);
   w.at_off = 0;
   w.bp_off = align256((size_t)npad_of(N) * rp * 2);
   w.red_off = w.bp_off + align256((size_t)mpad_of(M) * rp * 2);
-  w.total = w.red_off + 256;
+  w.total = w.red_off + align256((size_t)red_words(M) * 4);
   return w;
 }
 
@@ -81,6 +89,7 @@ struct PrepItem {
   uint16_t* at;
   uint16_t* bp;
   uint32_t* red;
+  int64_t nred;        // leading words of red to clear: 64, or 64 + Mpad for the two-pass rows
   int64_t work_begin;  // prefix of per-item work units (k_prep1: 0)
   int64_t block_begin; // prefix of per-item k_prep_many workgroups
   int vec_b;           // B rows load 4 ranks at once (ldb, rank % 4 == 0, 8-byte aligned)
@@ -132,8 +141,10 @@ __device__ __forceinline__ void prep_unit(const PrepItem& it, int64_t u) {
     return;
   }
   u -= n_bp;
-  if (u == 0 && it.red) {
-    for (int i = 0; i < 64; ++i) ((LM_GLOBAL uint32_t*)it.red)[i] = 0u;
+  if (it.red) {  // unit u clears words [64 u, 64 u + 64) (nred is a multiple of 16)
+    LM_GLOBAL lm_u32x4* r = (LM_GLOBAL lm_u32x4*)it.red + 16 * u;
+    const int n4 = (int)((it.nred - 64 * u) >> 2) < 16 ? (int)((it.nred - 64 * u) >> 2) : 16;
+    for (int i = 0; i < n4; ++i) r[i] = lm_u32x4{0u, 0u, 0u, 0u};
   }
 }
 
@@ -143,7 +154,7 @@ static inline int prep_vec_b(const PrepItem& it) {
 }
 __host__ __device__ static inline int64_t prep_units(const PrepItem& it) {
   const int64_t npad = (it.N + 127) / 128 * 128, mpad = (it.M + 15) / 16 * 16;
-  return npad * it.rpad / 4 + mpad * it.rpad / 4 + 1;
+  return npad * it.rpad / 4 + mpad * it.rpad / 4 + (it.nred + 63) / 64;
 }
 
 static __global__ __launch_bounds__(256) void k_prep1(PrepItem it, int64_t total) {
@@ -208,6 +219,7 @@ struct RowArgs {
   float strength;
   int qmin, qmax;
   uint64_t seed;
+  uint32_t* red;         // two-pass long rows: the workspace reduction slots (null otherwise)
 };
 
 template <int KIND>
@@ -595,12 +607,9 @@ __device__ __forceinline__ void fast_load_tile(const FastLane& L, int mt, FastTi
   fast_load_aop<NKC>(L, mt, t.aop);
 }
 
-// merged bf16 pairs of one tile into out[8]; amax = max(amax, |merged|) in fp32
-template <int KIND, int NKC>
-__device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const uint4& raw, const v4i16 (&aop)[4][NKC],
-                                                 const v4i16 (&bop)[NKC], float s_in,
-                                                 uint32_t (&out)[8], float& amax) {
-  float d[16];
+// the 16 deltas of a lane's share of one 16 x 64 tile (4 MFMA chains)
+template <int NKC>
+__device__ __forceinline__ void fast_tile_delta(const v4i16 (&aop)[4][NKC], const v4i16 (&bop)[NKC], float (&d)[16]) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const v4f32 acc = mfma_chain<NKC, false>(aop[k], bop);
@@ -609,30 +618,57 @@ __device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const uint4& 
     d[4 * k + 2] = acc[2];
     d[4 * k + 3] = acc[3];
   }
+}
+// merged values of one tile before their bf16 rounding into m[16], given the
+// codes and deltas; with AMAX, amax = max(amax, |m|) (the maximum of the
+// bf16-rounded values is bf16r of it)
+template <int KIND, bool AMAX = true>
+__device__ __forceinline__ void fast_merge_vals(const RowArgs& a, const uint4& raw, const float (&d)[16], float s_in,
+                                                float (&m)[16], float& amax) {
   const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const uint32_t word = w[k >> 1];
-    const int b0 = (2 * k) & 3, b1 = (2 * k + 1) & 3;
     float x0, x1;
     if constexpr (KIND == K_INT8) {
       // signed byte -> fp32 is one sign-extending SDWA convert; RN(q * s)
+      const int b0 = (2 * k) & 3, b1 = (2 * k + 1) & 3;
       x0 = (float)(int8_t)(word >> (8 * b0)) * s_in;
       x1 = (float)(int8_t)(word >> (8 * b1)) * s_in;
     } else {
-      x0 = fp8_decode<FmtLimit<KIND>::fmt>(word, b0) * s_in;
-      x1 = fp8_decode<FmtLimit<KIND>::fmt>(word, b1) * s_in;
+      const v2f32 c = (k & 1) ? fp8_decode_pair<FmtLimit<KIND>::fmt, true>(word)
+                              : fp8_decode_pair<FmtLimit<KIND>::fmt, false>(word);
+      x0 = c.x * s_in;
+      x1 = c.y * s_in;
     }
-    const float m0 = __builtin_fmaf(d[2 * k], a.strength, bf16r(x0));
-    const float m1 = __builtin_fmaf(d[2 * k + 1], a.strength, bf16r(x1));
-    out[k] = pack_bf16x2(m0, m1);
-    amax = max3_abs(amax, m0, m1);
+    m[2 * k] = __builtin_fmaf(d[2 * k], a.strength, bf16r(x0));
+    m[2 * k + 1] = __builtin_fmaf(d[2 * k + 1], a.strength, bf16r(x1));
+    if constexpr (AMAX) amax = max3_abs(amax, m[2 * k], m[2 * k + 1]);
   }
 }
+template <int KIND, int NKC, bool AMAX = true>
+__device__ __forceinline__ void fast_merged_f32(const RowArgs& a, const uint4& raw, const v4i16 (&aop)[4][NKC],
+                                                const v4i16 (&bop)[NKC], float s_in, float (&m)[16], float& amax) {
+  float d[16];
+  fast_tile_delta<NKC>(aop, bop, d);
+  fast_merge_vals<KIND, AMAX>(a, raw, d, s_in, m, amax);
+}
+// merged bf16 pairs of one tile into out[8]; amax = max(amax, |merged|) in fp32
+template <int KIND, int NKC>
+__device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const uint4& raw, const v4i16 (&aop)[4][NKC],
+                                                 const v4i16 (&bop)[NKC], float s_in,
+                                                 uint32_t (&out)[8], float& amax) {
+  float m[16];
+  fast_merged_f32<KIND, NKC>(a, raw, aop, bop, s_in, m, amax);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) out[k] = pack_bf16x2(m[2 * k], m[2 * k + 1]);
+}
 
+// quantize and store one tile given its bf16-valued merged values m[16];
+// old[i] is any register the INT8 stochastic path may overwrite for pair i
 template <int KIND, bool SR>
-__device__ __forceinline__ void fast_quant_store(const RowArgs& a, const FastLane& L, bool rok, int mt,
-                                                 const RowQP& qp, const uint32_t (&w)[8]) {
+__device__ __forceinline__ void fast_quant_store_vals(const RowArgs& a, const FastLane& L, bool rok, int mt,
+                                                      const RowQP& qp, const float (&m)[16], const uint32_t (&old)[8]) {
   if (!rok) return;
   uint32_t nw[8];  // complemented Philox words: 65535 - h in each half
   if constexpr (SR) sr_nwords16_even(a.seed, L.ctr + 8u * (uint32_t)mt, nw);
@@ -647,9 +683,9 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, const FastLan
       uint32_t pr[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float t0 = sr_i8_t(bf16_lo(w[i]), qp.rcp, 1536.0f, lo, hi);
-        const float t1 = sr_i8_t(bf16_hi(w[i]), qp.rcp, 1536.0f, lo, hi);
-        pr[i] = sr_i8_pair(w[i], t0, t1, nw[i] << 16, nw[i]);
+        const float t0 = sr_i8_t(m[2 * i], qp.rcp, 1536.0f, lo, hi);
+        const float t1 = sr_i8_t(m[2 * i + 1], qp.rcp, 1536.0f, lo, hi);
+        pr[i] = sr_i8_pair(old[i], t0, t1, nw[i] << 16, nw[i]);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) out[i] = pack_sr_i8(pr[2 * i], pr[2 * i + 1]);
@@ -657,8 +693,7 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, const FastLan
       const float qmin = (float)a.qmin, qmax = (float)a.qmax;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
-        const float x = __builtin_amdgcn_fmed3f(m * qp.inv, qmin, qmax);
+        const float x = __builtin_amdgcn_fmed3f(m[j] * qp.inv, qmin, qmax);
         y[j] = f2u(x + 12582912.0f);  // low byte = rint(x) (two's complement)
       }
 #pragma unroll
@@ -669,10 +704,7 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, const FastLan
     constexpr int F = FmtLimit<KIND>::fmt;
     float x[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float m = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
-      x[j] = __builtin_amdgcn_fmed3f(div_rn(m, qp.s, qp.rcp), -L8, L8);
-    }
+    for (int j = 0; j < 16; ++j) x[j] = __builtin_amdgcn_fmed3f(div_rn(m[j], qp.s, qp.rcp), -L8, L8);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if constexpr (SR) out[i] = sr_fp8_nword<F>(x + 4 * i, nw + 2 * i);
@@ -680,6 +712,18 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, const FastLan
     }
   }
   *(LM_GLOBAL lm_u32x4*)(L.out + (uint32_t)(mt * 64) + L.off) = lm_u32x4{out[0], out[1], out[2], out[3]};
+}
+// the same from the packed bf16 pairs w[8] of a cached tile
+template <int KIND, bool SR>
+__device__ __forceinline__ void fast_quant_store(const RowArgs& a, const FastLane& L, bool rok, int mt,
+                                                 const RowQP& qp, const uint32_t (&w)[8]) {
+  float m[16];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    m[2 * i] = bf16_lo(w[i]);
+    m[2 * i + 1] = bf16_hi(w[i]);
+  }
+  fast_quant_store_vals<KIND, SR>(a, L, rok, mt, qp, m, w);
 }
 
 // Tiles of A^T operands a wave keeps in flight ahead of the arithmetic (the
@@ -824,6 +868,121 @@ __global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_row
   }
   const RowArgs a = items[lo].a;
   rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_, LCACHE>(a, (t - items[lo].tile_begin) * 16);
+}
+
+// ---- long rows in two passes ------------------------------------------------
+// A workgroup that owns whole rows has to hold their merged values between
+// the row reduction and the requant; for rows of more than 8192 merged
+// values per 16-row group and rank above 32 that cache fills the register
+// file (one workgroup per CU) and the kernel waits on memory with its phases
+// serialized.  k_rows_split instead tiles the weight freely and runs twice:
+//   pass 1 (QUANT = false): merge, reduce max |bf16(merged)| per row, fold it
+//           into the row's slot of red with an atomic max (non-negative floats
+//           order like their bits; prep cleared the slots), and copy the input
+//           row scales into the workspace;
+//   pass 2 (QUANT = true):  recompute the same merged values from the codes,
+//           derive the row's qparams from the slot, quantize and store.
+// Pass 2 reads the input scales from the workspace copy, so outputs may alias
+// inputs (a workgroup of one column range may overwrite the row scale while
+// another still needs it).  Both passes address codes, A^T operands and
+// Philox counters exactly as k_rows_fast does, so results are bit-identical.
+// A wave covers RB 16-row blocks (they share each tile's A^T operands) and
+// TPW consecutive 64-column tiles; SPLIT_NW waves per workgroup take
+// consecutive tile ranges of the same rows.
+static constexpr int SPLIT_NW = 4;
+template <int KIND, bool SR, int NKC, int RB, int TPW, bool QUANT>
+__global__ __launch_bounds__(SPLIT_NW * 64) void k_rows_split(RowArgs a, int wg_per_group) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
+  const int ntiles = (int)(a.N >> 6);
+  const int64_t grp = blockIdx.x / wg_per_group;
+  const int t0 = ((int)(blockIdx.x - grp * wg_per_group) * SPLIT_NW + wave) * TPW;
+  if (t0 >= ntiles) return;  // wave-uniform; the kernel has no barrier
+  const int64_t mpad = (a.M + 15) / 16 * 16;
+  LM_GLOBAL uint32_t* rmax = (LM_GLOBAL uint32_t*)a.red + 64;
+  LM_GLOBAL float* s_copy = (LM_GLOBAL float*)(rmax + mpad);
+  FastLane L[RB];
+  v4i16 bop[RB][NKC];
+  float s_in[RB], amax[RB];
+  bool rok[RB];
+  int64_t row[RB];
+  RowQP qp[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    row[rb] = grp * (16 * RB) + 16 * rb + rl;
+    rok[rb] = row[rb] < a.M;
+    // rows past M work on row M-1 (valid memory) and never store
+    const int64_t rowc = rok[rb] ? row[rb] : a.M - 1;
+    L[rb] = fast_lane<NKC>(a, rowc, lane);
+    load_bop<NKC>(a.bp, rowc, lane, bop[rb]);
+    amax[rb] = 0.0f;
+    if constexpr (QUANT) {
+      s_in[rb] = s_copy[rowc];
+      const float mx = u2f(rmax[rowc]);
+      const bool writer = t0 == 0 && (lane >> 4) == 0 && rok[rb];  // one scale store per row
+      float stored;
+      if constexpr (KIND == K_INT8) {
+        int zp;
+        qp[rb] = int8_qparams<BF16, F32, false>(-mx, mx, a.qmin, a.qmax, stored, zp);
+        if (writer && a.zp_out) a.zp_out[row[rb]] = 0;
+      } else {
+        qp[rb] = fp8_qparams<BF16, KIND>(mx, stored);
+      }
+      if (writer) ((float*)a.scale_out)[row[rb]] = stored;
+    } else {
+      s_in[rb] = ((const LM_GLOBAL float*)a.scale)[rowc];
+    }
+  }
+  // one tile: the deltas of every row block first (the MFMAs consume the A^T
+  // operands), then the next tile's operands and codes are requested, then
+  // the merge / requant arithmetic of this tile hides their latency
+  v4i16 aop[4][NKC];
+  uint4 raw[RB];
+  auto load = [&](int mt) {
+    fast_load_aop<NKC>(L[0], mt, aop);  // A^T offsets depend on the lane only
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) raw[rb] = fast_load_codes(L[rb], mt);
+  };
+  auto tile = [&](int mt, int next) {
+    float d[RB][16];
+    uint4 cur[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      fast_tile_delta<NKC>(aop, bop[rb], d[rb]);
+      cur[rb] = raw[rb];
+    }
+    if (next >= 0) load(next);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      float m[16];
+      fast_merge_vals<KIND, !QUANT>(a, cur[rb], d[rb], s_in[rb], m, amax[rb]);
+      if constexpr (QUANT) {
+        uint32_t old[8];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) m[j] = bf16r(m[j]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) old[i] = f2u(m[2 * i]);
+        fast_quant_store_vals<KIND, SR>(a, L[rb], rok[rb], mt, qp[rb], m, old);
+      }
+    }
+  };
+  load(t0);
+  if (t0 + TPW <= ntiles) {
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) tile(t0 + i, i + 1 < TPW ? t0 + i + 1 : -1);
+  } else {
+    for (int mt = t0; mt < ntiles; ++mt) tile(mt, mt + 1 < ntiles ? mt + 1 : -1);
+  }
+  if constexpr (!QUANT) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      float vmx = bf16r(amax[rb]);  // = max |bf16(merged)| of the lane
+      vmx = lanes_max32(lanes_max16(vmx));
+      if ((lane >> 4) == 0 && rok[rb]) {
+        atomicMax((uint32_t*)(rmax + row[rb]), f2u(vmx));
+        if (t0 == 0) s_copy[row[rb]] = s_in[rb];
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1318,7 +1477,10 @@ static inline int check_lora(const lm_lora* l, int64_t M, int64_t N) {
   return LM_OK;
 }
 
-static inline int setup(Ctx& c, int64_t M, int64_t N, const lm_lora* l, void* ws, size_t wsb, void* stream) {
+// rows_split: the call runs the two-pass long-row kernels, whose row amax
+// slots the prep launch clears
+static inline int setup(Ctx& c, int64_t M, int64_t N, const lm_lora* l, void* ws, size_t wsb, void* stream,
+                        bool rows_split = false) {
   c.st = (hipStream_t)stream;
   const int rank = l ? l->rank : 0;
   WsLayout w = ws_layout(M, N, rank);
@@ -1342,6 +1504,7 @@ static inline int setup(Ctx& c, int64_t M, int64_t N, const lm_lora* l, void* ws
   it.at = c.at;
   it.bp = c.bp;
   it.red = c.red;
+  it.nred = rows_split ? 64 + mpad_of(M) : 64;
   it.work_begin = 0;
   it.block_begin = 0;
   it.vec_b = prep_vec_b(it);
@@ -1509,9 +1672,47 @@ static int launch_rows_fast(const RowArgs& a, hipStream_t st) {
   return LM_OK;
 }
 
+// Two-pass long rows (k_rows_split): wave tiles of 16 RB rows x 64 TPW
+// columns.  The amax pass has little arithmetic per A^T operand and shares
+// each tile's operands among 8 row blocks (128 rows); the quant pass, which
+// holds the Philox state and the quantized words as well, among 4.  Measured
+// on MI355X, FP8 [8192, 8192] rank 64, stochastic: amax pass 28.6 us at
+// RB 8 (30.4 at RB 4, 42 at RB 2); quant pass 53.9 us at RB 4, TPW 8 (56.3 at
+// RB 2, 58.3 without the one-tile operand prefetch).
+static constexpr int SPLIT_RB1 = 8, SPLIT_TPW1 = 8, SPLIT_RB2 = 4, SPLIT_TPW2 = 8;
+// whether a per-row merge runs the two-pass kernels: rows too long for the
+// register cache at rank above 32, where the cached kernel runs one
+// workgroup per CU
+static inline bool rows_split_wanted(int kind, int cd, int sdt, bool asym, bool sr, int nkc, int64_t M, int64_t N) {
+  return rows_fast_ok(kind, cd, sdt, asym, nkc, M, N) && nkc == 4 && rows_long_mode(nkc, sr, N) == ROWS_DEEP;
+}
+template <int KIND, bool SR, int NKC, int RB, int TPW, bool QUANT>
+static int launch_rows_split_pass(const RowArgs& a, hipStream_t st) {
+  const int64_t waves = (a.N / 64 + TPW - 1) / TPW;
+  const int64_t wg_per_group = (waves + SPLIT_NW - 1) / SPLIT_NW;
+  const int64_t groups = (a.M + 16 * RB - 1) / (16 * RB);
+  if (groups * wg_per_group > 0x7fffffff) return fail(LM_EUNSUPPORTED, "weight too large for one row launch");
+  {
+    TimedLaunch timed("rows", st);
+    hipLaunchKernelGGL((k_rows_split<KIND, SR, NKC, RB, TPW, QUANT>), dim3((unsigned)(groups * wg_per_group)),
+                       dim3(SPLIT_NW * 64), 0, st, a, (int)wg_per_group);
+  }
+  LAUNCH_CHECK();
+  return LM_OK;
+}
+template <int KIND, bool SR, int NKC>
+static int launch_rows_split(const RowArgs& a, hipStream_t st) {
+  const int rc = launch_rows_split_pass<KIND, SR, NKC, SPLIT_RB1, SPLIT_TPW1, false>(a, st);
+  return rc ? rc : launch_rows_split_pass<KIND, SR, NKC, SPLIT_RB2, SPLIT_TPW2, true>(a, st);
+}
+
 template <int KIND, bool FROM_DENSE>
 static int run_rows(const RowArgs& a, int cd, int sdt, bool asym, bool sr, int nkc, hipStream_t st) {
   if (!FROM_DENSE && rows_fast_ok(KIND, cd, sdt, asym, nkc, a.M, a.N)) {
+    if (a.red) {  // the caller chose the two-pass kernels (rows_split_wanted: rank bucket 64) and had prep clear the slots
+      if (nkc_bucket(nkc) != 4) return fail(LM_EINVAL, "two-pass rows need the rank-64 bucket");
+      return sr ? launch_rows_split<KIND, true, 4>(a, st) : launch_rows_split<KIND, false, 4>(a, st);
+    }
     if (sr) {
       NKC_SWITCH(nkc_bucket(nkc), return (launch_rows_fast<KIND, true, NKC_>(a, st)));
     } else {

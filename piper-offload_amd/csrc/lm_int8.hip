@@ -25,10 +25,12 @@ static int int8_common(const int8_t* q, const void* scale, const int8_t* zp, con
   if ((rc = check_lora(lora, M, N))) return rc;
   if ((rc = check_rounding(rnd))) return rc;
   if (!q_out || !scale_out) return fail(LM_EINVAL, "INT8 outputs must be non-null");
-  Ctx c;
-  if ((rc = setup(c, M, N, lora, ws, wsb, stream))) return rc;
   const int cd = lora ? lora->dtype : dense_dt;
   const bool sr = is_sr(rnd);
+  const bool split = !dense && group == N && lora &&
+                     rows_split_wanted(K_INT8, cd, sdt, asym != 0, sr, rpad_of(lora->rank) / 16, M, N);
+  Ctx c;
+  if ((rc = setup(c, M, N, lora, ws, wsb, stream, split))) return rc;
   const int qmin = reduce_range ? -64 : -128, qmax = reduce_range ? 63 : 127;
   if (group == N || group != M * N) {  // per-row, or per-group
     RowArgs a;
@@ -48,6 +50,7 @@ static int int8_common(const int8_t* q, const void* scale, const int8_t* zp, con
     a.qmin = qmin;
     a.qmax = qmax;
     a.seed = seed_of(rnd);
+    a.red = split ? c.red : nullptr;
     if (group != N) {
       if (dense) return run_groups<K_INT8, true>(a, group, cd, sdt, asym != 0, sr, 0, c.st);
       return run_groups<K_INT8, false>(a, group, cd, sdt, asym != 0, sr, c.nkc, c.st);

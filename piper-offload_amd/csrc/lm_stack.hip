@@ -30,6 +30,7 @@ static int stack_layout(const lm_stack_item* items, int32_t count, void* ws, siz
     p.at = (uint16_t*)(base + cursor + w.at_off);
     p.bp = (uint16_t*)(base + cursor + w.bp_off);
     p.red = (uint32_t*)(base + cursor + w.red_off);
+    p.nred = 64;
     p.vec_b = prep_vec_b(p);
     cursor += w.total;
   }
@@ -109,6 +110,7 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
     a.qmin = -128;
     a.qmax = 127;
     a.seed = s.seed;
+    a.red = nullptr;
     r.tile_begin = tiles[grp];
     tiles[grp] += (s.M + 15) / 16;
   }

@@ -64,11 +64,12 @@ def int8_initial(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return q, scale
 
 
-def fp8_initial(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Per-row amax/448 fp32 encode to e4m3fn."""
+def fp8_initial(w: torch.Tensor, fp8: torch.dtype = torch.float8_e4m3fn) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row amax/limit fp32 encode to e4m3fn (limit 448) or e5m2 (57344)."""
+    limit = float(torch.finfo(fp8).max)
     wf = w.float()
-    scale = (wf.abs().amax(dim=1, keepdim=True) / 448.0).clamp_min(torch.finfo(torch.float32).eps)
-    q = (wf / scale).clamp(-448, 448).to(torch.float8_e4m3fn)
+    scale = (wf.abs().amax(dim=1, keepdim=True) / limit).clamp_min(torch.finfo(torch.float32).eps)
+    q = (wf / scale).clamp(-limit, limit).to(fp8)
     return q, scale
 
 

@@ -60,6 +60,34 @@ def test_fp8_fused_equals_requant_of_gpu_dense(shape, rank, strength, sr):
     assert np.array_equal(os_.cpu().numpy().reshape(-1), rs)
 
 
+# two-pass long rows (rank above 32, rows of more than 4096 columns): rows that
+# end inside a 64-row wave tile, a column count that leaves the last wave of a
+# row a partial tile range, and the same merge in place (outputs aliasing the
+# inputs, so the row scales are overwritten while other column ranges still
+# need them)
+@pytest.mark.parametrize("shape,rank", [((70, 8256), 64), ((130, 4160), 48), ((16, 12288), 64)])
+@pytest.mark.parametrize("fp8", [torch.float8_e4m3fn, torch.float8_e5m2])
+@pytest.mark.parametrize("sr", [False, True])
+def test_fp8_two_pass_rows_and_in_place(shape, rank, fp8, sr):
+    rows, cols = shape
+    w = normal_bf16(shape, 0.02, 11)
+    q, s = fp8_initial(w, fp8)
+    b, a = lora_factors(rows, cols, rank, 12)
+    qd, sd, bd, ad = q.to(DEV), s.to(DEV), b.to(DEV), a.to(DEV)
+    dense = K.dequantize_float8(qd, sd, (1, cols), lora=(bd, ad, 0.75))
+    obase = O.fp8_dequant(u8_np(q), s.numpy(), cols, fmt=FMT[fp8])
+    assert_merged_close(bf16_np(dense), O.merge_dense(obase, bf16_np(b), bf16_np(a), 0.75), obase)
+    seed = derive_seed("fp8.two-pass", rows) if sr else None
+    oq, os_ = K.merge_float8_lora(qd, sd, (1, cols), bd, ad, 0.75, rounding_seed=seed)
+    rq, rs = O.fp8_requant(bf16_np(dense), cols, fmt=FMT[fp8], sr_mode=O.SR_PHILOX8 if sr else O.SR_OFF,
+                           seed=seed or 0)
+    assert np.array_equal(u8_np(oq), rq)
+    assert np.array_equal(os_.cpu().numpy().reshape(-1), rs)
+    K.merge_float8_lora_into(qd, sd, (1, cols), bd, ad, 0.75, rounding_seed=seed, out_qdata=qd, out_scale=sd)
+    assert np.array_equal(u8_np(qd), rq)
+    assert np.array_equal(sd.cpu().numpy().reshape(-1), rs)
+
+
 def test_fp8_per_tensor_and_adapter_in_place():
     rows, cols, rank = 32, 512, 16
     w = normal_bf16((rows, cols), 0.02, 1)

@@ -121,6 +121,28 @@ def test_int8_fused_equals_requant_of_gpu_dense(shape, rank, strength, sr, scale
     assert not oz.any()
 
 
+# two-pass long rows (rank above 32, rows of more than 4096 columns): rows that
+# end inside a 64-row wave tile and a partial last tile range, merged out of
+# place and then in place (outputs aliasing the inputs)
+@pytest.mark.parametrize("shape,rank", [((70, 8256), 64), ((130, 4160), 48)])
+@pytest.mark.parametrize("sr", [False, True])
+def test_int8_two_pass_rows_and_in_place(shape, rank, sr):
+    rows, cols = shape
+    q, s, b, a = _int8_case(rows, cols, rank, seed=21)
+    qd, sd, bd, ad = q.to(DEV), s.to(DEV), b.to(DEV), a.to(DEV)
+    seed = derive_seed("int8.two-pass", rows) if sr else None
+    dense = K.dequantize_int8(qd, sd, None, (1, cols), lora=(bd, ad, 0.5))
+    rq, rs, _ = O.int8_requant(bf16_np(dense), cols, sr_mode=O.SR_PHILOX8 if sr else O.SR_OFF, seed=seed or 0)
+    oq, os_, oz = K.merge_int8_lora(qd, sd, None, (1, cols), bd, ad, 0.5, asymmetric=False, reduce_range=False,
+                                    rounding_seed=seed)
+    assert np.array_equal(oq.cpu().numpy(), rq)
+    assert np.array_equal(_scale_np(os_), rs)
+    K.merge_int8_lora_into(qd, sd, None, (1, cols), bd, ad, 0.5, asymmetric=False, reduce_range=False,
+                           rounding_seed=seed, out_qdata=qd, out_scale=sd, out_zero_point=None)
+    assert np.array_equal(qd.cpu().numpy(), rq)
+    assert np.array_equal(_scale_np(sd), rs)
+
+
 def test_int8_fused_vs_oracle_pipeline():
     rows, cols, rank = 64, 4096, 32
     q, s, b, a = _int8_case(rows, cols, rank)
