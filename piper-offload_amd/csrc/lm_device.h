@@ -29,6 +29,9 @@ typedef uint32_t lm_u32x4 __attribute__((ext_vector_type(4)));
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef _Float16 v4f16 __attribute__((ext_vector_type(4)));
 typedef float v4f32 __attribute__((ext_vector_type(4)));
+typedef short v8i16 __attribute__((ext_vector_type(8)));
+typedef _Float16 v8f16 __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf16 __attribute__((ext_vector_type(8)));
 
 namespace lm {
 
@@ -559,16 +562,33 @@ DEV uint32_t mx_scale(float max_abs, int mode, int emax, float maxpos, int mbits
 // SPAN*(l >> 4).  The MFMA computes D^T (positions x rows): position p of
 // MFMA t maps to column SPAN*(p >> 2) + 4t + (p & 3), so the four fp32
 // results of MFMA t in lane l are columns SPAN*(l>>4) + 4t + 0..3.
+// Rank above 16: chunks kc = 2h and 2h + 1 go to one 16x16x32 MFMA, which
+// gfx950 issues at the rate of one 16x16x16 (twice the work per cycle).  Its
+// lane group g supplies k slots 8g..8g+7; the operand words hold
+// k = 32h + 4g + 0..3 and 32h + 16 + 4g + 0..3 there, for A and B alike, so
+// the slot-to-k map is the same on both sides and the sum covers the 32 k
+// of the pair.
 template <int NKC, bool F16>
 DEV v4f32 mfma_chain(const v4i16 (&a)[NKC], const v4i16 (&b)[NKC]) {
   v4f32 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int kc = 0; kc < NKC; ++kc) {
+  if constexpr (NKC == 1) {
     if constexpr (F16)
-      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4f16, a[kc]), __builtin_bit_cast(v4f16, b[kc]),
-                                                  acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4f16, a[0]), __builtin_bit_cast(v4f16, b[0]), acc,
+                                                  0, 0, 0);
     else
-      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a[kc], b[kc], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a[0], b[0], acc, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int h = 0; h < NKC / 2; ++h) {
+      const v8i16 av = __builtin_shufflevector(a[2 * h], a[2 * h + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+      const v8i16 bv = __builtin_shufflevector(b[2 * h], b[2 * h + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+      if constexpr (F16)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8f16, av), __builtin_bit_cast(v8f16, bv), acc,
+                                                     0, 0, 0);
+      else
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf16, av), __builtin_bit_cast(v8bf16, bv),
+                                                      acc, 0, 0, 0);
+    }
   }
   return acc;
 }
