@@ -45,6 +45,7 @@ _F = ctypes.c_float
 
 _SIGS = {
     "lmo_philox4x32": (None, [_P, ctypes.c_uint32, ctypes.c_uint32, _I, _P]),
+    "lmo_sr_rounds": (_I, []),
     "lmo_uniforms": (None, [_I, _U64, _U64, _I64, _P]),
     "lmo_merge_dense": (None, [_P, _P, _I, _I64, _I64, _P, _I64, _P, _I64, _I, _I, _F, _I]),
     "lmo_routed_residual": (None, [_P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P, _P]),
@@ -204,6 +205,11 @@ def philox4x32(ctr: tuple[int, int, int, int], key: tuple[int, int], rounds: int
     out = np.empty(4, np.uint32)
     load().lmo_philox4x32(_p(c), key[0], key[1], rounds, _p(out))
     return tuple(int(v) for v in out)
+
+
+def sr_rounds() -> int:
+    """Philox rounds of the SR_PHILOX8 stream (the HIP kernels' SR_ROUNDS)."""
+    return int(load().lmo_sr_rounds())
 
 
 def uniforms(seed: int, start: int, n: int, mode: int = SR_PHILOX8) -> np.ndarray:

@@ -17,7 +17,7 @@
  *   - merged = round_cd(fmaf(delta, strength, base))
  *     (P/_triton_int8_lora.py:89-93);
  *   - stochastic rounding draws u = k * 2^-16 with k the 16-bit half-word
- *     (idx & 7) of Philox4x32-10(ctr = (idx >> 3, 0, 0), key = seed), or the
+ *     (idx & 7) of Philox4x32-7(ctr = (idx >> 3, 0, 0), key = seed), or the
  *     Triton tl.rand stream (P/_triton_stochastic_quantization.py:19-22) in
  *     compatibility mode.
  *
@@ -188,6 +188,11 @@ EXPORT void lmo_philox4x32(const uint32_t* ctr, uint32_t k0, uint32_t k1, int ro
   memcpy(out, c, 16);
 }
 
+/* Rounds of the SR_PHILOX8 stream: Random123's Philox4x32-7 (published
+ * known answers in tests/golden/kat.json; the HIP kernels' SR_ROUNDS). */
+#define SR_PHILOX_ROUNDS 7
+EXPORT int lmo_sr_rounds(void) { return SR_PHILOX_ROUNDS; }
+
 /* Uniform for the element at logical offset idx.
  * SR_PHILOX8: one Philox call per 8 consecutive offsets, 16 bits each.
  * SR_TRITON : triton tl.rand(seed, idx) (uint_to_uniform_float of word 0). */
@@ -202,7 +207,7 @@ static inline float sr_uniform(int mode, uint64_t seed, uint64_t idx) {
   }
   uint64_t g = idx >> 3;
   uint32_t c[4] = {(uint32_t)g, (uint32_t)(g >> 32), 0, 0};
-  philox4x32(c, k0, k1, 10);
+  philox4x32(c, k0, k1, SR_PHILOX_ROUNDS);
   int j = (int)(idx & 7);
   uint32_t w = c[j >> 1];
   uint32_t h = (j & 1) ? (w >> 16) : (w & 0xffffu);
@@ -229,7 +234,7 @@ static inline uint32_t sr_h16(uint64_t seed, uint64_t idx) {
   uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
   uint64_t g = idx >> 3;
   uint32_t c[4] = {(uint32_t)g, (uint32_t)(g >> 32), 0, 0};
-  philox4x32(c, k0, k1, 10);
+  philox4x32(c, k0, k1, SR_PHILOX_ROUNDS);
   int j = (int)(idx & 7);
   uint32_t w = c[j >> 1];
   return (j & 1) ? (w >> 16) : (w & 0xffffu);

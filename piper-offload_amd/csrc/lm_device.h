@@ -206,8 +206,14 @@ DEV float e8m0_value(uint32_t c) {
   return u2f(c << 23);
 }
 
-// ---- Philox4x32-10 (Random123; triton.language.random.philox_impl) -----
-DEV void philox10(uint64_t ctr, uint64_t seed, uint32_t (&c)[4]) {
+// ---- Philox4x32-7: the stochastic-rounding stream ----------------------
+// Random123's Philox4x32 (the round function of
+// triton.language.random.philox_impl) with 7 rounds, the smallest count its
+// authors report free of TestU01 BigCrush failures (Salmon et al., SC'11,
+// "Parallel random numbers: as easy as 1, 2, 3"); Random123 publishes
+// known-answer vectors for it.  Triton's default is 10 rounds.
+constexpr int SR_ROUNDS = 7;
+DEV void philox_sr(uint64_t ctr, uint64_t seed, uint32_t (&c)[4]) {
   c[0] = (uint32_t)ctr;
   c[1] = (uint32_t)(ctr >> 32);
   c[2] = 0;
@@ -216,7 +222,7 @@ DEV void philox10(uint64_t ctr, uint64_t seed, uint32_t (&c)[4]) {
   // One round: both halves of each 32x32 product come from one v_mad_u64_u32
   // and each output word is one v_bitop3_b32 (0x96 = a ^ b ^ c).
 #pragma unroll
-  for (int r = 0; r < 10; ++r) {
+  for (int r = 0; r < SR_ROUNDS; ++r) {
     const uint64_t pb = (uint64_t)c[2] * 0xCD9E8D57u;
     const uint64_t pa = (uint64_t)c[0] * 0xD2511F53u;
     c[0] = __builtin_amdgcn_bitop3_b32((uint32_t)(pb >> 32), c[1], k0, 0x96);
@@ -227,22 +233,22 @@ DEV void philox10(uint64_t ctr, uint64_t seed, uint32_t (&c)[4]) {
     k1 += 0xBB67AE85u;
   }
 }
-// Philox4x32-10 of the counter (lo, hi) with output words 0 and 2
+// philox_sr of the counter (lo, hi) with output words 0 and 2
 // complemented: the last round's three-way XOR of those words becomes an
 // XNOR (v_bitop3_b32 0x69), so the complement costs nothing.  The stochastic
 // rounding rules below consume 65535 - h = ~h (16 bits), i.e. complemented
 // words.
-DEV void philox10_n02(uint32_t lo, uint32_t hi, uint64_t seed, uint32_t (&c)[4]) {
+DEV void philox_sr_n02(uint32_t lo, uint32_t hi, uint64_t seed, uint32_t (&c)[4]) {
   c[0] = lo;
   c[1] = hi;
   c[2] = 0;
   c[3] = 0;
   uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
 #pragma unroll
-  for (int r = 0; r < 10; ++r) {
+  for (int r = 0; r < SR_ROUNDS; ++r) {
     const uint64_t pb = (uint64_t)c[2] * 0xCD9E8D57u;
     const uint64_t pa = (uint64_t)c[0] * 0xD2511F53u;
-    if (r < 9) {
+    if (r < SR_ROUNDS - 1) {
       c[0] = __builtin_amdgcn_bitop3_b32((uint32_t)(pb >> 32), c[1], k0, 0x96);
       c[2] = __builtin_amdgcn_bitop3_b32((uint32_t)(pa >> 32), c[3], k1, 0x96);
     } else {
@@ -262,7 +268,7 @@ DEV void sr_nwords16_even(uint64_t seed, uint32_t ctr, uint32_t (&nw)[8]) {
 #pragma unroll
   for (int gi = 0; gi < 2; ++gi) {
     uint32_t c[4];
-    philox10_n02(ctr | (uint32_t)gi, 0u, seed, c);
+    philox_sr_n02(ctr | (uint32_t)gi, 0u, seed, c);
     nw[4 * gi + 0] = c[0];
     nw[4 * gi + 1] = ~c[1];
     nw[4 * gi + 2] = c[2];
@@ -279,7 +285,7 @@ DEV void sr_nwords_aligned(uint64_t seed, uint64_t idx0, uint32_t (&nw)[SPAN / 2
 #pragma unroll
   for (int gi = 0; gi < SPAN / 8; ++gi) {
     uint32_t c[4];
-    philox10_n02(lo | (uint32_t)gi, hi, seed, c);
+    philox_sr_n02(lo | (uint32_t)gi, hi, seed, c);
     nw[4 * gi + 0] = c[0];
     nw[4 * gi + 1] = ~c[1];
     nw[4 * gi + 2] = c[2];
@@ -293,7 +299,7 @@ DEV void sr_bits(uint64_t seed, uint64_t idx0, uint32_t (&h)[SPAN]) {
 #pragma unroll
     for (int gi = 0; gi < SPAN / 8; ++gi) {
       uint32_t c[4];
-      philox10((idx0 >> 3) + gi, seed, c);
+      philox_sr((idx0 >> 3) + gi, seed, c);
 #pragma unroll
       for (int j = 0; j < 8; ++j) h[gi * 8 + j] = (j & 1) ? (c[j >> 1] >> 16) : (c[j >> 1] & 0xffffu);
     }
@@ -301,7 +307,7 @@ DEV void sr_bits(uint64_t seed, uint64_t idx0, uint32_t (&h)[SPAN]) {
     for (int j = 0; j < SPAN; ++j) {
       uint64_t idx = idx0 + j;
       uint32_t c[4];
-      philox10(idx >> 3, seed, c);
+      philox_sr(idx >> 3, seed, c);
       int jj = (int)(idx & 7);
       h[j] = (jj & 1) ? (c[jj >> 1] >> 16) : (c[jj >> 1] & 0xffffu);
     }
@@ -314,7 +320,7 @@ DEV void sr_words_aligned(uint64_t seed, uint64_t idx0, uint32_t (&w)[SPAN / 2])
 #pragma unroll
   for (int gi = 0; gi < SPAN / 8; ++gi) {
     uint32_t c[4];
-    philox10((idx0 >> 3) + gi, seed, c);
+    philox_sr((idx0 >> 3) + gi, seed, c);
 #pragma unroll
     for (int k = 0; k < 4; ++k) w[gi * 4 + k] = c[k];
   }

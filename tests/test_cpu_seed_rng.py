@@ -2,7 +2,7 @@
 
 Pins: the reference's derive_seed known answer and error contract
 (tests/test_stochastic_rounding.py:23-39 of the reference), the published
-Random123 Philox4x32-10 vectors, and the stream properties the reference's
+Random123 Philox4x32-10 and Philox4x32-7 vectors, and the stream properties the reference's
 tests assert of its uniforms (replay, range, decorrelation by target path
 and merge index, launch-geometry independence; P/_stochastic_quantization.py
 and P/_triton_stochastic_quantization.py).
@@ -55,25 +55,31 @@ def test_package_and_oracle_seeds_agree() -> None:
         assert seeding.derive_seed(key, idx) == O.derive_seed(key, idx)
 
 
-@pytest.mark.parametrize("case", GOLDEN["philox4x32_10"], ids=lambda c: c["ctr"][0])
-def test_philox_known_answers(case: dict) -> None:
+@pytest.mark.parametrize("rounds,case", [(10, c) for c in GOLDEN["philox4x32_10"]]
+                         + [(7, c) for c in GOLDEN["philox4x32_7"]], ids=lambda v: str(v) if isinstance(v, int) else v["ctr"][0])
+def test_philox_known_answers(rounds: int, case: dict) -> None:
     ctr = tuple(_hex(v) for v in case["ctr"])
     key = tuple(_hex(v) for v in case["key"])
-    assert O.philox4x32(ctr, key) == tuple(_hex(v) for v in case["out"])
+    assert O.philox4x32(ctr, key, rounds=rounds) == tuple(_hex(v) for v in case["out"])
 
 
-def test_philox_round_count_matters() -> None:
-    # a dropped or extra round must not reproduce the 10-round vectors
-    case = GOLDEN["philox4x32_10"][2]
+@pytest.mark.parametrize("rounds", [10, 7])
+def test_philox_round_count_matters(rounds: int) -> None:
+    # a dropped or extra round must not reproduce the published vectors
+    case = GOLDEN[f"philox4x32_{rounds}"][2]
     ctr = tuple(_hex(v) for v in case["ctr"])
     key = tuple(_hex(v) for v in case["key"])
     want = tuple(_hex(v) for v in case["out"])
-    assert O.philox4x32(ctr, key, rounds=9) != want
-    assert O.philox4x32(ctr, key, rounds=11) != want
+    assert O.philox4x32(ctr, key, rounds=rounds - 1) != want
+    assert O.philox4x32(ctr, key, rounds=rounds + 1) != want
+
+
+def test_sr_stream_uses_seven_rounds() -> None:
+    assert O.sr_rounds() == 7
 
 
 def test_stream_layout_eight_halfwords_per_philox_call() -> None:
-    # element i uses half-word (i & 7) of Philox4x32-10(counter = i >> 3, key = seed):
+    # element i uses half-word (i & 7) of Philox4x32-7(counter = i >> 3, key = seed):
     # word j>>1, low half for even j; u = h * 2^-16
     seed = O.derive_seed("layers.0.weight", 0)
     key = (seed & 0xFFFFFFFF, seed >> 32)
@@ -82,7 +88,7 @@ def test_stream_layout_eight_halfwords_per_philox_call() -> None:
     for k in range(64):
         idx = start + k
         ctr = idx >> 3
-        words = O.philox4x32((ctr & 0xFFFFFFFF, ctr >> 32, 0, 0), key)
+        words = O.philox4x32((ctr & 0xFFFFFFFF, ctr >> 32, 0, 0), key, rounds=7)
         j = idx & 7
         h = (words[j >> 1] >> (16 * (j & 1))) & 0xFFFF
         assert u[k] == np.float32(h / 65536.0)
@@ -119,3 +125,13 @@ def test_uniforms_are_uniform_on_the_16_bit_grid() -> None:
     chi2 = float(((counts - expected) ** 2 / expected).sum())
     assert chi2 < 45.0  # 15 dof; p ~ 1e-4
     assert abs(float(u.mean()) - (0.5 - 2.0 ** -17)) < 0.003
+
+
+def test_sr_stream_has_no_serial_correlation() -> None:
+    # Philox4x32-7 draws: neighbouring elements (same call, next half-word,
+    # next word, next call) are uncorrelated at the 2^18-sample level
+    u = O.uniforms(O.derive_seed("serial", 0), 0, 1 << 18).astype(np.float64) - 0.5
+    for lag in (1, 2, 3, 4, 7, 8, 9, 16):
+        r = float(np.dot(u[:-lag], u[lag:]) / np.dot(u, u))
+        assert abs(r) < 0.01, (lag, r)
+

@@ -143,6 +143,35 @@ def test_int8_two_pass_rows_and_in_place(shape, rank, sr):
     assert np.array_equal(_scale_np(sd), rs)
 
 
+def test_int8_fused_sr_two_neighbours_and_unbiased():
+    """The fused merge's stochastic codes (Philox4x32-7 draws) over 64 seeds:
+    every code is floor or ceil of merged / scale, and the mean code is
+    merged / scale within 0.005 overall and within 0.01 in each tenth of the
+    fractional part (the reference's contract: E[code] = x, P(up) = frac)."""
+    rows, cols, rank = 64, 4096, 16
+    q, s, b, a = _int8_case(rows, cols, rank, seed=31)
+    qd, sd, bd, ad = q.to(DEV), s.to(DEV), b.to(DEV), a.to(DEV)
+    dense = K.dequantize_int8(qd, sd, None, (1, cols), lora=(bd, ad, 0.5))
+    acc = np.zeros((rows, cols), np.float64)
+    n_seeds = 64
+    for i in range(n_seeds):
+        oq, os_, _ = K.merge_int8_lora(qd, sd, None, (1, cols), bd, ad, 0.5, asymmetric=False, reduce_range=False,
+                                       rounding_seed=derive_seed("int8.sr-stats", i))
+        if i == 0:
+            y = O.bf16_to_f32(bf16_np(dense)).astype(np.float64) / _scale_np(os_).astype(np.float64)[:, None]
+            yc = np.clip(y, -128, 127)
+        qf = oq.cpu().numpy().astype(np.float64)
+        assert np.all((qf == np.floor(yc)) | (qf == np.ceil(yc)))
+        acc += qf
+    interior = (y > -128) & (y < 127) & (y != np.floor(y))
+    err = (acc / n_seeds - y)[interior]
+    assert abs(err.mean()) < 0.005
+    frac = (y - np.floor(y))[interior]
+    for lo in np.arange(0.0, 1.0, 0.1):
+        sel = (frac >= lo) & (frac < lo + 0.1)
+        assert abs(err[sel].mean()) < 0.01, (lo, err[sel].mean())
+
+
 def test_int8_fused_vs_oracle_pipeline():
     rows, cols, rank = 64, 4096, 32
     q, s, b, a = _int8_case(rows, cols, rank)
