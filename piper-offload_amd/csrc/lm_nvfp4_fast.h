@@ -22,8 +22,9 @@
 //                 rounded values is the rounded max of the unrounded ones;
 //   k_nv_quant -- g = max(amax / 2688, eps); per block s = e4m3(clamp(
 //                 (bmax / 6) / g, 2^-6, 448)); codes = e2m1(merged * ((1/g)/s));
-//   k_nv_finalize -- writes g once every quant workgroup has read the inputs
-//                 (the outputs may alias them).
+//   The amax pass copies the input g into red[1] and the quant pass reads
+//   that copy, so the quant pass's first workgroup can write the output g
+//   even where it aliases the input.
 // Single-level tensors skip the amax pass and divide by the block scale.
 #pragma once
 #include "lm_impl.h"
@@ -308,6 +309,8 @@ DEV void nv_amax_body_direct(const NvArgs& a, int64_t row0, int t0, int t1) {
   const bool second = row0 + 16 < a.M;  // wave-uniform
   const int ntiles = t1;
   const float gin = *(const LM_GLOBAL float*)a.gin;
+  // the quant pass reads this copy: the per-tensor scale output may alias gin
+  if (row0 == 0 && t0 == 0 && threadIdx.x == 0) ((LM_GLOBAL uint32_t*)a.red)[1] = f2u(gin);
   const float strength = a.strength;
   // rows past M read row M - 1 (valid memory) and are left out of the max
   const NvLane<NKC> l0 = nv_lane<NKC>(a, rok0 ? r0 : a.M - 1, lane);
@@ -373,6 +376,8 @@ DEV void nv_amax_body_lds(const NvArgs& a, int64_t row0, int t0, int t1) {
   const int steps = (ntiles - t0 + NV_NW - 1) / NV_NW;  // workgroup-uniform
   const int64_t half = a.N >> 1, scols = a.N >> 4;
   const float gin = *(const LM_GLOBAL float*)a.gin;
+  // the quant pass reads this copy: the per-tensor scale output may alias gin
+  if (row0 == 0 && t0 == 0 && threadIdx.x == 0) ((LM_GLOBAL uint32_t*)a.red)[1] = f2u(gin);
   const float strength = a.strength;
   const bool second = row0 + 16 < a.M;  // workgroup-uniform
   // staging: thread tid loads code chunks q = tid, tid + 512 (row q >> 5,
@@ -485,11 +490,14 @@ DEV void nv_quant_body(const NvArgs& a, int64_t row0, int t0, int t1, const floa
   const bool rok = row < a.M;
   const int64_t rowc = rok ? row : a.M - 1;
   const int ntiles = t1;
-  const float gin = TWO ? *(const LM_GLOBAL float*)a.gin : 1.0f;
+  // the input per-tensor scale from the amax pass's copy (red[1]); the
+  // output one is written here, by one thread, since it may alias the input
+  const float gin = TWO ? u2f(((const LM_GLOBAL uint32_t*)a.red)[1]) : 1.0f;
   float gq = 1.0f, inv_g = 1.0f;
   if constexpr (TWO) {
     gq = __builtin_fmaxf(u2f(*(const LM_GLOBAL uint32_t*)a.red) / 2688.0f, kEps);
     inv_g = 1.0f / gq;
+    if (row0 == 0 && t0 == 0 && threadIdx.x == 0 && a.gout != nullptr) *(LM_GLOBAL float*)a.gout = gq;
   }
   const NvLane<NKC> l = nv_lane<NKC>(a, rowc, lane);
   LM_GLOBAL uint8_t* qo = (LM_GLOBAL uint8_t*)a.q_out + rowc * (a.N >> 1) + 16 * (lane >> 4);
@@ -560,21 +568,10 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant_stack(const NvStackItem
   const NvArgs& a = items[i].a;
   nv_quant_body<NKC, TWO, SR>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16, 0, (int)(a.N >> 7), rtab);
 }
-// one thread per item: g = max(amax / 2688, eps)
-static __global__ void k_nv_finalize(const NvStackItem* __restrict__ items, int count) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= count) return;
-  const NvArgs& a = items[i].a;
-  if (a.gin != nullptr && a.gout != nullptr) *a.gout = __builtin_fmaxf(u2f(*a.red) / 2688.0f, kEps);
-}
-static __global__ void k_nv_finalize1(NvArgs a) {
-  if (threadIdx.x == 0 && a.gin != nullptr && a.gout != nullptr) *a.gout = __builtin_fmaxf(u2f(*a.red) / 2688.0f, kEps);
-}
-
 // bf16 factors, a rank bucket, whole macro tiles
 static inline bool nv_fast_ok(int cd, int nkc, int64_t N) { return cd == LM_BF16 && nkc > 0 && (N % 128) == 0; }
 
-// single tensor: amax (two-level), quant, finalize on `st`
+// single tensor: amax (two-level), then quant on `st`
 static int nv_fast_run(const NvArgs& a, int nkc, bool sr, hipStream_t st) {
   const dim3 grid((unsigned)nv_units(a.M, a.N), (unsigned)(((a.N >> 7) + NV_CHUNK - 1) / NV_CHUNK)), block(NV_NW * 64);
   if (a.gin) {
@@ -589,10 +586,6 @@ static int nv_fast_run(const NvArgs& a, int nkc, bool sr, hipStream_t st) {
     if (a.gin) { if (sr) { NQ1(true, true); } else { NQ1(false, true); } }
     else { if (sr) { NQ1(true, false); } else { NQ1(false, false); } }
 #undef NQ1
-    LAUNCH_CHECK();
-  }
-  if (a.gin) {
-    hipLaunchKernelGGL(k_nv_finalize1, dim3(1), dim3(64), 0, st, a);
     LAUNCH_CHECK();
   }
   return LM_OK;

@@ -173,7 +173,7 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
 }
 
 // Grouped NVFP4 merge: one amax launch over the two-level items, one quant
-// launch per scale level (two-level, single-level), one finalize.  `dev_items` is workspace for the
+// launch per scale level (two-level, single-level).  `dev_items` is workspace for the
 // descriptor table (fits in the BlkArgs region of lm_stack_workspace_extra).
 static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swizzled, bool sr, const PrepItem* preps,
                          uint8_t* dev_items, hipStream_t st) {
@@ -241,11 +241,6 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
 #undef NQ
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 quant launch: %s", hipGetErrorString(e));
-  }
-  if (rc == LM_OK && n_two > 0) {
-    hipLaunchKernelGGL(k_nv_finalize, dim3((n_two + 63) / 64), dim3(64), 0, st, d, n_two);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 finalize launch: %s", hipGetErrorString(e));
   }
   free(h);
   return rc;
