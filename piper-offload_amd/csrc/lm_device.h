@@ -138,6 +138,17 @@ DEV float div_rn(float v, float s, float r) {
   return __builtin_copysignf(q1, q0);
 }
 
+// A 16-byte global store whose data registers stay unwritten for two wait
+// states after it.  On gfx950 a VALU write to a data register of a 16-byte
+// store in the very next instruction corrupts what the store writes (the
+// last lanes of each row of 16), and the compiler does not pad it; the
+// s_nop takes the data registers as inputs, so nothing can overwrite them
+// before it.
+DEV void store_b128_guarded(LM_GLOBAL lm_u32x4* p, lm_u32x4 v) {
+  *p = v;
+  asm volatile("s_nop 1" ::"v"(v) : "memory");
+}
+
 // ---- 8-bit floats -----------------------------------------------------
 template <int FMT>
 DEV float fp8_decode(uint32_t word, int byte) {

@@ -711,7 +711,7 @@ __device__ __forceinline__ void fast_quant_store_vals(const RowArgs& a, const Fa
       else out[i] = fp8_pack4<F>(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
     }
   }
-  *(LM_GLOBAL lm_u32x4*)(L.out + (uint32_t)(mt * 64) + L.off) = lm_u32x4{out[0], out[1], out[2], out[3]};
+  store_b128_guarded((LM_GLOBAL lm_u32x4*)(L.out + (uint32_t)(mt * 64) + L.off), lm_u32x4{out[0], out[1], out[2], out[3]});
 }
 // the same from the packed bf16 pairs w[8] of a cached tile
 template <int KIND, bool SR>
@@ -890,12 +890,22 @@ __global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_row
 // TPW consecutive 64-column tiles; SPLIT_NW waves per workgroup take
 // consecutive tile ranges of the same rows.
 static constexpr int SPLIT_NW = 4;
-template <int KIND, bool SR, int NKC, int RB, int TPW, bool QUANT>
+// PIPE 0: per tile, the MFMAs of every row block first (they consume the A^T
+// fragment), then the next tile's loads into the same registers, then the
+// arithmetic (holds RB x 16 deltas).  PIPE 1: two register sets of operands
+// and codes, the next tile's loads issued before this tile's row blocks are
+// processed one at a time (holds one block's deltas).
+template <int KIND, bool SR, int NKC, int RB, int TPW, bool QUANT, int PIPE = 0, int IL = 0>
 __global__ __launch_bounds__(SPLIT_NW * 64) void k_rows_split(RowArgs a, int wg_per_group) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int ntiles = (int)(a.N >> 6);
   const int64_t grp = blockIdx.x / wg_per_group;
-  const int t0 = ((int)(blockIdx.x - grp * wg_per_group) * SPLIT_NW + wave) * TPW;
+  // IL: the workgroup's waves take interleaved tiles (wave w: w, w + 4, ...)
+  // of its 4 TPW, so that at any time they read neighbouring 64-byte halves
+  // of the same 128-byte lines
+  const int wgi = (int)(blockIdx.x - grp * wg_per_group);
+  const int t0 = IL ? wgi * SPLIT_NW * TPW + wave : (wgi * SPLIT_NW + wave) * TPW;
+  constexpr int TS = IL ? SPLIT_NW : 1;  // tile stride of a wave
   if (t0 >= ntiles) return;  // wave-uniform; the kernel has no barrier
   const int64_t mpad = (a.M + 15) / 16 * 16;
   LM_GLOBAL uint32_t* rmax = (LM_GLOBAL uint32_t*)a.red + 64;
@@ -932,6 +942,46 @@ __global__ __launch_bounds__(SPLIT_NW * 64) void k_rows_split(RowArgs a, int wg_
       s_in[rb] = ((const LM_GLOBAL float*)a.scale)[rowc];
     }
   }
+  // merge (and requant) of one row block of one tile
+  auto block = [&](int rb, int mt, const uint4& codes, const float (&d)[16]) {
+    float m[16];
+    fast_merge_vals<KIND, !QUANT>(a, codes, d, s_in[rb], m, amax[rb]);
+    if constexpr (QUANT) {
+      uint32_t old[8];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) m[j] = bf16r(m[j]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) old[i] = f2u(m[2 * i]);
+      fast_quant_store_vals<KIND, SR>(a, L[rb], rok[rb], mt, qp[rb], m, old);
+    }
+  };
+  if constexpr (PIPE == 1) {
+    v4i16 aopA[4][NKC], aopB[4][NKC];
+    uint4 rawA[RB], rawB[RB];
+    auto load2 = [&](v4i16 (&aop)[4][NKC], uint4 (&raw)[RB], int mt) {
+      fast_load_aop<NKC>(L[0], mt, aop);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) raw[rb] = fast_load_codes(L[rb], mt);
+    };
+    auto tile2 = [&](const v4i16 (&aop)[4][NKC], const uint4 (&raw)[RB], int mt) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        float d[16];
+        fast_tile_delta<NKC>(aop, bop[rb], d);
+        block(rb, mt, raw[rb], d);
+      }
+    };
+    const int t1 = t0 + TS * TPW <= ntiles ? t0 + TS * TPW : ntiles;
+    load2(aopA, rawA, t0);
+    for (int mt = t0; mt < t1; mt += 2 * TS) {
+      if (mt + TS < t1) load2(aopB, rawB, mt + TS);
+      tile2(aopA, rawA, mt);
+      if (mt + TS < t1) {
+        if (mt + 2 * TS < t1) load2(aopA, rawA, mt + 2 * TS);
+        tile2(aopB, rawB, mt + TS);
+      }
+    }
+  } else {
   // one tile: the deltas of every row block first (the MFMAs consume the A^T
   // operands), then the next tile's operands and codes are requested, then
   // the merge / requant arithmetic of this tile hides their latency
@@ -952,25 +1002,15 @@ __global__ __launch_bounds__(SPLIT_NW * 64) void k_rows_split(RowArgs a, int wg_
     }
     if (next >= 0) load(next);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      float m[16];
-      fast_merge_vals<KIND, !QUANT>(a, cur[rb], d[rb], s_in[rb], m, amax[rb]);
-      if constexpr (QUANT) {
-        uint32_t old[8];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) m[j] = bf16r(m[j]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) old[i] = f2u(m[2 * i]);
-        fast_quant_store_vals<KIND, SR>(a, L[rb], rok[rb], mt, qp[rb], m, old);
-      }
-    }
+    for (int rb = 0; rb < RB; ++rb) block(rb, mt, cur[rb], d[rb]);
   };
   load(t0);
-  if (t0 + TPW <= ntiles) {
+  if (t0 + TS * (TPW - 1) < ntiles) {
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) tile(t0 + i, i + 1 < TPW ? t0 + i + 1 : -1);
+    for (int i = 0; i < TPW; ++i) tile(t0 + TS * i, i + 1 < TPW ? t0 + TS * (i + 1) : -1);
   } else {
-    for (int mt = t0; mt < ntiles; ++mt) tile(mt, mt + 1 < ntiles ? mt + 1 : -1);
+    for (int mt = t0; mt < ntiles; mt += TS) tile(mt, mt + TS < ntiles ? mt + TS : -1);
+  }
   }
   if constexpr (!QUANT) {
 #pragma unroll
@@ -1680,13 +1720,16 @@ static int launch_rows_fast(const RowArgs& a, hipStream_t st) {
 // RB 8 (30.4 at RB 4, 42 at RB 2); quant pass 53.9 us at RB 4, TPW 8 (56.3 at
 // RB 2, 58.3 without the one-tile operand prefetch).
 static constexpr int SPLIT_RB1 = 8, SPLIT_TPW1 = 8, SPLIT_RB2 = 4, SPLIT_TPW2 = 8;
+// the workgroup's 4 waves take interleaved tiles (amax pass 25.9 -> 24.0 us,
+// quant pass 50.7 -> 49.8 us on FP8 config 3, stochastic)
+static constexpr int SPLIT_IL = 1;
 // whether a per-row merge runs the two-pass kernels: rows too long for the
 // register cache at rank above 32, where the cached kernel runs one
 // workgroup per CU
 static inline bool rows_split_wanted(int kind, int cd, int sdt, bool asym, bool sr, int nkc, int64_t M, int64_t N) {
   return rows_fast_ok(kind, cd, sdt, asym, nkc, M, N) && nkc == 4 && rows_long_mode(nkc, sr, N) == ROWS_DEEP;
 }
-template <int KIND, bool SR, int NKC, int RB, int TPW, bool QUANT>
+template <int KIND, bool SR, int NKC, int RB, int TPW, bool QUANT, int PIPE = 0, int IL = 0>
 static int launch_rows_split_pass(const RowArgs& a, hipStream_t st) {
   const int64_t waves = (a.N / 64 + TPW - 1) / TPW;
   const int64_t wg_per_group = (waves + SPLIT_NW - 1) / SPLIT_NW;
@@ -1694,7 +1737,7 @@ static int launch_rows_split_pass(const RowArgs& a, hipStream_t st) {
   if (groups * wg_per_group > 0x7fffffff) return fail(LM_EUNSUPPORTED, "weight too large for one row launch");
   {
     TimedLaunch timed("rows", st);
-    hipLaunchKernelGGL((k_rows_split<KIND, SR, NKC, RB, TPW, QUANT>), dim3((unsigned)(groups * wg_per_group)),
+    hipLaunchKernelGGL((k_rows_split<KIND, SR, NKC, RB, TPW, QUANT, PIPE, IL>), dim3((unsigned)(groups * wg_per_group)),
                        dim3(SPLIT_NW * 64), 0, st, a, (int)wg_per_group);
   }
   LAUNCH_CHECK();
@@ -1702,8 +1745,8 @@ static int launch_rows_split_pass(const RowArgs& a, hipStream_t st) {
 }
 template <int KIND, bool SR, int NKC>
 static int launch_rows_split(const RowArgs& a, hipStream_t st) {
-  const int rc = launch_rows_split_pass<KIND, SR, NKC, SPLIT_RB1, SPLIT_TPW1, false>(a, st);
-  return rc ? rc : launch_rows_split_pass<KIND, SR, NKC, SPLIT_RB2, SPLIT_TPW2, true>(a, st);
+  const int rc = launch_rows_split_pass<KIND, SR, NKC, SPLIT_RB1, SPLIT_TPW1, false, 0, SPLIT_IL>(a, st);
+  return rc ? rc : launch_rows_split_pass<KIND, SR, NKC, SPLIT_RB2, SPLIT_TPW2, true, 0, SPLIT_IL>(a, st);
 }
 
 template <int KIND, bool FROM_DENSE>
