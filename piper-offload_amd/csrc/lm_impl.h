@@ -887,15 +887,11 @@ __global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_row
 // another still needs it).  Both passes address codes, A^T operands and
 // Philox counters exactly as k_rows_fast does, so results are bit-identical.
 // A wave covers RB 16-row blocks (they share each tile's A^T operands) and
-// TPW consecutive 64-column tiles; SPLIT_NW waves per workgroup take
-// consecutive tile ranges of the same rows.
+// TPW 64-column tiles; the SPLIT_NW waves of a workgroup share the same rows
+// and a range of SPLIT_NW x TPW tiles (interleaved with IL, else consecutive
+// per wave).
 static constexpr int SPLIT_NW = 4;
-// PIPE 0: per tile, the MFMAs of every row block first (they consume the A^T
-// fragment), then the next tile's loads into the same registers, then the
-// arithmetic (holds RB x 16 deltas).  PIPE 1: two register sets of operands
-// and codes, the next tile's loads issued before this tile's row blocks are
-// processed one at a time (holds one block's deltas).
-template <int KIND, bool SR, int NKC, int RB, int TPW, bool QUANT, int PIPE = 0, int IL = 0>
+template <int KIND, bool SR, int NKC, int RB, int TPW, bool QUANT, int IL = 0>
 __global__ __launch_bounds__(SPLIT_NW * 64) void k_rows_split(RowArgs a, int wg_per_group) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int ntiles = (int)(a.N >> 6);
@@ -955,33 +951,6 @@ __global__ __launch_bounds__(SPLIT_NW * 64) void k_rows_split(RowArgs a, int wg_
       fast_quant_store_vals<KIND, SR>(a, L[rb], rok[rb], mt, qp[rb], m, old);
     }
   };
-  if constexpr (PIPE == 1) {
-    v4i16 aopA[4][NKC], aopB[4][NKC];
-    uint4 rawA[RB], rawB[RB];
-    auto load2 = [&](v4i16 (&aop)[4][NKC], uint4 (&raw)[RB], int mt) {
-      fast_load_aop<NKC>(L[0], mt, aop);
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) raw[rb] = fast_load_codes(L[rb], mt);
-    };
-    auto tile2 = [&](const v4i16 (&aop)[4][NKC], const uint4 (&raw)[RB], int mt) {
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        float d[16];
-        fast_tile_delta<NKC>(aop, bop[rb], d);
-        block(rb, mt, raw[rb], d);
-      }
-    };
-    const int t1 = t0 + TS * TPW <= ntiles ? t0 + TS * TPW : ntiles;
-    load2(aopA, rawA, t0);
-    for (int mt = t0; mt < t1; mt += 2 * TS) {
-      if (mt + TS < t1) load2(aopB, rawB, mt + TS);
-      tile2(aopA, rawA, mt);
-      if (mt + TS < t1) {
-        if (mt + 2 * TS < t1) load2(aopA, rawA, mt + 2 * TS);
-        tile2(aopB, rawB, mt + TS);
-      }
-    }
-  } else {
   // one tile: the deltas of every row block first (the MFMAs consume the A^T
   // operands), then the next tile's operands and codes are requested, then
   // the merge / requant arithmetic of this tile hides their latency
@@ -1010,7 +979,6 @@ __global__ __launch_bounds__(SPLIT_NW * 64) void k_rows_split(RowArgs a, int wg_
     for (int i = 0; i < TPW; ++i) tile(t0 + TS * i, i + 1 < TPW ? t0 + TS * (i + 1) : -1);
   } else {
     for (int mt = t0; mt < ntiles; mt += TS) tile(mt, mt + TS < ntiles ? mt + TS : -1);
-  }
   }
   if constexpr (!QUANT) {
 #pragma unroll
@@ -1729,7 +1697,7 @@ static constexpr int SPLIT_IL = 1;
 static inline bool rows_split_wanted(int kind, int cd, int sdt, bool asym, bool sr, int nkc, int64_t M, int64_t N) {
   return rows_fast_ok(kind, cd, sdt, asym, nkc, M, N) && nkc == 4 && rows_long_mode(nkc, sr, N) == ROWS_DEEP;
 }
-template <int KIND, bool SR, int NKC, int RB, int TPW, bool QUANT, int PIPE = 0, int IL = 0>
+template <int KIND, bool SR, int NKC, int RB, int TPW, bool QUANT, int IL = 0>
 static int launch_rows_split_pass(const RowArgs& a, hipStream_t st) {
   const int64_t waves = (a.N / 64 + TPW - 1) / TPW;
   const int64_t wg_per_group = (waves + SPLIT_NW - 1) / SPLIT_NW;
@@ -1737,7 +1705,7 @@ static int launch_rows_split_pass(const RowArgs& a, hipStream_t st) {
   if (groups * wg_per_group > 0x7fffffff) return fail(LM_EUNSUPPORTED, "weight too large for one row launch");
   {
     TimedLaunch timed("rows", st);
-    hipLaunchKernelGGL((k_rows_split<KIND, SR, NKC, RB, TPW, QUANT, PIPE, IL>), dim3((unsigned)(groups * wg_per_group)),
+    hipLaunchKernelGGL((k_rows_split<KIND, SR, NKC, RB, TPW, QUANT, IL>), dim3((unsigned)(groups * wg_per_group)),
                        dim3(SPLIT_NW * 64), 0, st, a, (int)wg_per_group);
   }
   LAUNCH_CHECK();
@@ -1745,8 +1713,8 @@ static int launch_rows_split_pass(const RowArgs& a, hipStream_t st) {
 }
 template <int KIND, bool SR, int NKC>
 static int launch_rows_split(const RowArgs& a, hipStream_t st) {
-  const int rc = launch_rows_split_pass<KIND, SR, NKC, SPLIT_RB1, SPLIT_TPW1, false, 0, SPLIT_IL>(a, st);
-  return rc ? rc : launch_rows_split_pass<KIND, SR, NKC, SPLIT_RB2, SPLIT_TPW2, true, 0, SPLIT_IL>(a, st);
+  const int rc = launch_rows_split_pass<KIND, SR, NKC, SPLIT_RB1, SPLIT_TPW1, false, SPLIT_IL>(a, st);
+  return rc ? rc : launch_rows_split_pass<KIND, SR, NKC, SPLIT_RB2, SPLIT_TPW2, true, SPLIT_IL>(a, st);
 }
 
 template <int KIND, bool FROM_DENSE>
