@@ -17,7 +17,8 @@
  *   - merged = round_cd(fmaf(delta, strength, base))
  *     (P/_triton_int8_lora.py:89-93);
  *   - stochastic rounding draws u = k * 2^-16 with k the 16-bit half-word
- *     (idx & 7) of Philox4x32-7(ctr = (idx >> 3, 0, 0), key = seed), or the
+ *     (idx & 7) of Philox4x32-7(ctr = (idx >> 3, 0, 0), key = seed), taken
+ *     from the complement of words 1 and 3, or the
  *     Triton tl.rand stream (P/_triton_stochastic_quantization.py:19-22) in
  *     compatibility mode.
  *
@@ -193,6 +194,19 @@ EXPORT void lmo_philox4x32(const uint32_t* ctr, uint32_t k0, uint32_t k1, int ro
 #define SR_PHILOX_ROUNDS 7
 EXPORT int lmo_sr_rounds(void) { return SR_PHILOX_ROUNDS; }
 
+/* 16-bit Philox draw h of the element at offset idx (SR_PHILOX8 layout):
+ * half (idx & 1) of word k = (idx & 7) >> 1 of Philox4x32-7(counter
+ * idx >> 3, key seed), complemented for odd k (words 1 and 3). */
+static inline uint32_t sr_h16(uint64_t seed, uint64_t idx) {
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+  uint64_t g = idx >> 3;
+  uint32_t c[4] = {(uint32_t)g, (uint32_t)(g >> 32), 0, 0};
+  philox4x32(c, k0, k1, SR_PHILOX_ROUNDS);
+  int j = (int)(idx & 7);
+  uint32_t w = ((j >> 1) & 1) ? ~c[j >> 1] : c[j >> 1];
+  return (j & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
 /* Uniform for the element at logical offset idx.
  * SR_PHILOX8: one Philox call per 8 consecutive offsets, 16 bits each.
  * SR_TRITON : triton tl.rand(seed, idx) (uint_to_uniform_float of word 0). */
@@ -205,13 +219,7 @@ static inline float sr_uniform(int mode, uint64_t seed, uint64_t idx) {
     if (x < 0) x = -x - 1;
     return (float)x * (float)4.6566127342e-10;
   }
-  uint64_t g = idx >> 3;
-  uint32_t c[4] = {(uint32_t)g, (uint32_t)(g >> 32), 0, 0};
-  philox4x32(c, k0, k1, SR_PHILOX_ROUNDS);
-  int j = (int)(idx & 7);
-  uint32_t w = c[j >> 1];
-  uint32_t h = (j & 1) ? (w >> 16) : (w & 0xffffu);
-  return (float)h * (1.0f / 65536.0f);
+  return (float)sr_h16(seed, idx) * (1.0f / 65536.0f);
 }
 EXPORT void lmo_uniforms(int mode, uint64_t seed, uint64_t start, int64_t n, float* out) {
 #pragma omp parallel for schedule(static)
@@ -228,17 +236,7 @@ static inline int sr_int(float x, int det, float u, int qmin, int qmax) {
   float rounded = lower + ((u < p) ? 1.0f : 0.0f);
   return (interior && p > 0.0f) ? (int)rounded : det;
 }
-/* 16-bit Philox draw h of the element at offset idx (SR_PHILOX8 layout; the
- * uniform of sr_uniform is h * 2^-16). */
-static inline uint32_t sr_h16(uint64_t seed, uint64_t idx) {
-  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
-  uint64_t g = idx >> 3;
-  uint32_t c[4] = {(uint32_t)g, (uint32_t)(g >> 32), 0, 0};
-  philox4x32(c, k0, k1, SR_PHILOX_ROUNDS);
-  int j = (int)(idx & 7);
-  uint32_t w = c[j >> 1];
-  return (j & 1) ? (w >> 16) : (w & 0xffffu);
-}
+
 /* Integer stochastic rounding (INT8, Q8_0) in the form the HIP kernels run on
  * gfx950's v_cvt_sr_f16_f32 (the selection rule of
  * P/_triton_stochastic_quantization.py:25-40, u < p):

@@ -272,23 +272,28 @@ DEV void philox_sr_n02(uint32_t lo, uint32_t hi, uint64_t seed, uint32_t (&c)[4]
     k1 += 0xBB67AE85u;
   }
 }
-// The 8 complemented Philox words (~w) of the 16 offsets 8 ctr .. 8 ctr + 15
-// for an even 32-bit counter ctr (offsets below 2^35): the second block's
-// counter is ctr | 1, and the high counter word is 0.
+// The stream: element idx draws the 16-bit h from half (idx & 1) of word
+// k = (idx & 7) >> 1 of philox_sr(counter idx >> 3), complemented when k is
+// odd (words 1 and 3).  The rounding rules consume 65535 - h = ~h: words 0
+// and 2 come out of philox_sr_n02 complemented, and the complements of
+// words 1 and 3 are their raw values, so ~h costs no instruction.
+// The 8 words ~h of the 16 offsets 8 ctr .. 8 ctr + 15 for an even 32-bit
+// counter ctr (offsets below 2^35): the second block's counter is ctr | 1,
+// and the high counter word is 0.
 DEV void sr_nwords16_even(uint64_t seed, uint32_t ctr, uint32_t (&nw)[8]) {
 #pragma unroll
   for (int gi = 0; gi < 2; ++gi) {
     uint32_t c[4];
     philox_sr_n02(ctr | (uint32_t)gi, 0u, seed, c);
     nw[4 * gi + 0] = c[0];
-    nw[4 * gi + 1] = ~c[1];
+    nw[4 * gi + 1] = c[1];
     nw[4 * gi + 2] = c[2];
-    nw[4 * gi + 3] = ~c[3];
+    nw[4 * gi + 3] = c[3];
   }
 }
-// The SPAN/2 complemented Philox words (~w) of offsets idx0 .. idx0+SPAN-1
-// when idx0 % SPAN == 0 (SPAN a multiple of 8): the SPAN/8 counters are
-// (idx0 >> 3) | gi with no carry.
+// The SPAN/2 words ~h of offsets idx0 .. idx0+SPAN-1 when idx0 % SPAN == 0
+// (SPAN a multiple of 8): the SPAN/8 counters are (idx0 >> 3) | gi with no
+// carry.
 template <int SPAN>
 DEV void sr_nwords_aligned(uint64_t seed, uint64_t idx0, uint32_t (&nw)[SPAN / 2]) {
   const uint64_t ctr = idx0 >> 3;
@@ -298,12 +303,16 @@ DEV void sr_nwords_aligned(uint64_t seed, uint64_t idx0, uint32_t (&nw)[SPAN / 2
     uint32_t c[4];
     philox_sr_n02(lo | (uint32_t)gi, hi, seed, c);
     nw[4 * gi + 0] = c[0];
-    nw[4 * gi + 1] = ~c[1];
+    nw[4 * gi + 1] = c[1];
     nw[4 * gi + 2] = c[2];
-    nw[4 * gi + 3] = ~c[3];
+    nw[4 * gi + 3] = c[3];
   }
 }
 // 16-bit uniform integers h for offsets idx0 .. idx0+SPAN-1 (u = h * 2^-16)
+DEV uint32_t sr_h_of(const uint32_t (&c)[4], int j) {
+  const uint32_t w = ((j >> 1) & 1) ? ~c[j >> 1] : c[j >> 1];
+  return (j & 1) ? (w >> 16) : (w & 0xffffu);
+}
 template <int SPAN>
 DEV void sr_bits(uint64_t seed, uint64_t idx0, uint32_t (&h)[SPAN]) {
   if ((idx0 & 7u) == 0) {
@@ -312,28 +321,15 @@ DEV void sr_bits(uint64_t seed, uint64_t idx0, uint32_t (&h)[SPAN]) {
       uint32_t c[4];
       philox_sr((idx0 >> 3) + gi, seed, c);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) h[gi * 8 + j] = (j & 1) ? (c[j >> 1] >> 16) : (c[j >> 1] & 0xffffu);
+      for (int j = 0; j < 8; ++j) h[gi * 8 + j] = sr_h_of(c, j);
     }
   } else {
     for (int j = 0; j < SPAN; ++j) {
       uint64_t idx = idx0 + j;
       uint32_t c[4];
       philox_sr(idx >> 3, seed, c);
-      int jj = (int)(idx & 7);
-      h[j] = (jj & 1) ? (c[jj >> 1] >> 16) : (c[jj >> 1] & 0xffffu);
+      h[j] = sr_h_of(c, (int)(idx & 7));
     }
-  }
-}
-// The SPAN/2 Philox output words covering offsets idx0 .. idx0+SPAN-1 when idx0 % 8 == 0:
-// word k holds h for offsets idx0+2k (low half) and idx0+2k+1 (high half).
-template <int SPAN>
-DEV void sr_words_aligned(uint64_t seed, uint64_t idx0, uint32_t (&w)[SPAN / 2]) {
-#pragma unroll
-  for (int gi = 0; gi < SPAN / 8; ++gi) {
-    uint32_t c[4];
-    philox_sr((idx0 >> 3) + gi, seed, c);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) w[gi * 4 + k] = c[k];
   }
 }
 // u < p with u = h * 2^-16 (exact: both sides scaled by 2^16)
@@ -403,40 +399,12 @@ DEV uint32_t sr_e2m1_nword(const float* x, const uint32_t* nw) {
   od = cvt_sr_fp4<3>(od, x[7], x[6], sr_seed_hi(nw[3]));
   return (ev & 0x0f0f0f0fu) | ((od << 4) & 0xf0f0f0f0u);
 }
-// the same from the Philox words themselves
-DEV uint32_t sr_e2m1_word(const float* x, const uint32_t* w) {
-  uint32_t ev = 0u, od = 0u;
-  uint32_t nw = ~w[0];
-  ev = cvt_sr_fp4<0>(ev, x[0], x[1], sr_seed_lo(nw));
-  od = cvt_sr_fp4<0>(od, x[1], x[0], sr_seed_hi(nw));
-  nw = ~w[1];
-  ev = cvt_sr_fp4<1>(ev, x[2], x[3], sr_seed_lo(nw));
-  od = cvt_sr_fp4<1>(od, x[3], x[2], sr_seed_hi(nw));
-  nw = ~w[2];
-  ev = cvt_sr_fp4<2>(ev, x[4], x[5], sr_seed_lo(nw));
-  od = cvt_sr_fp4<2>(od, x[5], x[4], sr_seed_hi(nw));
-  nw = ~w[3];
-  ev = cvt_sr_fp4<3>(ev, x[6], x[7], sr_seed_lo(nw));
-  od = cvt_sr_fp4<3>(od, x[7], x[6], sr_seed_hi(nw));
-  return (ev & 0x0f0f0f0fu) | ((od << 4) & 0xf0f0f0f0u);
-}
 // Four fp8 codes of x[0..3] (clamped by the caller), element 2k + i drawn
 // from half i of the complemented Philox word nw[k] = ~w[k]
 template <int FMT>
 DEV uint32_t sr_fp8_nword(const float* x, const uint32_t* nw) {
   uint32_t r = 0u;
   const uint32_t n0 = nw[0], n1 = nw[1];
-  r = cvt_sr_fp8<FMT, 0>(r, x[0], sr_seed_lo(n0));
-  r = cvt_sr_fp8<FMT, 1>(r, x[1], sr_seed_hi(n0));
-  r = cvt_sr_fp8<FMT, 2>(r, x[2], sr_seed_lo(n1));
-  r = cvt_sr_fp8<FMT, 3>(r, x[3], sr_seed_hi(n1));
-  return r;
-}
-// the same from the Philox words themselves
-template <int FMT>
-DEV uint32_t sr_fp8_word(const float* x, const uint32_t* w) {
-  uint32_t r = 0u;
-  const uint32_t n0 = ~w[0], n1 = ~w[1];
   r = cvt_sr_fp8<FMT, 0>(r, x[0], sr_seed_lo(n0));
   r = cvt_sr_fp8<FMT, 1>(r, x[1], sr_seed_hi(n0));
   r = cvt_sr_fp8<FMT, 2>(r, x[2], sr_seed_lo(n1));
