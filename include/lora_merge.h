@@ -37,9 +37,9 @@
  *  - Return value: LM_OK or an lm_status; lm_last_error() returns a
  *    thread-local message for the last failure on the calling thread.
  *  - The deterministic path rounds to nearest even.  Stochastic rounding
- *    draws u = k * 2^-16, k the 16-bit half-word (idx & 7) of
- *    Philox4x32-7(counter = idx >> 3, key = seed), words 1 and 3
- *    complemented, idx = row * N + col.
+ *    draws u = k * 2^-16, k a 16-bit half of word (idx & 7) >> 1 of
+ *    Philox4x32-7(counter = idx >> 3, key = seed) (high half for even idx,
+ *    words 1 and 3 complemented), idx = row * N + col.
  *  - merged = round_compute(fma(delta, strength, base)), delta the fp32
  *    accumulation of B@A on bf16/fp16 MFMA.
  */

@@ -16,9 +16,9 @@
  *     is a canonical restatement -- see the tolerance contract in tests/);
  *   - merged = round_cd(fmaf(delta, strength, base))
  *     (P/_triton_int8_lora.py:89-93);
- *   - stochastic rounding draws u = k * 2^-16 with k the 16-bit half-word
- *     (idx & 7) of Philox4x32-7(ctr = (idx >> 3, 0, 0), key = seed), taken
- *     from the complement of words 1 and 3, or the
+ *   - stochastic rounding draws u = k * 2^-16 with k a 16-bit half of word
+ *     (idx & 7) >> 1 of Philox4x32-7(ctr = (idx >> 3, 0, 0), key = seed)
+ *     (the high half for even idx; words 1 and 3 complemented), or the
  *     Triton tl.rand stream (P/_triton_stochastic_quantization.py:19-22) in
  *     compatibility mode.
  *
@@ -195,8 +195,9 @@ EXPORT void lmo_philox4x32(const uint32_t* ctr, uint32_t k0, uint32_t k1, int ro
 EXPORT int lmo_sr_rounds(void) { return SR_PHILOX_ROUNDS; }
 
 /* 16-bit Philox draw h of the element at offset idx (SR_PHILOX8 layout):
- * half (idx & 1) of word k = (idx & 7) >> 1 of Philox4x32-7(counter
- * idx >> 3, key seed), complemented for odd k (words 1 and 3). */
+ * word k = (idx & 7) >> 1 of Philox4x32-7(counter idx >> 3, key seed),
+ * complemented for odd k (words 1 and 3); its high half for even idx, its
+ * low half for odd idx. */
 static inline uint32_t sr_h16(uint64_t seed, uint64_t idx) {
   uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
   uint64_t g = idx >> 3;
@@ -204,7 +205,7 @@ static inline uint32_t sr_h16(uint64_t seed, uint64_t idx) {
   philox4x32(c, k0, k1, SR_PHILOX_ROUNDS);
   int j = (int)(idx & 7);
   uint32_t w = ((j >> 1) & 1) ? ~c[j >> 1] : c[j >> 1];
-  return (j & 1) ? (w >> 16) : (w & 0xffffu);
+  return (j & 1) ? (w & 0xffffu) : (w >> 16);
 }
 
 /* Uniform for the element at logical offset idx.

@@ -272,9 +272,9 @@ DEV void philox_sr_n02(uint32_t lo, uint32_t hi, uint64_t seed, uint32_t (&c)[4]
     k1 += 0xBB67AE85u;
   }
 }
-// The stream: element idx draws the 16-bit h from half (idx & 1) of word
-// k = (idx & 7) >> 1 of philox_sr(counter idx >> 3), complemented when k is
-// odd (words 1 and 3).  The rounding rules consume 65535 - h = ~h: words 0
+// The stream: element idx draws the 16-bit h from word k = (idx & 7) >> 1 of
+// philox_sr(counter idx >> 3), complemented when k is odd (words 1 and 3):
+// the high half for even idx, the low half for odd idx.  The rounding rules consume 65535 - h = ~h: words 0
 // and 2 come out of philox_sr_n02 complemented, and the complements of
 // words 1 and 3 are their raw values, so ~h costs no instruction.
 // The 8 words ~h of the 16 offsets 8 ctr .. 8 ctr + 15 for an even 32-bit
@@ -311,7 +311,7 @@ DEV void sr_nwords_aligned(uint64_t seed, uint64_t idx0, uint32_t (&nw)[SPAN / 2
 // 16-bit uniform integers h for offsets idx0 .. idx0+SPAN-1 (u = h * 2^-16)
 DEV uint32_t sr_h_of(const uint32_t (&c)[4], int j) {
   const uint32_t w = ((j >> 1) & 1) ? ~c[j >> 1] : c[j >> 1];
-  return (j & 1) ? (w >> 16) : (w & 0xffffu);
+  return (j & 1) ? (w & 0xffffu) : (w >> 16);
 }
 template <int SPAN>
 DEV void sr_bits(uint64_t seed, uint64_t idx0, uint32_t (&h)[SPAN]) {
@@ -350,8 +350,13 @@ DEV void sr_bits(uint64_t seed, uint64_t idx0, uint32_t (&h)[SPAN]) {
 // (P/_triton_stochastic_quantization.py:110-177).
 // The builtin of the fp4 form does not tie its byte-select destination to the
 // previous value, so the conversions are written as asm with a "+v" operand.
-DEV uint32_t sr_seed_lo(uint32_t nw) { return (nw << 16) | 0xffffu; }  // nw = ~word: draw of its low half
-DEV uint32_t sr_seed_hi(uint32_t nw) { return nw | 0xffffu; }          // draw of its high half
+// nw = ~h of two elements: the even one in the high half, the odd one in
+// the low half
+DEV uint32_t sr_seed_hi(uint32_t nw) { return nw | 0xffffu; }          // the even element's R
+DEV uint32_t sr_seed_lo(uint32_t nw) { return (nw << 16) | 0xffffu; }  // the odd element's R
+// the odd element's R as the second operand of an fp4 pair conversion, which
+// rounds it with R << 1: (nw << 15) | 0x7fff, one v_lshl_or_b32
+DEV uint32_t sr_seed_lo_second(uint32_t nw) { return (nw << 15) | 0x7fffu; }
 DEV uint32_t sr_seed(uint32_t h) { return ((65535u - h) << 16) | 0xffffu; }
 
 // byte SEL of `old` := e2m1(a) | e2m1(b) << 4 (a with seed R, b with R << 1)
@@ -384,31 +389,37 @@ DEV uint32_t cvt_sr_fp8(uint32_t old, float x, uint32_t seed) {
 #undef LM_SR8
   return old;
 }
-// Eight e2m1 codes of x[0..7], element 2k drawn from the low half of the
-// complemented Philox word nw[k] = ~w[k] and 2k+1 from its high half
-// (independent draws: two conversions per pair, each keeping its low nibble).
+// Eight e2m1 codes of x[0..7], element 2k drawn from the high half of nw[k]
+// and 2k+1 from its low half.  Two conversions of the same pair (x[2k],
+// x[2k+1]) give independent draws: `ev` rounds the first element with the
+// even element's R and keeps the low nibbles; `od` passes the odd element's
+// R shifted right by one, so that the instruction's R << 1 for the second
+// element is that R, and keeps the high nibbles.
 DEV uint32_t sr_e2m1_nword(const float* x, const uint32_t* nw) {
-  uint32_t ev = 0u, od = 0u;
-  ev = cvt_sr_fp4<0>(ev, x[0], x[1], sr_seed_lo(nw[0]));
-  od = cvt_sr_fp4<0>(od, x[1], x[0], sr_seed_hi(nw[0]));
-  ev = cvt_sr_fp4<1>(ev, x[2], x[3], sr_seed_lo(nw[1]));
-  od = cvt_sr_fp4<1>(od, x[3], x[2], sr_seed_hi(nw[1]));
-  ev = cvt_sr_fp4<2>(ev, x[4], x[5], sr_seed_lo(nw[2]));
-  od = cvt_sr_fp4<2>(od, x[5], x[4], sr_seed_hi(nw[2]));
-  ev = cvt_sr_fp4<3>(ev, x[6], x[7], sr_seed_lo(nw[3]));
-  od = cvt_sr_fp4<3>(od, x[7], x[6], sr_seed_hi(nw[3]));
-  return (ev & 0x0f0f0f0fu) | ((od << 4) & 0xf0f0f0f0u);
+  // every byte of ev and od is written below: no initial value is needed
+  uint32_t ev, od;
+  asm("" : "=v"(ev), "=v"(od));
+  ev = cvt_sr_fp4<0>(ev, x[0], x[1], sr_seed_hi(nw[0]));
+  od = cvt_sr_fp4<0>(od, x[0], x[1], sr_seed_lo_second(nw[0]));
+  ev = cvt_sr_fp4<1>(ev, x[2], x[3], sr_seed_hi(nw[1]));
+  od = cvt_sr_fp4<1>(od, x[2], x[3], sr_seed_lo_second(nw[1]));
+  ev = cvt_sr_fp4<2>(ev, x[4], x[5], sr_seed_hi(nw[2]));
+  od = cvt_sr_fp4<2>(od, x[4], x[5], sr_seed_lo_second(nw[2]));
+  ev = cvt_sr_fp4<3>(ev, x[6], x[7], sr_seed_hi(nw[3]));
+  od = cvt_sr_fp4<3>(od, x[6], x[7], sr_seed_lo_second(nw[3]));
+  return (ev & 0x0f0f0f0fu) | (od & 0xf0f0f0f0u);
 }
-// Four fp8 codes of x[0..3] (clamped by the caller), element 2k + i drawn
-// from half i of the complemented Philox word nw[k] = ~w[k]
+// Four fp8 codes of x[0..3] (clamped by the caller), element 2k drawn from
+// the high half of nw[k] and 2k + 1 from its low half
 template <int FMT>
 DEV uint32_t sr_fp8_nword(const float* x, const uint32_t* nw) {
-  uint32_t r = 0u;
+  uint32_t r;  // every byte is written below
+  asm("" : "=v"(r));
   const uint32_t n0 = nw[0], n1 = nw[1];
-  r = cvt_sr_fp8<FMT, 0>(r, x[0], sr_seed_lo(n0));
-  r = cvt_sr_fp8<FMT, 1>(r, x[1], sr_seed_hi(n0));
-  r = cvt_sr_fp8<FMT, 2>(r, x[2], sr_seed_lo(n1));
-  r = cvt_sr_fp8<FMT, 3>(r, x[3], sr_seed_hi(n1));
+  r = cvt_sr_fp8<FMT, 0>(r, x[0], sr_seed_hi(n0));
+  r = cvt_sr_fp8<FMT, 1>(r, x[1], sr_seed_lo(n0));
+  r = cvt_sr_fp8<FMT, 2>(r, x[2], sr_seed_hi(n1));
+  r = cvt_sr_fp8<FMT, 3>(r, x[3], sr_seed_lo(n1));
   return r;
 }
 // single elements (generic kernels): det is the RTN code, which the hardware

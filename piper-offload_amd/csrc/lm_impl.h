@@ -676,16 +676,16 @@ __device__ __forceinline__ void fast_quant_store_vals(const RowArgs& a, const Fa
   if constexpr (KIND == K_INT8) {
     uint32_t y[16];
     if constexpr (SR) {
-      // integer stochastic rounding on the 13-bit grid (sr_i8_pair): the
-      // complemented Philox word nw[i] holds 65535 - h of elements 2i (low
-      // half) and 2i + 1 (high half), which are the random operands' top bits
+      // integer stochastic rounding on the 13-bit grid (sr_i8_pair): the word
+      // nw[i] holds 65535 - h of elements 2i (high half) and 2i + 1 (low
+      // half), which are the random operands' top bits
       const float lo = 1536.0f + (float)a.qmin, hi = 1536.0f + (float)a.qmax;
       uint32_t pr[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float t0 = sr_i8_t(m[2 * i], qp.rcp, 1536.0f, lo, hi);
         const float t1 = sr_i8_t(m[2 * i + 1], qp.rcp, 1536.0f, lo, hi);
-        pr[i] = sr_i8_pair(old[i], t0, t1, nw[i] << 16, nw[i]);
+        pr[i] = sr_i8_pair(old[i], t0, t1, nw[i], nw[i] << 16);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) out[i] = pack_sr_i8(pr[2 * i], pr[2 * i + 1]);

@@ -143,7 +143,7 @@ DEV void q8_tile(const Q8Args& a, const Q8Raw& raw, const Q8Ops<NKC>& in, uint8_
   uint32_t ob[9];
   ob[0] = (uint32_t)f16_bits(dq);
   if constexpr (SR) {
-    uint32_t nw[16];  // 65535 - h of element j in half (j & 1) of nw[j >> 1]
+    uint32_t nw[16];  // 65535 - h of element j in nw[j >> 1]: even j high half, odd j low half
     sr_nwords_aligned<32>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4)), nw);
     // integer stochastic rounding on the 13-bit grid (sr_i8_pair); pair i
     // holds codes 2i and 2i + 1 in bytes 0 and 2
@@ -151,7 +151,7 @@ DEV void q8_tile(const Q8Args& a, const Q8Raw& raw, const Q8Ops<NKC>& in, uint8_
 #pragma unroll
     for (int i = 0; i < 16; ++i)
       pr[i] = sr_i8_pair(nw[i], sr_i8_t(m[2 * i], id, 1536.0f, 1409.0f, 1663.0f),
-                         sr_i8_t(m[2 * i + 1], id, 1536.0f, 1409.0f, 1663.0f), nw[i] << 16, nw[i]);
+                         sr_i8_t(m[2 * i + 1], id, 1536.0f, 1409.0f, 1663.0f), nw[i], nw[i] << 16);
     // code j is byte 2 + j of the block: word (j + 2) >> 2
     ob[0] |= __builtin_amdgcn_perm(pr[0], pr[0], 0x06040c0cu);
 #pragma unroll

@@ -79,8 +79,8 @@ def test_sr_stream_uses_seven_rounds() -> None:
 
 
 def test_stream_layout_eight_halfwords_per_philox_call() -> None:
-    # element i uses half-word (i & 7) of Philox4x32-7(counter = i >> 3, key = seed):
-    # word j>>1, complemented when j>>1 is odd, low half for even j; u = h * 2^-16
+    # element i uses word j>>1 (j = i & 7) of Philox4x32-7(counter = i >> 3, key = seed),
+    # complemented when j>>1 is odd: its high half for even j, low half for odd j; u = h * 2^-16
     seed = O.derive_seed("layers.0.weight", 0)
     key = (seed & 0xFFFFFFFF, seed >> 32)
     start = (1 << 33) + 5  # counter above 2^32 exercises the high counter word
@@ -91,7 +91,7 @@ def test_stream_layout_eight_halfwords_per_philox_call() -> None:
         words = O.philox4x32((ctr & 0xFFFFFFFF, ctr >> 32, 0, 0), key, rounds=7)
         j = idx & 7
         w = words[j >> 1] ^ (0xFFFFFFFF if (j >> 1) & 1 else 0)
-        h = (w >> (16 * (j & 1))) & 0xFFFF
+        h = (w >> (16 * (1 - (j & 1)))) & 0xFFFF
         assert u[k] == np.float32(h / 65536.0)
 
 
