@@ -38,8 +38,10 @@ def _noalloc(q, s, b, a, strength, seed, q_out, s_out) -> int:  # noqa: ANN001
 
 @pytest.mark.parametrize("in_place", [False, True])
 def test_noalloc_equals_the_workspace_entry_point_on_consecutive_calls(in_place):
-    cases = [((4096, 4096), 32, 0.5, derive_seed("noalloc.first.weight", 0)),   # SR, rank 32
-             ((1000, 512), 16, -0.75, None)]                                    # smaller, RTN, ragged rows
+    cases = [((1000, 8192), 64, 1.0, derive_seed("noalloc.long.weight", 0)),  # two-pass rows (row slots in scratch)
+             ((300, 6144), 48, 0.5, derive_seed("noalloc.long.weight", 1)),    # smaller two-pass: stale slots would show
+             ((4096, 4096), 32, 0.5, derive_seed("noalloc.first.weight", 0)),  # SR, rank 32
+             ((1000, 512), 16, -0.75, None)]                                   # smaller, RTN, ragged rows
     for i, ((rows, cols), rank, strength, seed) in enumerate(cases):
         q, s = int8_initial(normal_bf16((rows, cols), 0.02, 50 + i))
         b, a = lora_factors(rows, cols, rank, 60 + i)
