@@ -8,12 +8,14 @@
 //   * e2m1 encodes use v_cvt_scalef32_pk_fp4_f32 with scale 1.0, which is
 //     round-to-nearest-even and therefore identical to the threshold chain of
 //     P/_triton_nvfp4_lora.py:55-85;
-//   * the per-element quotient v / s (INT8 stochastic rounding, FP8 and
-//     single-level NVFP4 quantization) is the IEEE-correct quotient computed
-//     as q0 = v*r, e = fma(-q0, s, v), q1 = fma(e, r, q0) with r = RN(1/s);
-//     this equals RN(v/s) for all bf16 and fp16 operands whose magnitudes
-//     and quotient lie in [2^-100, 2^100] (exhaustively checked on the CPU),
-//     the sign of a zero quotient is restored with copysign.
+//   * the per-element quotient v / s (FP8 and single-level NVFP4
+//     quantization) is the IEEE-correct quotient computed as q0 = v*r,
+//     e = fma(q0, s, -v), q1 = fma(-e, r, q0) with r = RN(1/s); this equals
+//     RN(v/s), the sign of a zero included, for all bf16 and fp16 operands
+//     whose magnitudes and quotient lie in [2^-100, 2^100] and for v = +-0
+//     (exhaustively checked on the CPU: tests/arith/identities.c).  The
+//     residual is taken negated so that v = -0 gives e = +0 and q1 =
+//     -0 * r + -0 = -0; the form with e = fma(-q0, s, v) loses that sign.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -132,10 +134,9 @@ DEV float round_runtime(float x, int dt) {
 
 // RN(v / s) given r = RN(1/s); see header comment for the validity domain.
 DEV float div_rn(float v, float s, float r) {
-  float q0 = v * r;
-  float e = __builtin_fmaf(-q0, s, v);
-  float q1 = __builtin_fmaf(e, r, q0);
-  return __builtin_copysignf(q1, q0);
+  const float q0 = v * r;
+  const float e = __builtin_fmaf(q0, s, -v);  // -(v - q0 s), exact
+  return __builtin_fmaf(-e, r, q0);
 }
 
 // A 16-byte global store whose data registers stay unwritten for two wait

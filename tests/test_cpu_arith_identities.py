@@ -1,6 +1,8 @@
-"""Exhaustive CPU check of an fp32 identity the HIP kernels use (tests/arith/identities.c):
-the two-instruction round-half-away of k_q8_fast, over every input of its
-domain (2.5e9 floats, about 10-15 s)."""
+"""Exhaustive CPU checks of fp32 identities the HIP kernels use (tests/arith/identities.c):
+the two-instruction round-half-away of k_q8_fast over every input of its
+domain (2.5e9 floats, about 10-15 s), and the three-instruction IEEE quotient
+of lm_device.h div_rn over every bf16 and every fp16 operand pair of its
+domain (1e9 and 2e9 pairs, about 11 and 15 s)."""
 
 from __future__ import annotations
 
@@ -24,7 +26,7 @@ def binary(tmp_path_factory) -> str:
     return out
 
 
-@pytest.mark.parametrize("identity", ["round"])
+@pytest.mark.parametrize("identity", ["round", "quotient_bf16", "quotient_f16"])
 def test_identity_holds_on_its_whole_domain(binary: str, identity: str) -> None:
     r = subprocess.run([binary, identity], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
