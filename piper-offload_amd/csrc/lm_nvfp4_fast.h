@@ -24,7 +24,8 @@
 //                 (bmax / 6) / g, 2^-6, 448)); codes = e2m1(merged * ((1/g)/s));
 //   The amax pass copies the input g into red[1] and the quant pass reads
 //   that copy, so the quant pass's first workgroup can write the output g
-//   even where it aliases the input.
+//   even where it aliases the input.  For a round-to-nearest stack both
+//   passes run in one launch (k_nv_fused_stack).
 // Single-level tensors skip the amax pass and divide by the block scale.
 #pragma once
 #include "lm_impl.h"
@@ -281,6 +282,13 @@ DEV void nv_quant_tile(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&b
 // code and scale loads, whose every instruction touches 16 rows: four
 // groups per wave, sharing the A^T loads further, measured the same.  Rows
 // row0 .. row0 + 31; the second group exists when row0 + 16 < M.
+// the copy of the input per-tensor scale in red[1]: a plain store when the
+// quant pass is a later launch, a device-scope atomic exchange when it runs in
+// the same launch (k_nv_fused_stack)
+DEV void nv_keep_gin(uint32_t* red, float gin, bool fused) {
+  if (fused) __hip_atomic_exchange(red + 1, f2u(gin), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else ((LM_GLOBAL uint32_t*)red)[1] = f2u(gin);
+}
 template <int NKC>
 struct NvAmaxIn {
   uint4 codes[2];
@@ -301,7 +309,7 @@ DEV void nv_amax_load(const NvLane<NKC>& l0, const NvLane<NKC>& l1, int mt, NvAm
   for (int k = 0; k < 8; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, t.aop[k]);
 }
 template <int NKC>
-DEV void nv_amax_body_direct(const NvArgs& a, int64_t row0, int t0, int t1) {
+DEV void nv_amax_body_direct(const NvArgs& a, int64_t row0, int t0, int t1, bool fused) {
   __shared__ float sh[NV_NW];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int64_t r0 = row0 + rl, r1 = row0 + 16 + rl;
@@ -310,7 +318,7 @@ DEV void nv_amax_body_direct(const NvArgs& a, int64_t row0, int t0, int t1) {
   const int ntiles = t1;
   const float gin = *(const LM_GLOBAL float*)a.gin;
   // the quant pass reads this copy: the per-tensor scale output may alias gin
-  if (row0 == 0 && t0 == 0 && threadIdx.x == 0) ((LM_GLOBAL uint32_t*)a.red)[1] = f2u(gin);
+  if (row0 == 0 && t0 == 0 && threadIdx.x == 0) nv_keep_gin(a.red, gin, fused);
   const float strength = a.strength;
   // rows past M read row M - 1 (valid memory) and are left out of the max
   const NvLane<NKC> l0 = nv_lane<NKC>(a, rok0 ? r0 : a.M - 1, lane);
@@ -366,7 +374,7 @@ DEV void nv_amax_body_direct(const NvArgs& a, int64_t row0, int t0, int t1) {
 // banks.
 constexpr int NV_CPITCH = 528, NV_SPITCH = 68;
 template <int NKC>
-DEV void nv_amax_body_lds(const NvArgs& a, int64_t row0, int t0, int t1) {
+DEV void nv_amax_body_lds(const NvArgs& a, int64_t row0, int t0, int t1, bool fused) {
   constexpr int RPAD = NKC * 16;
   __shared__ float sh[NV_NW];
   __shared__ __attribute__((aligned(16))) uint8_t lcodes[32 * NV_CPITCH];
@@ -377,7 +385,7 @@ DEV void nv_amax_body_lds(const NvArgs& a, int64_t row0, int t0, int t1) {
   const int64_t half = a.N >> 1, scols = a.N >> 4;
   const float gin = *(const LM_GLOBAL float*)a.gin;
   // the quant pass reads this copy: the per-tensor scale output may alias gin
-  if (row0 == 0 && t0 == 0 && threadIdx.x == 0) ((LM_GLOBAL uint32_t*)a.red)[1] = f2u(gin);
+  if (row0 == 0 && t0 == 0 && threadIdx.x == 0) nv_keep_gin(a.red, gin, fused);
   const float strength = a.strength;
   const bool second = row0 + 16 < a.M;  // workgroup-uniform
   // staging: thread tid loads code chunks q = tid, tid + 512 (row q >> 5,
@@ -475,27 +483,32 @@ DEV void nv_amax_body_lds(const NvArgs& a, int64_t row0, int t0, int t1) {
   }
 }
 // (the staged loads need 16-byte aligned codes and 8-byte aligned scales)
+// fused: the amax pass runs in the same launch as the quant pass
+// (k_nv_fused_stack), which reads the copy of gin as an atomic
 template <int NKC>
-DEV void nv_amax_body(const NvArgs& a, int64_t row0, int t0, int t1) {
+DEV void nv_amax_body(const NvArgs& a, int64_t row0, int t0, int t1, bool fused = false) {
   if (a.swizzled || (((uintptr_t)a.q) & 15) != 0 || (((uintptr_t)a.scale) & 7) != 0)
-    nv_amax_body_direct<NKC>(a, row0, t0, t1);
+    nv_amax_body_direct<NKC>(a, row0, t0, t1, fused);
   else
-    nv_amax_body_lds<NKC>(a, row0, t0, t1);
+    nv_amax_body_lds<NKC>(a, row0, t0, t1, fused);
 }
 
+// amax_bits, gin_bits: red[0] and red[1] as the amax pass left them (the
+// max |merged| and the copy of the input per-tensor scale); two-level only
 template <int NKC, bool TWO, bool SR>
-DEV void nv_quant_body(const NvArgs& a, int64_t row0, int t0, int t1, const float* rtab) {
+DEV void nv_quant_body(const NvArgs& a, int64_t row0, int t0, int t1, const float* rtab, uint32_t amax_bits,
+                       uint32_t gin_bits) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int64_t row = row0 + rl;
   const bool rok = row < a.M;
   const int64_t rowc = rok ? row : a.M - 1;
   const int ntiles = t1;
-  // the input per-tensor scale from the amax pass's copy (red[1]); the
-  // output one is written here, by one thread, since it may alias the input
-  const float gin = TWO ? u2f(((const LM_GLOBAL uint32_t*)a.red)[1]) : 1.0f;
+  // the input per-tensor scale from the amax pass's copy; the output one is
+  // written here, by one thread, since it may alias the input
+  const float gin = TWO ? u2f(gin_bits) : 1.0f;
   float gq = 1.0f, inv_g = 1.0f;
   if constexpr (TWO) {
-    gq = __builtin_fmaxf(u2f(*(const LM_GLOBAL uint32_t*)a.red) / 2688.0f, kEps);
+    gq = __builtin_fmaxf(u2f(amax_bits) / 2688.0f, kEps);
     inv_g = 1.0f / gq;
     if (row0 == 0 && t0 == 0 && threadIdx.x == 0 && a.gout != nullptr) *(LM_GLOBAL float*)a.gout = gq;
   }
@@ -528,9 +541,9 @@ DEV int nv_find(const NvStackItem* __restrict__ items, int count, int64_t t) {
 
 // ---- kernels: single tensor (args by value) and grouped (descriptor table) ---
 // One workgroup per 16 rows (tile_begin counts 16-row groups).
-static inline int64_t nv_units(int64_t M, int64_t /*N*/) { return (M + 15) / 16; }
+__host__ __device__ static inline int64_t nv_units(int64_t M, int64_t /*N*/) { return (M + 15) / 16; }
 // the amax pass: one workgroup per 32 rows
-static inline int64_t nv_pairs(int64_t M) { return (M + 31) / 32; }
+__host__ __device__ static inline int64_t nv_pairs(int64_t M) { return (M + 31) / 32; }
 
 // Single tensors: blocks are independent once the global scale is known, so a
 // workgroup owns 16 rows x NV_CHUNK macro tiles (blockIdx.y picks the chunk);
@@ -549,7 +562,9 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant(NvArgs a) {
   __shared__ float rtab[8];
   if (threadIdx.x < 8) rtab[threadIdx.x] = kRcpE4M3[threadIdx.x];
   __syncthreads();
-  nv_quant_body<NKC, TWO, SR>(a, (int64_t)blockIdx.x * 16, (int)blockIdx.y * NV_CHUNK, nv_chunk_end(a), rtab);
+  const LM_GLOBAL uint32_t* red = (const LM_GLOBAL uint32_t*)a.red;
+  nv_quant_body<NKC, TWO, SR>(a, (int64_t)blockIdx.x * 16, (int)blockIdx.y * NV_CHUNK, nv_chunk_end(a), rtab,
+                              TWO ? red[0] : 0u, TWO ? red[1] : 0u);
 }
 template <int NKC>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_amax_stack(const NvStackItem* __restrict__ items, int count) {
@@ -566,8 +581,119 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant_stack(const NvStackItem
   __syncthreads();
   const int i = nv_find(items, count, blockIdx.x);
   const NvArgs& a = items[i].a;
-  nv_quant_body<NKC, TWO, SR>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16, 0, (int)(a.N >> 7), rtab);
+  const LM_GLOBAL uint32_t* red = (const LM_GLOBAL uint32_t*)a.red;
+  nv_quant_body<NKC, TWO, SR>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16, 0, (int)(a.N >> 7), rtab,
+                              TWO ? red[0] : 0u, TWO ? red[1] : 0u);
 }
+// ---- grouped two-level stack in one launch ------------------------------------
+// The amax and quant passes of a round-to-nearest stack in one grid (the
+// host keeps two launches for stochastic rounding, where they measured
+// faster).  A workgroup takes the next ticket from a counter, so tickets are
+// handed out in order to running workgroups.  The tickets run through
+// segments, each covering all amax units (32 rows) or all quant units (16
+// rows) of one item.  An item's quant segment is placed at least
+// NV_LOOKAHEAD tickets after its last amax unit.  A quant unit waits until
+// the item's amax units have all published (red[2] counts them), which by
+// then they normally have.
+//   - Waiting cannot deadlock: every ticket before a quant unit's was taken
+//     by a running workgroup, and amax units wait on nothing.  The wait is
+//     bounded all the same (NV_SPIN_LIMIT polls); a unit that gives up sets
+//     the error word and stores nothing.
+//   - The texture-address-bound amax units and the quant units share the CUs
+//     instead of running one launch after the other.
+//   - An item's codes and scales are read twice within about NV_LOOKAHEAD
+//     units of work (~40 MB of 4096-column rows), so the second read can hit
+//     the 256 MB Infinity Cache.  (Measured per step on the 8B-shaped stack:
+//     4.35-4.37 ms at 512 tickets, 4.42 at 1024, 4.45 at 2048, 4.84 at 4096;
+//     4.84 at 256 and 5.45 at 128, where quant units wait; two launches
+//     4.76.  FETCH_SIZE, which counts L2 misses whether or not the Infinity
+//     Cache holds the line, reads the same as with two launches.)
+// Items must not share buffers (an item may be in place): a quant unit may
+// run while other items' amax units still read.
+struct NvSeg {
+  int32_t item;          // descriptor index
+  int32_t quant;         // 0: amax units, 1: quant units
+  int64_t ticket_begin;  // first ticket of the segment
+};
+constexpr int64_t NV_LOOKAHEAD = 512;
+constexpr uint32_t NV_SPIN_LIMIT = 1u << 22;  // polls of ~0.2 us: about a second
+
+// rank 16: both passes fit 128 VGPRs, two workgroups per CU
+template <int NKC>
+constexpr int nv_fused_min_waves() { return NKC == 1 ? 4 : 1; }
+template <int NKC>
+__global__ __launch_bounds__(NV_NW * 64, nv_fused_min_waves<NKC>()) void k_nv_fused_stack(const NvStackItem* __restrict__ items,
+                                                                  const NvSeg* __restrict__ segs, int nseg,
+                                                                  uint32_t* ctl) {
+  __shared__ float rtab[8];
+  __shared__ uint32_t sh_w[3];
+  if (threadIdx.x < 8) rtab[threadIdx.x] = kRcpE4M3[threadIdx.x];
+  if (threadIdx.x == 0) sh_w[0] = atomicAdd(ctl, 1u);
+  __syncthreads();
+  const int64_t t = sh_w[0];
+  int lo = 0, hi = nseg - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (segs[mid].ticket_begin <= t) lo = mid;
+    else hi = mid - 1;
+  }
+  const NvSeg sg = segs[lo];
+  const NvArgs& a = items[sg.item].a;
+  const int64_t unit = t - sg.ticket_begin;
+  uint32_t* red = a.red;
+  if (!sg.quant) {
+    nv_amax_body<NKC>(a, unit * 32, 0, (int)(a.N >> 7), true);
+    // Thread 0 made this unit's atomicMax (and unit 0's exchange of the gin
+    // copy), both device-scope atomics; once they are acknowledged, count the
+    // unit.  Everything a quant unit reads from red is an atomic, so no
+    // cache write-back or invalidation is needed (agent-scope release and
+    // acquire fences write back / invalidate the whole L2 of an XCD, which
+    // slowed the launch by a third).
+    if (threadIdx.x == 0) {
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // (flat atomics count in both)
+      __hip_atomic_fetch_add(red + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
+  if (threadIdx.x == 0) {
+    const uint32_t need = (uint32_t)nv_pairs(a.M);
+    uint32_t polls = 0;
+    while (__hip_atomic_load(red + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need && polls < NV_SPIN_LIMIT) {
+      __builtin_amdgcn_s_sleep(8);
+      ++polls;
+    }
+    const bool ok = polls < NV_SPIN_LIMIT;
+    if (!ok) __hip_atomic_fetch_or(ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh_w[0] = ok ? 1u : 0u;
+    sh_w[1] = __hip_atomic_load(red + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh_w[2] = __hip_atomic_load(red + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (sh_w[0] == 0u) return;
+  nv_quant_body<NKC, true, false>(a, unit * 16, 0, (int)(a.N >> 7), rtab, sh_w[1], sh_w[2]);
+}
+
+// Ticket order of the fused launch over the `n` two-level descriptors h[0,n):
+// amax segments in item order, each item's quant segment as soon as
+// NV_LOOKAHEAD tickets have followed its last amax unit (or no amax is left).
+// Returns the number of tickets; segs holds 2 n entries.
+static inline int64_t nv_schedule(const NvStackItem* h, int n, NvSeg* segs, int64_t* a_end) {
+  int64_t ticket = 0;
+  int ia = 0, iq = 0, k = 0;
+  while (iq < n) {
+    if (ia < n && (ia <= iq || ticket - a_end[iq] < NV_LOOKAHEAD)) {
+      segs[k++] = NvSeg{ia, 0, ticket};
+      ticket += nv_pairs(h[ia].a.M);
+      a_end[ia++] = ticket;
+    } else {
+      segs[k++] = NvSeg{iq, 1, ticket};
+      ticket += nv_units(h[iq].a.M, h[iq].a.N);
+      ++iq;
+    }
+  }
+  return ticket;
+}
+
 // bf16 factors, a rank bucket, whole macro tiles
 static inline bool nv_fast_ok(int cd, int nkc, int64_t N) { return cd == LM_BF16 && nkc > 0 && (N % 128) == 0; }
 

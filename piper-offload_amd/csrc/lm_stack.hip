@@ -172,20 +172,35 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
   return rc;
 }
 
-// Grouped NVFP4 merge: one amax launch over the two-level items, one quant
-// launch per scale level (two-level, single-level).  `dev_items` is workspace for the
-// descriptor table (fits in the BlkArgs region of lm_stack_workspace_extra).
+// Grouped NVFP4 merge.  Two-level items: round-to-nearest runs amax and
+// quant in one fused launch (k_nv_fused_stack), stochastic rounding one amax
+// launch and one quant launch.  Measured on the 8B-shaped stack (MI355X): the
+// fused launch takes round-to-nearest from 4.76 to 4.36 ms per step, but
+// stochastic rounding from 5.07 to 5.11 ms: its quant units keep the VALU
+// busy on their own (Philox), so the amax units' memory-bound phases have
+// nothing to hide behind.  Single-level items: one quant launch.
+// `dev_items` is workspace for the descriptor table (the BlkArgs region of
+// lm_stack_workspace_extra), `dev_segs` for the fused launch's ticket
+// segments (the RowStackItem region, unused by NVFP4).
 static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swizzled, bool sr, const PrepItem* preps,
-                         uint8_t* dev_items, hipStream_t st) {
+                         uint8_t* dev_items, uint8_t* dev_segs, hipStream_t st) {
   static_assert(sizeof(NvStackItem) <= sizeof(BlkArgs), "NVFP4 stack descriptors must fit the workspace slot");
+  static_assert(2 * sizeof(NvSeg) <= sizeof(RowStackItem), "NVFP4 ticket segments must fit the workspace slot");
   NvStackItem* h = (NvStackItem*)calloc(count, sizeof(NvStackItem));
-  if (!h) return fail(LM_EINVAL, "host allocation failed");
+  NvSeg* segs = (NvSeg*)calloc(2 * (size_t)count, sizeof(NvSeg));
+  int64_t* a_end = (int64_t*)calloc(count, sizeof(int64_t));
+  if (!h || !segs || !a_end) {
+    free(h);
+    free(segs);
+    free(a_end);
+    return fail(LM_EINVAL, "host allocation failed");
+  }
   // two-level items first, then single-level ones; each group numbers its
   // 16-row units from 0 and gets its own quant launch
   int n_two = 0;
   for (int i = 0; i < count; ++i) n_two += items[i].aux != nullptr ? 1 : 0;
   int64_t tiles[2] = {0, 0};
-  int64_t pairs = 0;  // 32-row units of the two-level items (amax launch)
+  int64_t pairs = 0;  // 32-row amax units of the two-level items
   int slot[2] = {0, n_two};
   int rc = LM_OK;
   for (int i = 0; i < count && rc == LM_OK; ++i) {
@@ -216,33 +231,52 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
     if (rc == LM_OK && swizzled) rc = zero_swizzle_pad((uint8_t*)s.scale_out, s.M, s.N / 16, st);
   }
   if (rc == LM_OK) rc = lm_stage_h2d(dev_items, h, sizeof(NvStackItem) * count, st);
+  int64_t tickets = 0;
+  const bool fused = !sr;
+  if (rc == LM_OK && n_two > 0 && fused) {
+    tickets = nv_schedule(h, n_two, segs, a_end);
+    if (tickets != pairs + tiles[0] || tickets > 0x7fffffff) rc = fail(LM_EUNSUPPORTED, "nvfp4 stack too large for one launch");
+    if (rc == LM_OK) rc = lm_stage_h2d(dev_segs, segs, sizeof(NvSeg) * 2 * n_two, st);
+  }
   const int nkc = preps[0].rpad / 16;
   const dim3 block(NV_NW * 64);
   const NvStackItem* d = (const NvStackItem*)dev_items;
-  if (rc == LM_OK && tiles[0] > 0) {
+  if (rc == LM_OK && n_two > 0 && !fused) {
     TimedLaunch timed("nvfp4", st);
-    const dim3 grid((unsigned)pairs);
-    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_amax_stack<NKC_>), grid, block, 0, st, d, n_two));
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_amax_stack<NKC_>), dim3((unsigned)pairs), block, 0, st, d, n_two));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 amax launch: %s", hipGetErrorString(e));
   }
-  if (rc == LM_OK) {
+  if (rc == LM_OK && n_two > 0 && !fused) {
     TimedLaunch timed("nvfp4", st);
-#define NQ(SR_, TWO_, D_, N_, T_)                                                                              \
-  NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, SR_, TWO_>), dim3((unsigned)(T_)), block, 0, \
-                                                 st, D_, N_))
-    if (tiles[0] > 0) {
-      if (sr) { NQ(true, true, d, n_two, tiles[0]); } else { NQ(false, true, d, n_two, tiles[0]); }
-    }
-    if (tiles[1] > 0) {
-      if (sr) { NQ(true, false, d + n_two, count - n_two, tiles[1]); }
-      else { NQ(false, false, d + n_two, count - n_two, tiles[1]); }
-    }
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, true, true>), dim3((unsigned)tiles[0]), block, 0,
+                                                   st, d, n_two));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 quant launch: %s", hipGetErrorString(e));
+  }
+  if (rc == LM_OK && n_two > 0 && fused) {
+    // ticket counter and error word: red[3] and red[4] of the first two-level
+    // item (cleared by the prep launch)
+    uint32_t* ctl = h[0].a.red + 3;
+    TimedLaunch timed("nvfp4", st);
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_fused_stack<NKC_>), dim3((unsigned)tickets), block, 0, st, d,
+                                                   (const NvSeg*)dev_segs, 2 * n_two, ctl));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 fused launch: %s", hipGetErrorString(e));
+  }
+  if (rc == LM_OK && tiles[1] > 0) {
+    TimedLaunch timed("nvfp4", st);
+#define NQ(SR_)                                                                                                 \
+  NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, SR_, false>), dim3((unsigned)tiles[1]), block, \
+                                                 0, st, d + n_two, count - n_two))
+    if (sr) { NQ(true); } else { NQ(false); }
 #undef NQ
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 quant launch: %s", hipGetErrorString(e));
   }
   free(h);
+  free(segs);
+  free(a_end);
   return rc;
 }
 
@@ -268,9 +302,9 @@ extern "C" int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, i
     fast = nv_fast_ok(items[i].lora.dtype, preps[i].rpad / 16, items[i].N) &&
            nkc_bucket(preps[i].rpad / 16) == nkc_bucket(preps[0].rpad / 16) && check_nvfp4(items[i].M, items[i].N) == 0;
   if (fast) {
+    uint8_t* dev_segs = base + align256((size_t)count * sizeof(PrepItem));
     rc = nv_stack_fast(items, count, swizzled, rounding_mode == LM_ROUND_STOCHASTIC, preps,
-                       base + align256((size_t)count * sizeof(PrepItem)) + align256((size_t)count * sizeof(RowStackItem)),
-                       st);
+                       dev_segs + align256((size_t)count * sizeof(RowStackItem)), dev_segs, st);
     free(preps);
     return rc;
   }
