@@ -260,7 +260,13 @@ DEV void philox_sr_n02(uint32_t lo, uint32_t hi, uint64_t seed, uint32_t (&c)[4]
   for (int r = 0; r < SR_ROUNDS; ++r) {
     const uint64_t pb = (uint64_t)c[2] * 0xCD9E8D57u;
     const uint64_t pa = (uint64_t)c[0] * 0xD2511F53u;
-    if (r < SR_ROUNDS - 1) {
+    if (r == 0) {
+      // c[2] = 0 makes the first word seed-only when the high counter word is
+      // wave-uniform: plain C keeps it (and the next round's product with it)
+      // on the scalar unit, where the builtin would move it to a VGPR
+      c[0] = (uint32_t)(pb >> 32) ^ c[1] ^ k0;
+      c[2] = __builtin_amdgcn_bitop3_b32((uint32_t)(pa >> 32), c[3], k1, 0x96);
+    } else if (r < SR_ROUNDS - 1) {
       c[0] = __builtin_amdgcn_bitop3_b32((uint32_t)(pb >> 32), c[1], k0, 0x96);
       c[2] = __builtin_amdgcn_bitop3_b32((uint32_t)(pa >> 32), c[3], k1, 0x96);
     } else {
@@ -271,6 +277,59 @@ DEV void philox_sr_n02(uint32_t lo, uint32_t hi, uint64_t seed, uint32_t (&c)[4]
     c[3] = (uint32_t)pa;
     k0 += 0x9E3779B9u;
     k1 += 0xBB67AE85u;
+  }
+}
+// philox_sr_n02 of the counter (lo, 0): with the high word zero the first
+// round's word 0 is the key itself, so round 2's A product and round 3's
+// word 3 are wave-uniform.  Written out, the compiler keeps them (and their
+// XOR with the round keys) on the scalar unit: three fewer VALU operations
+// per call, and no per-call v_mul_hi_u32 / v_mul_lo_u32 of the seed.
+DEV void philox_sr_n02_lo(uint32_t lo, uint64_t seed, uint32_t (&c)[4]) {
+  constexpr uint32_t MA = 0xD2511F53u, MB = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+  // round 1 of (lo, 0, 0, 0): the B product is 0
+  uint64_t pa = (uint64_t)lo * MA;
+  uint64_t pb;
+  c[0] = k0;
+  c[1] = 0u;
+  c[2] = (uint32_t)(pa >> 32) ^ k1;
+  c[3] = (uint32_t)pa;
+  k0 += W0;
+  k1 += W1;
+  // round 2: c[0] and c[1] are uniform
+  pb = (uint64_t)c[2] * MB;
+  pa = (uint64_t)c[0] * MA;
+  c[0] = (uint32_t)(pb >> 32) ^ k0;
+  c[2] = c[3] ^ ((uint32_t)(pa >> 32) ^ k1);
+  c[1] = (uint32_t)pb;
+  c[3] = (uint32_t)pa;
+  k0 += W0;
+  k1 += W1;
+  // round 3: c[3] is uniform
+  pb = (uint64_t)c[2] * MB;
+  pa = (uint64_t)c[0] * MA;
+  c[0] = __builtin_amdgcn_bitop3_b32((uint32_t)(pb >> 32), c[1], k0, 0x96);
+  c[2] = (uint32_t)(pa >> 32) ^ (c[3] ^ k1);
+  c[1] = (uint32_t)pb;
+  c[3] = (uint32_t)pa;
+  k0 += W0;
+  k1 += W1;
+#pragma unroll
+  for (int r = 3; r < SR_ROUNDS; ++r) {
+    pb = (uint64_t)c[2] * MB;
+    pa = (uint64_t)c[0] * MA;
+    const int op = r < SR_ROUNDS - 1 ? 0x96 : 0x69;  // XNOR in the last round
+    if (op == 0x96) {
+      c[0] = __builtin_amdgcn_bitop3_b32((uint32_t)(pb >> 32), c[1], k0, 0x96);
+      c[2] = __builtin_amdgcn_bitop3_b32((uint32_t)(pa >> 32), c[3], k1, 0x96);
+    } else {
+      c[0] = __builtin_amdgcn_bitop3_b32((uint32_t)(pb >> 32), c[1], k0, 0x69);
+      c[2] = __builtin_amdgcn_bitop3_b32((uint32_t)(pa >> 32), c[3], k1, 0x69);
+    }
+    c[1] = (uint32_t)pb;
+    c[3] = (uint32_t)pa;
+    k0 += W0;
+    k1 += W1;
   }
 }
 // The stream: element idx draws the 16-bit h from word k = (idx & 7) >> 1 of
@@ -285,7 +344,7 @@ DEV void sr_nwords16_even(uint64_t seed, uint32_t ctr, uint32_t (&nw)[8]) {
 #pragma unroll
   for (int gi = 0; gi < 2; ++gi) {
     uint32_t c[4];
-    philox_sr_n02(ctr | (uint32_t)gi, 0u, seed, c);
+    philox_sr_n02_lo(ctr | (uint32_t)gi, seed, c);
     nw[4 * gi + 0] = c[0];
     nw[4 * gi + 1] = c[1];
     nw[4 * gi + 2] = c[2];
