@@ -368,6 +368,20 @@ DEV void sr_nwords_aligned(uint64_t seed, uint64_t idx0, uint32_t (&nw)[SPAN / 2
     nw[4 * gi + 3] = c[3];
   }
 }
+// the same for idx0 < 2^35, whose counters fit the low word
+// (philox_sr_n02_lo); the fast block-format kernels require M N <= 2^35
+template <int SPAN>
+DEV void sr_nwords_aligned_lo(uint64_t seed, uint32_t ctr, uint32_t (&nw)[SPAN / 2]) {
+#pragma unroll
+  for (int gi = 0; gi < SPAN / 8; ++gi) {
+    uint32_t c[4];
+    philox_sr_n02_lo(ctr | (uint32_t)gi, seed, c);
+    nw[4 * gi + 0] = c[0];
+    nw[4 * gi + 1] = c[1];
+    nw[4 * gi + 2] = c[2];
+    nw[4 * gi + 3] = c[3];
+  }
+}
 // 16-bit uniform integers h for offsets idx0 .. idx0+SPAN-1 (u = h * 2^-16)
 DEV uint32_t sr_h_of(const uint32_t (&c)[4], int j) {
   const uint32_t w = ((j >> 1) & 1) ? ~c[j >> 1] : c[j >> 1];

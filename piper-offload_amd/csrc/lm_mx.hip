@@ -28,7 +28,7 @@ extern "C" int lm_mx_merge(uint8_t* q, uint8_t* scale, int64_t M, int64_t N, int
   if ((rc = check_rounding(rounding))) return rc;
   Ctx c;
   if ((rc = setup(c, M, N, lora, workspace, workspace_bytes, stream))) return rc;
-  if (mx_fast_ok(lora->dtype, c.nkc, N)) {
+  if (mx_fast_ok(lora->dtype, c.nkc, M, N)) {
     MxArgs ma;
     ma.q = q;
     ma.scale = scale;

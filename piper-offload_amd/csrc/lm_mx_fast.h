@@ -125,7 +125,7 @@ DEV void mx_tile(const MxArgs& a, const MxTileIn<ELEM, NKC>& in, const v4i16 (&b
   float inv;
   const uint32_t enc = mx_scale(amax, a.mode, MxTraits<ELEM>::emax, L, MxTraits<ELEM>::mbits, inv);
   uint32_t nw[16];  // complemented Philox words
-  if constexpr (SR) sr_nwords_aligned<32>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4)), nw);
+  if constexpr (SR) sr_nwords_aligned_lo<32>(a.seed, (uint32_t)((row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4)) >> 3), nw);
   float x[32];
 #pragma unroll
   for (int j = 0; j < 32; ++j) {
@@ -184,7 +184,10 @@ __global__ __launch_bounds__(NV_NW * 64) void k_mx_fast(MxArgs a) {
   }
 }
 
-static inline bool mx_fast_ok(int cd, int nkc, int64_t N) { return cd == LM_BF16 && nkc > 0 && (N % 128) == 0; }
+// (M N <= 2^35: the stochastic-rounding counters, offset / 8, fit 32 bits)
+static inline bool mx_fast_ok(int cd, int nkc, int64_t M, int64_t N) {
+  return cd == LM_BF16 && nkc > 0 && (N % 128) == 0 && M * N <= (int64_t(1) << 35);
+}
 
 static int mx_fast_run(const MxArgs& a, int elem, int nkc, bool sr, hipStream_t st) {
   const dim3 grid((unsigned)((a.M + 15) / 16), (unsigned)(((a.N >> 7) + NV_CHUNK - 1) / NV_CHUNK)), block(NV_NW * 64);

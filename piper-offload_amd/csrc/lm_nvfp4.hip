@@ -27,7 +27,7 @@ static int nvfp4_common(const uint8_t* q, const uint8_t* scale, const float* pts
   a.aux_out = pts_out;
   a.swizzled = swz;
   if (swz && (rc = zero_swizzle_pad(scale_out, M, N / 16, c.st))) return rc;
-  if (lora && !dense && nv_fast_ok(cd, c.nkc, N)) {
+  if (lora && !dense && nv_fast_ok(cd, c.nkc, M, N)) {
     NvArgs na;
     na.q = q;
     na.scale = scale;

@@ -208,7 +208,7 @@ DEV void nv_quant_block(const NvArgs& a, int64_t row, int mt, int lane, float gq
                         const float (&m)[16], uint32_t (&words)[4], uint32_t& scb) {
   uint32_t nw[8];  // complemented Philox words
   if constexpr (SR)
-    sr_nwords_aligned<16>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4) + 16 * B), nw);
+    sr_nwords_aligned_lo<16>(a.seed, (uint32_t)((row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4) + 16 * B) >> 3), nw);
   // bmax over the bf16-rounded values = bf16(max |m|) (rounding is monotone)
   float mb[16];
   float bmax = 0.0f;
@@ -695,7 +695,10 @@ static inline int64_t nv_schedule(const NvStackItem* h, int n, NvSeg* segs, int6
 }
 
 // bf16 factors, a rank bucket, whole macro tiles
-static inline bool nv_fast_ok(int cd, int nkc, int64_t N) { return cd == LM_BF16 && nkc > 0 && (N % 128) == 0; }
+// (M N <= 2^35: the stochastic-rounding counters, offset / 8, fit 32 bits)
+static inline bool nv_fast_ok(int cd, int nkc, int64_t M, int64_t N) {
+  return cd == LM_BF16 && nkc > 0 && (N % 128) == 0 && M * N <= (int64_t(1) << 35);
+}
 
 // single tensor: amax (two-level), then quant on `st`
 static int nv_fast_run(const NvArgs& a, int nkc, bool sr, hipStream_t st) {

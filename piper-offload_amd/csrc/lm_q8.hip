@@ -19,7 +19,7 @@ extern "C" int lm_q8_0_merge(const uint8_t* packed, uint8_t* packed_out, int64_t
   if ((rc = check_rounding(rounding))) return rc;
   Ctx c;
   if ((rc = setup(c, M, N, lora, workspace, workspace_bytes, stream))) return rc;
-  if (q8_fast_ok(lora->dtype, c.nkc, N)) {
+  if (q8_fast_ok(lora->dtype, c.nkc, M, N)) {
     Q8Args qa;
     qa.q = packed;
     qa.q_out = packed_out;

@@ -144,7 +144,7 @@ DEV void q8_tile(const Q8Args& a, const Q8Raw& raw, const Q8Ops<NKC>& in, uint8_
   ob[0] = (uint32_t)f16_bits(dq);
   if constexpr (SR) {
     uint32_t nw[16];  // 65535 - h of element j in nw[j >> 1]: even j high half, odd j low half
-    sr_nwords_aligned<32>(a.seed, (uint64_t)(row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4)), nw);
+    sr_nwords_aligned_lo<32>(a.seed, (uint32_t)((row * a.N + (int64_t)mt * 128 + 32 * (lane >> 4)) >> 3), nw);
     // integer stochastic rounding on the 13-bit grid (sr_i8_pair); pair i
     // holds codes 2i and 2i + 1 in bytes 0 and 2
     uint32_t pr[16];
@@ -308,7 +308,10 @@ static unsigned q8_resident_grid() {
   return v;
 }
 
-static inline bool q8_fast_ok(int cd, int nkc, int64_t N) { return cd == LM_BF16 && nkc > 0 && (N % 128) == 0; }
+// (M N <= 2^35: the stochastic-rounding counters, offset / 8, fit 32 bits)
+static inline bool q8_fast_ok(int cd, int nkc, int64_t M, int64_t N) {
+  return cd == LM_BF16 && nkc > 0 && (N % 128) == 0 && M * N <= (int64_t(1) << 35);
+}
 
 static int q8_fast_run(const Q8Args& a, int nkc, bool sr, hipStream_t st) {
   const int64_t nitems = ((a.M + 15) / 16) * (a.N >> 7);

@@ -299,7 +299,7 @@ extern "C" int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, i
   if (rc == LM_OK) rc = stack_prep(preps, count, base, st);
   bool fast = rc == LM_OK;
   for (int i = 0; fast && i < count; ++i)
-    fast = nv_fast_ok(items[i].lora.dtype, preps[i].rpad / 16, items[i].N) &&
+    fast = nv_fast_ok(items[i].lora.dtype, preps[i].rpad / 16, items[i].M, items[i].N) &&
            nkc_bucket(preps[i].rpad / 16) == nkc_bucket(preps[0].rpad / 16) && check_nvfp4(items[i].M, items[i].N) == 0;
   if (fast) {
     uint8_t* dev_segs = base + align256((size_t)count * sizeof(PrepItem));
