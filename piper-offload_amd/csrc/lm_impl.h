@@ -973,12 +973,34 @@ __global__ __launch_bounds__(SPLIT_NW * 64) void k_rows_split(RowArgs a, int wg_
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) block(rb, mt, cur[rb], d[rb]);
   };
+  // The amax pass holds two row blocks' deltas instead of RB: row block rb
+  // is merged while rb + 1's MFMAs run, each row block's next codes are
+  // requested as soon as its current ones are merged, and the next A^T
+  // operands once the last MFMA has read them.
+  auto tile_amax = [&](int mt, int next) {
+    float d[2][16];
+    fast_tile_delta<NKC>(aop, bop[0], d[0]);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      if (rb + 1 < RB) fast_tile_delta<NKC>(aop, bop[rb + 1], d[(rb + 1) & 1]);
+      else if (next >= 0) fast_load_aop<NKC>(L[0], next, aop);
+      float m[16];
+      fast_merge_vals<KIND, true>(a, raw[rb], d[rb & 1], s_in[rb], m, amax[rb]);
+      if (next >= 0) raw[rb] = fast_load_codes(L[rb], next);
+    }
+  };
   load(t0);
   if (t0 + TS * (TPW - 1) < ntiles) {
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) tile(t0 + TS * i, i + 1 < TPW ? t0 + TS * (i + 1) : -1);
+    for (int i = 0; i < TPW; ++i) {
+      if constexpr (QUANT) tile(t0 + TS * i, i + 1 < TPW ? t0 + TS * (i + 1) : -1);
+      else tile_amax(t0 + TS * i, i + 1 < TPW ? t0 + TS * (i + 1) : -1);
+    }
   } else {
-    for (int mt = t0; mt < ntiles; mt += TS) tile(mt, mt + TS < ntiles ? mt + TS : -1);
+    for (int mt = t0; mt < ntiles; mt += TS) {
+      if constexpr (QUANT) tile(mt, mt + TS < ntiles ? mt + TS : -1);
+      else tile_amax(mt, mt + TS < ntiles ? mt + TS : -1);
+    }
   }
   if constexpr (!QUANT) {
 #pragma unroll
