@@ -3,7 +3,7 @@
 // N % 128 == 0.  P/ = the reference's src/piper_offload/.
 //
 // Same decomposition as the NVFP4 kernels: a 512-thread workgroup owns 16
-// rows and a chunk of 16 macro tiles (blockIdx.y), wave w walks the
+// rows and a chunk of MX_CHUNK macro tiles (blockIdx.y), wave w walks the
 // 128-column macro tiles chunk + w, chunk + w + 8, ..., and a lane holds row
 // (lane & 15) and the 32 columns 32*(lane >> 4) .. +31 of a macro tile --
 // exactly one MX block, so the block max, the shared exponent and the codes
@@ -162,14 +162,18 @@ DEV void mx_tile(const MxArgs& a, const MxTileIn<ELEM, NKC>& in, const v4i16 (&b
   so[0] = (uint8_t)enc;
 }
 
+// Chunks of 16 tiles: for MXFP4 [14336, 4096] whole 32-tile rows measured
+// 0.0398 ms per step (stochastic) against 0.0379 (round-to-nearest 0.0326
+// against 0.0330).
+constexpr int MX_CHUNK = 2 * NV_NW;
 template <int ELEM, int NKC, bool SR>
 __global__ __launch_bounds__(NV_NW * 64) void k_mx_fast(MxArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int64_t row = (int64_t)blockIdx.x * 16 + rl;
   const bool rok = row < a.M;
   const int64_t rowc = rok ? row : a.M - 1;  // in-bounds loads; results dropped
-  const int t0 = (int)blockIdx.y * NV_CHUNK;  // this workgroup's chunk of macro tiles
-  const int ntiles = (int)((a.N >> 7) < t0 + NV_CHUNK ? (a.N >> 7) : t0 + NV_CHUNK);
+  const int t0 = (int)blockIdx.y * MX_CHUNK;  // this workgroup's chunk of macro tiles
+  const int ntiles = (int)((a.N >> 7) < t0 + MX_CHUNK ? (a.N >> 7) : t0 + MX_CHUNK);
   const MxLane<ELEM, NKC> l = mx_lane<ELEM, NKC>(a, rowc, lane);
   v4i16 bop[NKC];
   load_bop<NKC>(a.bp, row, lane, bop);  // Bp holds ceil(M/16)*16 rows
@@ -190,7 +194,7 @@ static inline bool mx_fast_ok(int cd, int nkc, int64_t M, int64_t N) {
 }
 
 static int mx_fast_run(const MxArgs& a, int elem, int nkc, bool sr, hipStream_t st) {
-  const dim3 grid((unsigned)((a.M + 15) / 16), (unsigned)(((a.N >> 7) + NV_CHUNK - 1) / NV_CHUNK)), block(NV_NW * 64);
+  const dim3 grid((unsigned)((a.M + 15) / 16), (unsigned)(((a.N >> 7) + MX_CHUNK - 1) / MX_CHUNK)), block(NV_NW * 64);
   TimedLaunch timed("mx", st);
 #define MXL(E_, SR_) NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_mx_fast<E_, NKC_, SR_>), grid, block, 0, st, a))
   if (elem == LM_E2M1) { if (sr) { MXL(E2M1, true); } else { MXL(E2M1, false); } }
