@@ -257,7 +257,10 @@ int lm_routed_residual(const void* x, const void* y, void* out, int64_t T, int64
 
 /* ---------------- stacks: many targets, one grouped launch ------------
  * `items` is a HOST array of `count` descriptors.  Each target gets its own
- * seed (derive_seed(param_path, merge_index)). */
+ * seed (derive_seed(param_path, merge_index)).  An item's outputs may alias
+ * its own inputs (in place); items must not share buffers with each other
+ * (the NVFP4 round-to-nearest stack runs one item's quantization while
+ * other items are still being read). */
 typedef struct lm_stack_item {
   const void* q;        /* packed codes in */
   const void* scale;    /* scales in */
