@@ -377,8 +377,10 @@ template <int NKC>
 DEV void nv_amax_body_lds(const NvArgs& a, int64_t row0, int t0, int t1, bool fused) {
   constexpr int RPAD = NKC * 16;
   __shared__ float sh[NV_NW];
-  __shared__ __attribute__((aligned(16))) uint8_t lcodes[32 * NV_CPITCH];
-  __shared__ __attribute__((aligned(16))) uint8_t lsc[32 * NV_SPITCH];
+  // two buffers: step s reads buffer s & 1 while the next step's bytes go to
+  // the other one, so a step needs one barrier
+  __shared__ __attribute__((aligned(16))) uint8_t lcodes[2][32 * NV_CPITCH];
+  __shared__ __attribute__((aligned(16))) uint8_t lsc[2][32 * NV_SPITCH];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, rl = lane & 15, g = lane >> 4;
   const int ntiles = t1;
   const int steps = (ntiles - t0 + NV_NW - 1) / NV_NW;  // workgroup-uniform
@@ -407,11 +409,11 @@ DEV void nv_amax_body_lds(const NvArgs& a, int64_t row0, int t0, int t1, bool fu
       ss = *(const LM_GLOBAL lm_u32x2*)(sb + rowc(tid >> 3) * scols + (int64_t)tc * 8);
     }
   };
-  auto publish = [&]() {
-    *(lm_u32x4*)(lcodes + (tid >> 5) * NV_CPITCH + (tid & 31) * 16) = sc0;
-    *(lm_u32x4*)(lcodes + ((tid + 512) >> 5) * NV_CPITCH + (tid & 31) * 16) = sc1;
+  auto publish = [&](int b) {
+    *(lm_u32x4*)(lcodes[b] + (tid >> 5) * NV_CPITCH + (tid & 31) * 16) = sc0;
+    *(lm_u32x4*)(lcodes[b] + ((tid + 512) >> 5) * NV_CPITCH + (tid & 31) * 16) = sc1;
     if (tid < 256) {
-      uint32_t* d = (uint32_t*)(lsc + (tid >> 3) * NV_SPITCH + (tid & 7) * 8);
+      uint32_t* d = (uint32_t*)(lsc[b] + (tid >> 3) * NV_SPITCH + (tid & 7) * 8);
       d[0] = ss.x;
       d[1] = ss.y;
     }
@@ -437,9 +439,11 @@ DEV void nv_amax_body_lds(const NvArgs& a, int64_t row0, int t0, int t1, bool fu
   v4i16 aop[8][NKC];
   stage(t0);
   load_aop(t0, aop);
-  publish();
+  publish(0);
   __syncthreads();
   for (int s = 0; s < steps; ++s) {
+    const uint8_t* lc = lcodes[s & 1];
+    const uint8_t* ls = lsc[s & 1];
     const int ts = t0 + s * NV_NW;
     if (s + 1 < steps) stage(ts + NV_NW);
     v4i16 nxt[8][NKC];
@@ -448,22 +452,23 @@ DEV void nv_amax_body_lds(const NvArgs& a, int64_t row0, int t0, int t1, bool fu
       const int cofs = wave * 64 + 16 * g, sofs = wave * 8 + 2 * g;
       float m[32];
       {
-        const lm_u32x4 c = *(const lm_u32x4*)(lcodes + rl * NV_CPITCH + cofs);
-        const uint32_t scv = *(const uint16_t*)(lsc + rl * NV_SPITCH + sofs);
+        const lm_u32x4 c = *(const lm_u32x4*)(lc + rl * NV_CPITCH + cofs);
+        const uint32_t scv = *(const uint16_t*)(ls + rl * NV_SPITCH + sofs);
         nv_merged_parts<NKC, true>(make_uint4(c.x, c.y, c.z, c.w), scv, aop, bop0, strength, gin, m);
 #pragma unroll
         for (int j = 0; j < 32; j += 2) mx0 = max3_abs(mx0, m[j], m[j + 1]);
       }
       if (second) {
-        const lm_u32x4 c = *(const lm_u32x4*)(lcodes + (16 + rl) * NV_CPITCH + cofs);
-        const uint32_t scv = *(const uint16_t*)(lsc + (16 + rl) * NV_SPITCH + sofs);
+        const lm_u32x4 c = *(const lm_u32x4*)(lc + (16 + rl) * NV_CPITCH + cofs);
+        const uint32_t scv = *(const uint16_t*)(ls + (16 + rl) * NV_SPITCH + sofs);
         nv_merged_parts<NKC, true>(make_uint4(c.x, c.y, c.z, c.w), scv, aop, bop1, strength, gin, m);
 #pragma unroll
         for (int j = 0; j < 32; j += 2) mx1 = max3_abs(mx1, m[j], m[j + 1]);
       }
     }
-    __syncthreads();  // every wave has read this step's LDS
-    if (s + 1 < steps) publish();
+    // the other buffer was last read in step s - 1, before the barrier that
+    // ended it; after this one, step s + 1 may read it
+    if (s + 1 < steps) publish((s + 1) & 1);
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 8; ++k)
