@@ -518,6 +518,11 @@ DEV uint32_t sr_fp8(float v, uint32_t h, float /*limit*/) { return cvt_sr_fp8<FM
 // stale registers depending on timing.  The compiled kernels are checked for
 // both by csrc/check_asm_hazards.py (make check-asm).
 //
+// the wave's index in its workgroup, as a wave-uniform (scalar) value: from
+// threadIdx.x alone the compiler treats it as per-lane, and every address
+// derived from it (tile offsets) then costs 64-bit VALU adds per tile
+DEV int wave_index() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 // max(acc, |a|, |b|) in one v_max3_f32 (IEEE maxNum: a NaN operand is
 // ignored, as fmaxf does).  Written as asm because the builtin form makes the
 // compiler add canonicalizing maxima of loop-carried values (+2-4% VALU

@@ -407,7 +407,7 @@ __device__ __forceinline__ void rows_body(const RowArgs& a, int64_t row0, int sc
   __shared__ float sh_mx[NW][16];
   __shared__ float sh_mn[NW][16];
   __shared__ float sh_qp[4][16];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15, g = lane >> 4;
+  const int lane = threadIdx.x & 63, wave = wave_index(), rl = lane & 15, g = lane >> 4;
   const int64_t row = row0 + rl;
   const bool rok = row < a.M;
   const int64_t N = a.N;
@@ -740,7 +740,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   __shared__ float sh_mx[16][NW];
   __shared__ lm_u32x4 lcache[LCACHE > 0 ? LCACHE : 1][NW][2][64];
   constexpr int PF = PF_ < CACHE ? PF_ : CACHE;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
+  const int lane = threadIdx.x & 63, wave = wave_index(), rl = lane & 15;
   const int64_t row = row0 + rl;
   const bool rok = row < a.M;
   // rows past M load row M-1 (valid memory); their results are never stored
@@ -893,6 +893,7 @@ __global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_row
 static constexpr int SPLIT_NW = 4;
 template <int KIND, bool SR, int NKC, int RB, int TPW, bool QUANT, int IL = 0>
 __global__ __launch_bounds__(SPLIT_NW * 64) void k_rows_split(RowArgs a, int wg_per_group) {
+  // (the per-lane wave index: wave_index() left the VALU count unchanged)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int ntiles = (int)(a.N >> 6);
   const int64_t grp = blockIdx.x / wg_per_group;
@@ -1345,7 +1346,7 @@ __global__ __launch_bounds__(256) void k_blocks(BlkArgs a) {
   constexpr int SPAN = BlkTraits<F>::SPAN;
   constexpr int MTW = 4 * SPAN;
   __shared__ float sh_red[2][4];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15, g = lane >> 4;
+  const int lane = threadIdx.x & 63, wave = wave_index(), rl = lane & 15, g = lane >> 4;
   const int64_t M = a.M, N = a.N;
   const int ntiles = (int)((N + MTW - 1) / MTW);
   const int tpw = a.tpw;

@@ -168,6 +168,7 @@ DEV void mx_tile(const MxArgs& a, const MxTileIn<ELEM, NKC>& in, const v4i16 (&b
 constexpr int MX_CHUNK = 2 * NV_NW;
 template <int ELEM, int NKC, bool SR>
 __global__ __launch_bounds__(NV_NW * 64) void k_mx_fast(MxArgs a) {
+  // (the per-lane wave index: wave_index() measured 2.7% slower here)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
   const int64_t row = (int64_t)blockIdx.x * 16 + rl;
   const bool rok = row < a.M;

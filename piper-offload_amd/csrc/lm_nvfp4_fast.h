@@ -311,7 +311,7 @@ DEV void nv_amax_load(const NvLane<NKC>& l0, const NvLane<NKC>& l1, int mt, NvAm
 template <int NKC>
 DEV void nv_amax_body_direct(const NvArgs& a, int64_t row0, int t0, int t1, bool fused) {
   __shared__ float sh[NV_NW];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
+  const int lane = threadIdx.x & 63, wave = wave_index(), rl = lane & 15;
   const int64_t r0 = row0 + rl, r1 = row0 + 16 + rl;
   const bool rok0 = r0 < a.M, rok1 = r1 < a.M;
   const bool second = row0 + 16 < a.M;  // wave-uniform
@@ -381,7 +381,7 @@ DEV void nv_amax_body_lds(const NvArgs& a, int64_t row0, int t0, int t1, bool fu
   // the other one, so a step needs one barrier
   __shared__ __attribute__((aligned(16))) uint8_t lcodes[2][32 * NV_CPITCH];
   __shared__ __attribute__((aligned(16))) uint8_t lsc[2][32 * NV_SPITCH];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, rl = lane & 15, g = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(), rl = lane & 15, g = lane >> 4;
   const int ntiles = t1;
   const int steps = (ntiles - t0 + NV_NW - 1) / NV_NW;  // workgroup-uniform
   const int64_t half = a.N >> 1, scols = a.N >> 4;
@@ -503,7 +503,7 @@ DEV void nv_amax_body(const NvArgs& a, int64_t row0, int t0, int t1, bool fused 
 template <int NKC, bool TWO, bool SR>
 DEV void nv_quant_body(const NvArgs& a, int64_t row0, int t0, int t1, const float* rtab, uint32_t amax_bits,
                        uint32_t gin_bits) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
+  const int lane = threadIdx.x & 63, wave = wave_index(), rl = lane & 15;
   const int64_t row = row0 + rl;
   const bool rok = row < a.M;
   const int64_t rowc = rok ? row : a.M - 1;

@@ -114,7 +114,7 @@ __device__ __forceinline__ v4f32 mfma1(const v4i16& a, const v4i16& b, const v4f
 template <bool HALF>
 __global__ __launch_bounds__(RT_NW * 64) void k_routed_down(RoutedArgs a) {
   __shared__ float sh[RT_NW][64][4];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15, g = lane >> 4;
+  const int lane = threadIdx.x & 63, wave = wave_index(), rl = lane & 15, g = lane >> 4;
   const int64_t t0 = (int64_t)blockIdx.x * 16;
   const int split = blockIdx.y;
   const int64_t kb = (int64_t)split * a.kspan, ke = kb + a.kspan < a.K ? kb + a.kspan : a.K;
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256) void k_routed_finalize(RoutedArgs a) {
 template <bool HALF, int CMAX>
 __global__ __launch_bounds__(RT_NW * 64) void k_routed_up(RoutedArgs a) {
   constexpr int DT = HALF ? F16 : BF16;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15, g = lane >> 4;
+  const int lane = threadIdx.x & 63, wave = wave_index(), rl = lane & 15, g = lane >> 4;
   const int64_t mt = (int64_t)blockIdx.x * RT_NW + wave;  // the wave's column tile
   const int64_t ntiles = (a.N + 63) / 64;
   if (mt >= ntiles) return;
@@ -305,7 +305,7 @@ __global__ __launch_bounds__(RT_SNW * 64) void k_routed_small(RoutedArgs a) {
   constexpr bool PRE = CMAX <= 2;  // B operands loaded up front
   __shared__ float sh[RT_SNW][64][4];
   __shared__ uint32_t spw[16][RT_MAX_CHUNKS * 8];      // ps of token t: ranks 2j, 2j + 1 in word j
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15, g = lane >> 4;
+  const int lane = threadIdx.x & 63, wave = wave_index(), rl = lane & 15, g = lane >> 4;
   const int64_t mt = (int64_t)blockIdx.x * RT_SNW + wave;
   const bool tile = mt < (a.N + 63) / 64;
   const int64_t c0 = mt * 64 + 16 * g, t = rl;
