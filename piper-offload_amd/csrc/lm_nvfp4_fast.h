@@ -624,7 +624,7 @@ struct NvSeg {
   int64_t ticket_begin;  // first ticket of the segment
 };
 constexpr int64_t NV_LOOKAHEAD = 512;
-constexpr uint32_t NV_SPIN_LIMIT = 1u << 22;  // polls of ~0.2 us: about a second
+constexpr uint32_t NV_SPIN_LIMIT = 1u << 20;  // polls of up to ~3 us: a few seconds
 
 // rank 16: both passes fit 128 VGPRs, two workgroups per CU
 template <int NKC>
@@ -667,7 +667,10 @@ __global__ __launch_bounds__(NV_NW * 64, nv_fused_min_waves<NKC>()) void k_nv_fu
     const uint32_t need = (uint32_t)nv_pairs(a.M);
     uint32_t polls = 0;
     while (__hip_atomic_load(red + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need && polls < NV_SPIN_LIMIT) {
-      __builtin_amdgcn_s_sleep(8);
+      // back off: many waiting workgroups polling one counter slow every
+      // other access (small stacks, where most quant units do wait)
+      const uint32_t reps = polls < 16 ? 1u : (polls < 64 ? 4u : 16u);
+      for (uint32_t k = 0; k < reps; ++k) __builtin_amdgcn_s_sleep(8);
       ++polls;
     }
     const bool ok = polls < NV_SPIN_LIMIT;
