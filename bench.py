@@ -529,7 +529,7 @@ def cpu_baseline(kind: str, stochastic: bool, budget_s: float, gguf_type: str = 
 
     INT8 workloads run the reference's portable merge (dequantize, addmm_,
     requantize; oracle/portable.py) with torch CPU ops on every core of this
-    process's affinity, as BASELINE.md prescribes: one warm-up, then repeats
+    process's affinity (the reference's own CPU fallback): one warm-up, then repeats
     until the budget is spent (at least 5), and the median repeat is reported.
     GGUF runs the oracle's dequantize (C, OpenMP).
     """
