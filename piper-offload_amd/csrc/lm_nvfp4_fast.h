@@ -606,7 +606,8 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant_stack(const NvStackItem
 //   - Waiting cannot deadlock: every ticket before a quant unit's was taken
 //     by a running workgroup, and amax units wait on nothing.  The wait is
 //     bounded all the same (NV_SPIN_LIMIT polls); a unit that gives up sets
-//     the error word and stores nothing.
+//     the stack workspace's status word (lm_stack_status_offset) and stores
+//     nothing.
 //   - The texture-address-bound amax units and the quant units share the CUs
 //     instead of running one launch after the other.
 //   - An item's codes and scales are read twice within about NV_LOOKAHEAD
@@ -625,6 +626,16 @@ struct NvSeg {
 };
 constexpr int64_t NV_LOOKAHEAD = 512;
 constexpr uint32_t NV_SPIN_LIMIT = 1u << 20;  // polls of up to ~3 us: a few seconds
+// The fused launch's bounded wait: a quant unit polls at most spin_limit
+// times for need + extra_need finished amax units (extra_need is 0 except
+// under lm_debug_stack_wait, which lets a test make every wait give up while
+// each wave still ends normally).  A unit that gives up stores nothing and
+// sets bit 0 of the caller-visible status word.
+struct NvWait {
+  uint32_t* status;      // sticky status word of the stack workspace
+  uint32_t spin_limit;
+  uint32_t extra_need;
+};
 
 // rank 16: both passes fit 128 VGPRs, two workgroups per CU
 template <int NKC>
@@ -632,9 +643,12 @@ constexpr int nv_fused_min_waves() { return NKC == 1 ? 4 : 1; }
 template <int NKC>
 __global__ __launch_bounds__(NV_NW * 64, nv_fused_min_waves<NKC>()) void k_nv_fused_stack(const NvStackItem* __restrict__ items,
                                                                   const NvSeg* __restrict__ segs, int nseg,
-                                                                  uint32_t* ctl) {
+                                                                  uint32_t* ctl, NvWait wt) {
   __shared__ float rtab[8];
-  __shared__ uint32_t sh_w[3];
+  // [0] the ticket (read by every thread after the first barrier), [1] [2]
+  // the amax words, [3] the quant unit's go / give-up flag: separate slots, so
+  // no thread can read a ticket that the flag has overwritten
+  __shared__ uint32_t sh_w[4];
   if (threadIdx.x < 8) rtab[threadIdx.x] = kRcpE4M3[threadIdx.x];
   if (threadIdx.x == 0) sh_w[0] = atomicAdd(ctl, 1u);
   __syncthreads();
@@ -664,23 +678,25 @@ __global__ __launch_bounds__(NV_NW * 64, nv_fused_min_waves<NKC>()) void k_nv_fu
     return;
   }
   if (threadIdx.x == 0) {
-    const uint32_t need = (uint32_t)nv_pairs(a.M);
+    const uint32_t need = (uint32_t)nv_pairs(a.M) + wt.extra_need;
     uint32_t polls = 0;
-    while (__hip_atomic_load(red + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need && polls < NV_SPIN_LIMIT) {
+    uint32_t done = __hip_atomic_load(red + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    while (done < need && polls < wt.spin_limit) {
       // back off: many waiting workgroups polling one counter slow every
       // other access (small stacks, where most quant units do wait)
       const uint32_t reps = polls < 16 ? 1u : (polls < 64 ? 4u : 16u);
       for (uint32_t k = 0; k < reps; ++k) __builtin_amdgcn_s_sleep(8);
       ++polls;
+      done = __hip_atomic_load(red + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    const bool ok = polls < NV_SPIN_LIMIT;
-    if (!ok) __hip_atomic_fetch_or(ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sh_w[0] = ok ? 1u : 0u;
+    const bool ok = done >= need;
+    if (!ok) __hip_atomic_fetch_or(wt.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh_w[3] = ok ? 1u : 0u;
     sh_w[1] = __hip_atomic_load(red + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     sh_w[2] = __hip_atomic_load(red + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  if (sh_w[0] == 0u) return;
+  if (sh_w[3] == 0u) return;
   nv_quant_body<NKC, true, false>(a, unit * 16, 0, (int)(a.N >> 7), rtab, sh_w[1], sh_w[2]);
 }
 

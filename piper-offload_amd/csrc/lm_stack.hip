@@ -4,9 +4,22 @@
 // ---------------------------------------------------------------------------
 // stacks
 // ---------------------------------------------------------------------------
-extern "C" size_t lm_stack_workspace_extra(int32_t count) {
+// Stack workspace: the descriptor tables, then one 256-byte block whose first
+// word is the caller-visible status word (never cleared by the library), then
+// 256 bytes of slack, then the per-item regions.
+static size_t stack_status_off(int32_t count) {
   return align256((size_t)count * sizeof(PrepItem)) + align256((size_t)count * sizeof(RowStackItem)) +
-         align256((size_t)count * sizeof(BlkArgs)) + 256;
+         align256((size_t)count * sizeof(BlkArgs));
+}
+extern "C" size_t lm_stack_workspace_extra(int32_t count) { return stack_status_off(count) + 512; }
+extern "C" size_t lm_stack_status_offset(int32_t count) { return stack_status_off(count); }
+
+// test hook for the fused NVFP4 launch's bounded wait (see NvWait)
+static uint32_t g_spin_limit = NV_SPIN_LIMIT, g_extra_need = 0;
+extern "C" int lm_debug_stack_wait(uint32_t spin_limit, uint32_t extra_need) {
+  g_spin_limit = spin_limit;
+  g_extra_need = extra_need;
+  return LM_OK;
 }
 
 static int stack_layout(const lm_stack_item* items, int32_t count, void* ws, size_t wsb, PrepItem* preps,
@@ -183,7 +196,7 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
 // lm_stack_workspace_extra), `dev_segs` for the fused launch's ticket
 // segments (the RowStackItem region, unused by NVFP4).
 static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swizzled, bool sr, const PrepItem* preps,
-                         uint8_t* dev_items, uint8_t* dev_segs, hipStream_t st) {
+                         uint8_t* dev_items, uint8_t* dev_segs, uint32_t* status, hipStream_t st) {
   static_assert(sizeof(NvStackItem) <= sizeof(BlkArgs), "NVFP4 stack descriptors must fit the workspace slot");
   static_assert(2 * sizeof(NvSeg) <= sizeof(RowStackItem), "NVFP4 ticket segments must fit the workspace slot");
   NvStackItem* h = (NvStackItem*)calloc(count, sizeof(NvStackItem));
@@ -255,12 +268,13 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 quant launch: %s", hipGetErrorString(e));
   }
   if (rc == LM_OK && n_two > 0 && fused) {
-    // ticket counter and error word: red[3] and red[4] of the first two-level
-    // item (cleared by the prep launch)
+    // ticket counter: red[3] of the first two-level item (cleared by the
+    // prep launch); a quant unit that gives up waiting sets *status
     uint32_t* ctl = h[0].a.red + 3;
+    const NvWait wt{status, g_spin_limit, g_extra_need};
     TimedLaunch timed("nvfp4", st);
     NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_fused_stack<NKC_>), dim3((unsigned)tickets), block, 0, st, d,
-                                                   (const NvSeg*)dev_segs, 2 * n_two, ctl));
+                                                   (const NvSeg*)dev_segs, 2 * n_two, ctl, wt));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 fused launch: %s", hipGetErrorString(e));
   }
@@ -304,7 +318,8 @@ extern "C" int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, i
   if (fast) {
     uint8_t* dev_segs = base + align256((size_t)count * sizeof(PrepItem));
     rc = nv_stack_fast(items, count, swizzled, rounding_mode == LM_ROUND_STOCHASTIC, preps,
-                       dev_segs + align256((size_t)count * sizeof(RowStackItem)), dev_segs, st);
+                       dev_segs + align256((size_t)count * sizeof(RowStackItem)), dev_segs,
+                       (uint32_t*)(base + stack_status_off(count)), st);
     free(preps);
     return rc;
   }

@@ -31,7 +31,7 @@ from torch import nn
 
 from .lora import LoRA, LoRATransform, ScaledLoRAFactor
 from .registry import param_representation, param_tensor_id
-from .stack import StackPlan, StackTarget
+from .stack import StackTarget, merge_once
 
 logger = logging.getLogger(__name__)
 
@@ -166,7 +166,7 @@ def _apply(targets: list[_Target]) -> None:
         if len(members) == 1:  # one tensor: its single-target launch is the tuned path
             alone.append(members[0][0])
             continue
-        StackPlan([st for _t, st in members], kind).merge(stochastic=rest[-1])
+        merge_once([st for _t, st in members], kind, stochastic=rest[-1])
         for target, _st in members:
             target.transform.advance()
             if target.bias is not None:

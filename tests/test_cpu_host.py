@@ -277,3 +277,51 @@ def test_pinned_lora_factors_share_one_arena():
                                 "attn.lora_B.weight": lora32.targets["attn.weight"].b}, dtype=torch.bfloat16)
     assert f32.targets["attn.weight"].a.dtype is torch.bfloat16
     assert torch.equal(f32.targets["attn.weight"].a, lora32.targets["attn.weight"].a.to(torch.bfloat16))
+
+
+# ---- stack plans: items must not share buffers ---------------------------------
+def _nv_cpu(rows: int, cols: int, pts: torch.Tensor | None = None, q: torch.Tensor | None = None):  # noqa: ANN202
+    from piper_offload_amd import NVFP4Weight
+
+    q = torch.zeros(rows, cols // 2, dtype=torch.uint8) if q is None else q
+    s = torch.zeros(rows, cols // 16, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    return NVFP4Weight(q, s, pts, 16, torch.bfloat16, False)
+
+
+@pytest.mark.parametrize("case", ["same_weight", "shared_global", "fused_view", "int8_same"])
+def test_stack_plan_rejects_items_that_share_buffers(case: str) -> None:
+    from piper_offload_amd import Int8Weight
+    from piper_offload_amd.stack import StackPlan, StackTarget
+
+    b = torch.zeros(32, 16, dtype=torch.bfloat16)
+    a = torch.zeros(16, 64, dtype=torch.bfloat16)
+    if case == "same_weight":
+        w = _nv_cpu(32, 64, torch.ones(()))
+        targets, kind = [StackTarget(w, b, a, 1.0), StackTarget(w, b, a, 1.0)], "nvfp4"
+    elif case == "shared_global":
+        g = torch.ones(())
+        targets, kind = [StackTarget(_nv_cpu(32, 64, g), b, a, 1.0), StackTarget(_nv_cpu(32, 64, g), b, a, 1.0)], "nvfp4"
+    elif case == "fused_view":
+        fused = torch.zeros(64, 32, dtype=torch.uint8)  # two views over one fused q/k tensor, overlapping by a row
+        targets = [StackTarget(_nv_cpu(32, 64, torch.ones(()), fused[:32]), b, a, 1.0),
+                   StackTarget(_nv_cpu(32, 64, torch.ones(()), fused[31:63]), b, a, 1.0)]
+        kind = "nvfp4"
+    else:
+        q = torch.zeros(32, 64, dtype=torch.int8)
+        s = torch.ones(32, 1)
+        w = Int8Weight(q, s, (1, 64), torch.bfloat16)
+        targets, kind = [StackTarget(w, b, a, 1.0), StackTarget(Int8Weight(q, torch.ones(32, 1), (1, 64), torch.bfloat16),
+                                                                 b, a, 1.0)], "int8"
+    with pytest.raises(ValueError, match="must not share buffers"):
+        StackPlan(targets, kind)
+
+
+def test_stack_plan_overlap_check_passes_disjoint_views() -> None:
+    # adjacent, non-overlapping views of one buffer are fine (the check stops at the ValueError stage on CPU)
+    from piper_offload_amd.stack import StackTarget, _reject_shared_buffers
+
+    fused = torch.zeros(64, 32, dtype=torch.uint8)
+    b = torch.zeros(32, 16, dtype=torch.bfloat16)
+    a = torch.zeros(16, 64, dtype=torch.bfloat16)
+    _reject_shared_buffers([StackTarget(_nv_cpu(32, 64, torch.ones(()), fused[:32]), b, a, 1.0),
+                            StackTarget(_nv_cpu(32, 64, torch.ones(()), fused[32:]), b, a, 1.0)])

@@ -333,3 +333,52 @@ def test_stack_plan_merges_on_two_streams_run_in_order():
         m = mismatch_report(t.weight.qdata.cpu().numpy(), rq.numpy(), f"item {i} codes", 64)
         assert not m, m
         assert torch.equal(t.weight.scale.cpu().reshape(-1), rs.reshape(-1))
+
+
+# ---- the fused NVFP4 launch's bounded wait ---------------------------------------
+def test_nvfp4_fused_stack_give_up_is_reported():
+    """Force every quant unit of the fused round-to-nearest launch to give up its bounded wait (the test
+    hook asks for amax units that never come, with a budget of 4 polls, so every wave still ends
+    normally): the merge must be reported incomplete at the next check, and a normal merge afterwards
+    must match the oracle again."""
+    from piper_offload_amd import _lib
+    from piper_offload_amd.stack import check_stack_status
+
+    lib = _lib.lib()
+    shapes = [(256, 512), (128, 1024), (64, 256)]
+    targets, expected = [], []
+    for i, (rows, cols) in enumerate(shapes):
+        b, a = lora_factors(rows, cols, 16, 700 + i)
+        b, a = b.to(DEV), a.to(DEV)
+        w = _nvfp4_weight(rows, cols, 710 + i, True, False)
+        targets.append(StackTarget(w, b, a, 1.0, derive_seed(f"give_up.{i}.weight", 0)))
+    plan = StackPlan(targets, "nvfp4")
+    before = [t.weight.qdata.clone() for t in targets]
+    assert lib.lm_debug_stack_wait(4, 1 << 20) == 0
+    try:
+        plan.merge(stochastic=False)
+    finally:
+        assert lib.lm_debug_stack_wait(1 << 20, 0) == 0
+    with pytest.raises(RuntimeError, match="incomplete"):
+        plan.synchronize()
+    # nothing was quantized: the codes are untouched
+    for t, q0 in zip(targets, before):
+        assert torch.equal(t.weight.qdata, q0)
+    plan.synchronize()  # the error was reported once and the status word cleared
+    for t in targets:
+        expected.append(_nvfp4_oracle(t.weight, t.b, t.a, t.strength, t.seed, False))
+    plan.merge(stochastic=False)
+    plan.synchronize()
+    errors = []
+    for i, (t, exp) in enumerate(zip(targets, expected)):
+        errors += _nvfp4_errors("stack", i, t.weight.qdata, t.weight.scale, t.weight.per_tensor_scale, exp)
+    assert not errors, "\n".join(errors)
+    # the one-shot path reports through check_stack_status
+    assert lib.lm_debug_stack_wait(4, 1 << 20) == 0
+    try:
+        merge_nvfp4_stack(targets, stochastic=False)
+    finally:
+        assert lib.lm_debug_stack_wait(1 << 20, 0) == 0
+    with pytest.raises(RuntimeError, match="incomplete"):
+        check_stack_status()
+    check_stack_status()
