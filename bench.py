@@ -527,11 +527,14 @@ def _cpu_model() -> str:
 def cpu_baseline(kind: str, stochastic: bool, budget_s: float, gguf_type: str = "Q4_K") -> dict | None:
     """Time the CPU path on the host cores, on a bounded sample of the workload.
 
-    INT8 workloads run the reference's portable merge (dequantize, addmm_,
-    requantize; oracle/portable.py) with torch CPU ops on every core of this
-    process's affinity (the reference's own CPU fallback): one warm-up, then repeats
-    until the budget is spent (at least 5), and the median repeat is reported.
-    GGUF runs the oracle's dequantize (C, OpenMP).
+    Merge workloads run the reference's portable merge of their format
+    (dequantize, addmm_, requantize; oracle/portable.py) with torch CPU ops on
+    every core of this process's affinity (the reference's own CPU fallback) on
+    one tensor of the workload's shape: INT8 (stacks, reload, api), FP8, NVFP4
+    (single and stack), MXFP4, Q8_0.  GGUF runs the oracle's dequantize (C,
+    OpenMP); routed runs the residual in torch CPU ops; copy and h2d a torch CPU
+    copy of the same bytes.  One warm-up, then repeats until the budget is spent
+    (at least 3), and the median repeat is reported.
     """
     if budget_s <= 0:
         return None
@@ -567,6 +570,81 @@ def cpu_baseline(kind: str, stochastic: bool, budget_s: float, gguf_type: str = 
         what = (f"reference portable path in torch CPU ops (dequantize, addmm_, requantize, "
                 f"{'stochastic' if stochastic else 'round-to-nearest'}) of one {rows} x {cols} gate_proj-shaped "
                 f"INT8 tensor, rank {rank}")
+    elif kind in ("fp8", "nvfp4", "nvfp4_stack", "mxfp4", "q8_0"):
+        from oracle import portable as P
+
+        if kind == "fp8":
+            rows, cols, rank, strength, label = 8192, 8192, 64, 1.0, "config-3 [8192, 8192] e4m3fn per-row"
+        elif kind == "q8_0":
+            rows, cols, rank, strength, label = 13824, 5120, 16, 1.0, "config-4 [13824, 5120] GGUF Q8_0"
+        else:
+            rank, strength = 16, 1.0
+            label = f"{rows} x {cols} gate_proj-shaped " + ("MXFP4 (FLOOR scales)" if kind == "mxfp4" else
+                                                          "two-level NVFP4")
+        g = torch.Generator(device="cpu").manual_seed(derive_seed(path, 0) % (1 << 63))
+        w = (torch.randn((rows, cols), generator=g) * 0.02).to(torch.bfloat16)
+        a = (torch.randn((rank, cols), generator=g) / rank).to(torch.bfloat16)
+        b = (torch.randn((rows, rank), generator=g) * 0.01).to(torch.bfloat16)
+        seeds = iter(range(1 << 30))
+
+        def seed() -> int | None:
+            return derive_seed(path, next(seeds)) if stochastic else None
+
+        if kind == "fp8":
+            q, sc = P.fp8_requant(w)
+
+            def run() -> None:
+                P.fp8_merge(q, sc, b, a, strength, rounding_seed=seed())
+
+            nbytes = 2 * rows * cols + 8 * rows + 2 * rank * (rows + cols)
+        elif kind == "q8_0":
+            pk = P.q8_0_requant(w)
+
+            def run() -> None:
+                P.q8_0_merge(pk, cols, b, a, strength, rounding_seed=seed())
+
+            nbytes = 2 * rows * (cols // 32 * 34) + 2 * rank * (rows + cols)
+        elif kind == "mxfp4":
+            q, sc = P.mxfp4_requant(w)
+
+            def run() -> None:
+                P.mxfp4_merge(q, sc, b, a, strength, rounding_seed=seed())
+
+            nbytes = 2 * (rows * cols // 2 + rows * cols // 32) + 2 * rank * (rows + cols)
+        else:
+            q, sc, gs = P.nvfp4_requant(w)
+
+            def run() -> None:
+                P.nvfp4_merge(q, sc, gs, b, a, strength, rounding_seed=seed())
+
+            nbytes = _nvfp4_bytes(rows, cols, rank)
+        del w
+        what = (f"reference portable path in torch CPU ops (dequantize, addmm_, requantize, "
+                f"{'stochastic' if stochastic else 'round-to-nearest'}) of one {label} tensor, rank {rank}")
+    elif kind == "routed":
+        tokens, K_, N_, rank = 4096, 4096, 14336, 16
+        g = torch.Generator(device="cpu").manual_seed(11)
+        x = torch.randn((tokens, K_), generator=g).to(torch.bfloat16)
+        y = (torch.randn((tokens, N_), generator=g) * 0.5).to(torch.bfloat16)
+        a = (torch.randn((rank, K_), generator=g) / rank).to(torch.bfloat16)
+        b = (torch.randn((N_, rank), generator=g) * 0.01).to(torch.bfloat16)
+
+        def run() -> None:
+            # P/lora.py:801-829: y + strength * ((x A^T) B^T), torch CPU ops
+            torch.addmm(y, x @ a.t(), b.t(), alpha=1.0)
+
+        nbytes = 2 * (tokens * K_ + 2 * tokens * N_ + rank * (K_ + N_))
+        what = f"routed residual y + (x A^T) B^T in torch CPU ops, {tokens} tokens x [4096 -> 14336], rank 16"
+    elif kind in ("copy", "h2d"):
+        src = torch.empty(1 << 28, dtype=torch.int32)
+        src.fill_(7)
+        dst = torch.empty_like(src)
+
+        def run() -> None:
+            dst.copy_(src)
+
+        nbytes = 2 * src.numel() * 4
+        what = "torch CPU copy 1 GiB -> 1 GiB"
     elif kind == "gguf":
         import oracle as O
 
@@ -586,7 +664,7 @@ def cpu_baseline(kind: str, stochastic: bool, budget_s: float, gguf_type: str = 
     run()  # warm-up: first touch of the buffers and the thread pool
     times: list[float] = []
     t_start = time.perf_counter()
-    while len(times) < 5 or time.perf_counter() - t_start < budget_s:
+    while len(times) < 3 or time.perf_counter() - t_start < budget_s:
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
