@@ -93,7 +93,19 @@ struct PrepItem {
   int64_t work_begin;  // prefix of per-item work units (k_prep1: 0)
   int64_t block_begin; // prefix of per-item k_prep_many workgroups
   int vec_b;           // B rows load 4 ranks at once (ldb, rank % 4 == 0, 8-byte aligned)
+  int at_rows16;       // rank 16, At in the row kernels' tile order (at_rows16_offset)
 };
+
+// At for the per-row kernels at rank <= 16 (RPAD 16): per 64-column tile,
+// 1024 elements ordered [h][lane][kk][i], so that lane l's A^T fragments of
+// the tile's 4 MFMAs (k = 2h + kk) arrive in two 16-byte loads, each load
+// of the wave covering 1 KiB contiguously.  Lane l = p + 16 g takes column
+// 16 (p >> 2) + 4 k + (p & 3) of the tile at ranks 4 g + i (the same
+// columns and ranks as the plain At[col][g][kc][i] order).
+__host__ __device__ inline int64_t at_rows16_offset(int64_t col, int g) {
+  const int c = (int)(col & 63), k = (c >> 2) & 3, lane = ((c >> 4) << 2) + (c & 3) + 16 * g;
+  return (col >> 6) * 1024 + (((k >> 1) * 64 + lane) * 2 + (k & 1)) * 4;
+}
 
 __device__ __forceinline__ void prep_unit(const PrepItem& it, int64_t u) {
   // units: [0, Npad*rpad/4) for At, then [.., + Mpad*rpad/4) for Bp, then 1
@@ -115,7 +127,8 @@ __device__ __forceinline__ void prep_unit(const PrepItem& it, int64_t u) {
       v[i] = (k < it.rank && col < it.N) ? ((const LM_GLOBAL uint16_t*)it.a)[(int64_t)k * it.lda + col] : (uint16_t)0;
     }
     const lm_u32x2 w = {(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16)};
-    *(LM_GLOBAL lm_u32x2*)((LM_GLOBAL uint16_t*)it.at + col * it.rpad + (g * nkc + kc) * 4) = w;
+    const int64_t off = it.at_rows16 ? at_rows16_offset(col, g) : col * it.rpad + (g * nkc + kc) * 4;
+    *(LM_GLOBAL lm_u32x2*)((LM_GLOBAL uint16_t*)it.at + off) = w;
     return;
   }
   u -= n_at;
@@ -574,16 +587,17 @@ struct FastLane {
   uint32_t ctr;                  // Philox counter of the lane's first offset in tile 0 (even)
 };
 
-template <int NKC>
+template <int NKC, bool R16 = false>
 __device__ __forceinline__ FastLane fast_lane(const RowArgs& a, int64_t rowc, int lane) {
   constexpr int RPAD = NKC * 16;
+  static_assert(!R16 || NKC == 1, "the rows16 operand order is for rank 16");
   const int p = lane & 15, g = lane >> 4;
   FastLane L;
   L.q = (const LM_GLOBAL uint8_t*)a.q;
   L.out = (LM_GLOBAL uint8_t*)a.q_out;
   L.at = (const LM_GLOBAL uint16_t*)a.at;
   L.off = (uint32_t)rowc * (uint32_t)a.N + 16u * (uint32_t)g;
-  L.aoff = (uint32_t)((16 * (p >> 2) + (p & 3)) * RPAD + g * (NKC * 4));
+  L.aoff = R16 ? (uint32_t)lane * 8u : (uint32_t)((16 * (p >> 2) + (p & 3)) * RPAD + g * (NKC * 4));
   // N % 64 == 0: off / 8 is even, so the lane's second Philox block (offsets
   // +8 .. +15) is counter | 1; rows past M never store, so their counter is moot
   L.ctr = L.off >> 3;
@@ -594,17 +608,26 @@ __device__ __forceinline__ uint4 fast_load_codes(const FastLane& L, int mt) {
   const lm_u32x4 raw = *(const LM_GLOBAL lm_u32x4*)(L.q + (uint32_t)(mt * 64) + L.off);
   return make_uint4(raw.x, raw.y, raw.z, raw.w);
 }
-template <int NKC>
+template <int NKC, bool R16 = false>
 __device__ __forceinline__ void fast_load_aop(const FastLane& L, int mt, v4i16 (&aop)[4][NKC]) {
   constexpr int RPAD = NKC * 16;
   const LM_GLOBAL uint16_t* at = L.at + (uint32_t)(mt * (64 * RPAD)) + L.aoff;
+  if constexpr (R16) {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, aop[k]);
+    for (int h = 0; h < 2; ++h) {
+      const lm_u32x4 w = *(const LM_GLOBAL lm_u32x4*)(at + 512 * h);
+      aop[2 * h][0] = __builtin_bit_cast(v4i16, lm_u32x2{w.x, w.y});
+      aop[2 * h + 1][0] = __builtin_bit_cast(v4i16, lm_u32x2{w.z, w.w});
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, aop[k]);
+  }
 }
-template <int NKC>
+template <int NKC, bool R16 = false>
 __device__ __forceinline__ void fast_load_tile(const FastLane& L, int mt, FastTileIn<NKC>& t) {
   t.raw = fast_load_codes(L, mt);
-  fast_load_aop<NKC>(L, mt, t.aop);
+  fast_load_aop<NKC, R16>(L, mt, t.aop);
 }
 
 // the 16 deltas of a lane's share of one 16 x 64 tile (4 MFMA chains)
@@ -735,7 +758,8 @@ constexpr int fast_prefetch() { return NKC == 1 ? 4 : 2; }
 // LCACHE: merged tiles per wave kept in LDS after the register cache (2 KiB
 // each: [half][lane][4 words], so the two 16-byte writes of a lane are
 // consecutive across lanes); tiles beyond CACHE + LCACHE are merged twice.
-template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0>
+template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0,
+          bool R16 = false>
 __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   __shared__ float sh_mx[16][NW];
   __shared__ lm_u32x4 lcache[LCACHE > 0 ? LCACHE : 1][NW][2][64];
@@ -746,7 +770,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   // rows past M load row M-1 (valid memory); their results are never stored
   const int64_t rowc = rok ? row : a.M - 1;
   const int ntiles = (int)(a.N >> 6);
-  const FastLane L = fast_lane<NKC>(a, rowc, lane);
+  const FastLane L = fast_lane<NKC, R16>(a, rowc, lane);
   v4i16 bop[NKC];
   load_bop<NKC>(a.bp, row, lane, bop);
   const float s_in = rok ? ((const LM_GLOBAL float*)a.scale)[row] : 0.0f;
@@ -762,11 +786,11 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
 #pragma unroll
     for (int i = 0; i < CACHE; ++i) raw[i] = fast_load_codes(L, wave + i * NW);
 #pragma unroll
-    for (int i = 0; i < PF; ++i) fast_load_aop<NKC>(L, wave + i * NW, aop[i]);
+    for (int i = 0; i < PF; ++i) fast_load_aop<NKC, R16>(L, wave + i * NW, aop[i]);
 #pragma unroll
     for (int i = 0; i < CACHE; ++i) {
       fast_merged_tile<KIND, NKC>(a, raw[i], aop[i % PF], bop, s_in, cache[i], amax);
-      if (i + PF < CACHE) fast_load_aop<NKC>(L, wave + (i + PF) * NW, aop[i % PF]);
+      if (i + PF < CACHE) fast_load_aop<NKC, R16>(L, wave + (i + PF) * NW, aop[i % PF]);
     }
   } else {
 #pragma unroll
@@ -774,7 +798,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
       const int mt = wave + i * NW;
       if (mt < ntiles) {
         FastTileIn<NKC> in;
-        fast_load_tile<NKC>(L, mt, in);
+        fast_load_tile<NKC, R16>(L, mt, in);
         fast_merged_tile<KIND, NKC>(a, in.raw, in.aop, bop, s_in, cache[i], amax);
       }
     }
@@ -784,11 +808,11 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   // of them are kept in LDS
   if (wave + CACHE * NW < ntiles) {
     FastTileIn<NKC> cur;
-    fast_load_tile<NKC>(L, wave + CACHE * NW, cur);
+    fast_load_tile<NKC, R16>(L, wave + CACHE * NW, cur);
     int l = 0;
     for (int mt = wave + CACHE * NW; mt < ntiles; mt += NW, ++l) {
       FastTileIn<NKC> nxt;
-      fast_load_tile<NKC>(L, mt + NW < ntiles ? mt + NW : mt, nxt);
+      fast_load_tile<NKC, R16>(L, mt + NW < ntiles ? mt + NW : mt, nxt);
       uint32_t t[8];
       fast_merged_tile<KIND, NKC>(a, cur.raw, cur.aop, bop, s_in, t, amax);
       if (LCACHE > 0 && l < LCACHE) {
@@ -835,10 +859,10 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   }
   if (wave + (CACHE + LCACHE) * NW < ntiles) {
     FastTileIn<NKC> cur;
-    fast_load_tile<NKC>(L, wave + (CACHE + LCACHE) * NW, cur);
+    fast_load_tile<NKC, R16>(L, wave + (CACHE + LCACHE) * NW, cur);
     for (int mt = wave + (CACHE + LCACHE) * NW; mt < ntiles; mt += NW) {
       FastTileIn<NKC> nxt;
-      fast_load_tile<NKC>(L, mt + NW < ntiles ? mt + NW : mt, nxt);
+      fast_load_tile<NKC, R16>(L, mt + NW < ntiles ? mt + NW : mt, nxt);
       uint32_t t[8];
       float unused = 0.0f;
       fast_merged_tile<KIND, NKC>(a, cur.raw, cur.aop, bop, s_in, t, unused);
@@ -857,17 +881,39 @@ template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch
 __global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_rows_fast(RowArgs a) {
   rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_, LCACHE>(a, (int64_t)blockIdx.x * 16);
 }
-template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0>
-__global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_rows_fast_stack(const RowStackItem* __restrict__ items, int count) {
-  int lo = 0, hi = count - 1;
-  const int64_t t = blockIdx.x;
-  while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
-    if (items[mid].tile_begin <= t) lo = mid;
-    else hi = mid - 1;
+// The item that owns 16-row group t: the last of the `count` ascending first
+// groups begins[] that is <= t.  Every lane compares four entries per pass
+// of 256 (one 16-byte load from a table that stays in L2) and the wave counts
+// them with ballots, instead of a chain of dependent scalar loads.
+__device__ __forceinline__ int stack_item_of(const int32_t* __restrict__ begins, int count, int32_t t) {
+  const int lane = threadIdx.x & 63;
+  int n = 0;
+  for (int base = 0; base < count; base += 256) {
+    const int i0 = base + 4 * lane;
+    int32_t v[4] = {INT32_MAX, INT32_MAX, INT32_MAX, INT32_MAX};
+    if (i0 + 3 < count) {
+      const lm_u32x4 w = *(const LM_GLOBAL lm_u32x4*)((const LM_GLOBAL int32_t*)begins + i0);
+      v[0] = (int32_t)w.x; v[1] = (int32_t)w.y; v[2] = (int32_t)w.z; v[3] = (int32_t)w.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (i0 + j < count) v[j] = begins[i0 + j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) n += __builtin_popcountll(__ballot(v[j] <= t));
   }
-  const RowArgs a = items[lo].a;
-  rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_, LCACHE>(a, (t - items[lo].tile_begin) * 16);
+  return n - 1;
+}
+
+template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0,
+          bool R16 = false>
+__global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_rows_fast_stack(const RowStackItem* __restrict__ items,
+                                                                                             const int32_t* __restrict__ begins,
+                                                                                             int count) {
+  const int32_t t = (int32_t)blockIdx.x;
+  const int it = __builtin_amdgcn_readfirstlane(stack_item_of(begins, count, t));
+  const RowArgs a = items[it].a;
+  rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_, LCACHE, R16>(a, (int64_t)(t - begins[it]) * 16);
 }
 
 // ---- long rows in two passes ------------------------------------------------
@@ -1523,7 +1569,7 @@ static inline int setup(Ctx& c, int64_t M, int64_t N, const lm_lora* l, void* ws
   c.bp = (uint16_t*)(base + w.bp_off);
   c.red = (uint32_t*)(base + w.red_off);
   c.nkc = rpad_of(rank) / 16;
-  PrepItem it;
+  PrepItem it{};
   it.b = l ? (const uint16_t*)l->b : nullptr;
   it.a = l ? (const uint16_t*)l->a : nullptr;
   it.ldb = l ? l->ldb : 0;

@@ -80,13 +80,19 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
   uint8_t* dev_rows = base + align256((size_t)count * sizeof(PrepItem));
   size_t cursor = extra;
   // host tables; lm_stage_h2d copies them into pinned staging before returning
+  // the rows table and, right after its region, the items' first groups
+  // (begins, int32, in launch order): one upload into the RowStackItem and
+  // BlkArgs regions of the workspace (the INT8 stack does not use the latter)
+  const size_t rows_bytes = align256((size_t)count * sizeof(RowStackItem));
+  static_assert(sizeof(BlkArgs) >= sizeof(int32_t), "begins fit the BlkArgs region");
   PrepItem* preps = (PrepItem*)calloc(count, sizeof(PrepItem));
-  RowStackItem* rows = (RowStackItem*)calloc(count, sizeof(RowStackItem));
+  RowStackItem* rows = (RowStackItem*)calloc(1, rows_bytes + (size_t)count * sizeof(int32_t));
   if (!preps || !rows) {
     free(preps);
     free(rows);
     return fail(LM_EINVAL, "host allocation failed");
   }
+  int32_t* begins = (int32_t*)((uint8_t*)rows + rows_bytes);
   int rc = stack_layout(items, count, workspace, workspace_bytes, preps, cursor);
   int nkc_max = 0, cd = items[0].lora.dtype;
   for (int i = 0; i < count; ++i) {
@@ -102,6 +108,9 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
   for (int i = 0; i < count; ++i) n_regular += (fast && rows_long_mode(nkc_max, sr, items[i].N) != ROWS_REGULAR) ? 0 : 1;
   int64_t tiles[2] = {0, 0};
   int slot[2] = {0, n_regular};
+  // rank 16 on the fast kernels: A^T in the row kernels' tile order
+  const bool r16 = fast && nkc_bucket(nkc_max) == 1;
+  for (int i = 0; i < count; ++i) preps[i].at_rows16 = r16 ? 1 : 0;
   for (int i = 0; rc == LM_OK && i < count; ++i) {
     const lm_stack_item& s = items[i];
     if (s.lora.dtype != cd) rc = fail(LM_EUNSUPPORTED, "all stack items must share one factor dtype");
@@ -125,8 +134,11 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
     a.seed = s.seed;
     a.red = nullptr;
     r.tile_begin = tiles[grp];
+    begins[slot[grp] - 1] = (int32_t)tiles[grp];
     tiles[grp] += (s.M + 15) / 16;
   }
+  if (rc == LM_OK && (tiles[0] > 0x7fffffff || tiles[1] > 0x7fffffff))
+    rc = fail(LM_EUNSUPPORTED, "stack too large for one launch");
   if (rc == LM_OK) rc = stack_prep(preps, count, dev_prep, st);
   if (rc == LM_OK) {
     // every item uses the largest rank bucket: the prepared layouts are per item,
@@ -135,7 +147,8 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
       if (nkc_bucket(rpad_of(items[i].lora.rank) / 16) != nkc_bucket(nkc_max))
         rc = fail(LM_EUNSUPPORTED, "stack items must share one rank bucket (16/32/64)");
   }
-  if (rc == LM_OK) rc = lm_stage_h2d(dev_rows, rows, sizeof(RowStackItem) * count, st);
+  if (rc == LM_OK) rc = lm_stage_h2d(dev_rows, rows, rows_bytes + sizeof(int32_t) * count, st);
+  const int32_t* dev_begins = (const int32_t*)(dev_rows + rows_bytes);
   if (rc == LM_OK) {
     const dim3 block(ROW_NW * 64);
     TimedLaunch timed("rows_stack", st);
@@ -143,7 +156,7 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
     if (fast) {
       if (tiles[0] > 0) {
         const dim3 grid((unsigned)tiles[0]);
-#define RF(SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, row_reg_cache<NKC_>(), fast_prefetch<NKC_, SR_>(), row_lds_cache<NKC_>()>), grid, block, 0, st, d0, n_regular))
+#define RF(SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, row_reg_cache<NKC_>(), fast_prefetch<NKC_, SR_>(), row_lds_cache<NKC_>(), NKC_ == 1>), grid, block, 0, st, d0, dev_begins, n_regular))
         if (sr) { RF(true); } else { RF(false); }
 #undef RF
       }
@@ -154,13 +167,13 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
         if (nkc_bucket(nkc_max) == 1) {  // ROWS_WIDE: 16-wave workgroups
           const dim3 wblock(ROW_NW_WIDE * 64);
           if (sr)
-            hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, true, 1, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<1, true>(), ROW_WIDE_LDS>),
-                               grid, wblock, 0, st, d1, n_deep);
+            hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, true, 1, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<1, true>(), ROW_WIDE_LDS, true>),
+                               grid, wblock, 0, st, d1, dev_begins + n_regular, n_deep);
           else
-            hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, false, 1, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<1, false>(), ROW_WIDE_LDS>),
-                               grid, wblock, 0, st, d1, n_deep);
+            hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, false, 1, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<1, false>(), ROW_WIDE_LDS, true>),
+                               grid, wblock, 0, st, d1, dev_begins + n_regular, n_deep);
         } else {  // ROWS_DEEP
-#define RD(SR_, PF_) NKC_SWITCH(nkc_bucket(nkc_max), if constexpr (NKC_ != 1 && (NKC_ == 4 || !SR_)) hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, ROW_DEEP_CACHE, PF_>), grid, block, 0, st, d1, n_deep))
+#define RD(SR_, PF_) NKC_SWITCH(nkc_bucket(nkc_max), if constexpr (NKC_ != 1 && (NKC_ == 4 || !SR_)) hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, ROW_DEEP_CACHE, PF_>), grid, block, 0, st, d1, dev_begins + n_regular, n_deep))
           if (sr) { RD(true, 1); } else if (nkc_max == 4) { RD(false, 1); } else { RD(false, 2); }
 #undef RD
         }
