@@ -1,8 +1,8 @@
-"""Merge on reload (P/model_offloader.py:245-288 post-copy hooks) through
-ReloadMergePipeline: every reload re-merges the pristine stored weights.  Each
-reloaded weight equals the oracle's requant of the GPU dense merge of the
-stored weight with seed derive_seed(path, merge_index), and a grouped stack
-merge of copies of the stored weights with the same seeds."""
+"""Merge on reload (P/model_offloader.py:245-288 post-copy hooks, P/pinned_module.py:682-695) through
+ReloadMergePipeline: every reload re-merges the pristine stored weights.  Each reloaded weight (per-row
+INT8, per-row FP8, NVFP4 with one or two scale levels, plain or swizzled) equals the oracle's requant of
+the GPU dense merge of the stored weight with seed derive_seed(path, merge_index); INT8 layers also
+equal a grouped stack merge of copies of the stored weights with the same seeds."""
 
 from __future__ import annotations
 
@@ -105,3 +105,93 @@ def test_merge_index_changes_the_stochastic_codes() -> None:
     # the scales come from the merged row maxima, which do not depend on the seed
     for x, y in zip(a, b):
         assert np.array_equal(x.scale.cpu().numpy(), y.scale.cpu().numpy())
+
+
+# ---- layers of mixed formats: per-row INT8, per-row FP8, two- and single-level NVFP4 ----
+MIXED = (("q_proj", "int8", 64, 256), ("o_proj", "fp8", 48, 512), ("gate_proj", "nvfp4", 64, 512),
+         ("up_proj", "nvfp4_1", 32, 256))
+
+
+def _mixed_layers(n: int, rank: int = 16, swizzled: bool = False) -> list[list]:
+    layers = []
+    for li in range(n):
+        layer = []
+        for name, fmt, rows, cols in MIXED:
+            w = normal_bf16((rows, cols), 0.02, 1000 * li + rows + cols)
+            b, a = lora_factors(rows, cols, rank, 11 * li + cols)
+            b, a = b.to(DEV), a.to(DEV)
+            path, strength = f"layers.{li}.{name}.weight", 0.75 if li % 2 else 1.0
+            if fmt == "int8":
+                q, s = int8_initial(w)
+                layer.append(R.HostInt8Target(path, q.pin_memory(), s.pin_memory(), b, a, strength))
+            elif fmt == "fp8":
+                s = (w.float().abs().amax(1, keepdim=True) / 448.0).clamp_min(2.0 ** -23)
+                q = (w.float() / s).clamp(-448, 448).to(torch.float8_e4m3fn)
+                layer.append(R.HostFloat8Target(path, q.pin_memory(), s.pin_memory(), b, a, strength))
+            else:
+                two = fmt == "nvfp4"
+                q, sc, pts = O.nvfp4_requant(bf16_np(w), two_level=two, swizzled=swizzled)
+                pt = None if pts is None else torch.from_numpy(pts.reshape(())).pin_memory()
+                layer.append(R.HostNvfp4Target(path, torch.from_numpy(q).pin_memory(),
+                                               torch.from_numpy(sc).view(torch.float8_e4m3fn).pin_memory(), pt,
+                                               b, a, strength, swizzled))
+        layers.append(layer)
+    return layers
+
+
+def _mixed_oracle(t, merge_index: int, stochastic: bool) -> list[np.ndarray]:  # noqa: ANN001
+    """The oracle's requant of the GPU dense merge of one stored weight: [codes, scales(, global scale)]."""
+    seed = derive_seed(t.path, merge_index) if stochastic else 0
+    sr = O.SR_PHILOX8 if stochastic else O.SR_OFF
+    lora = (t.b, t.a, t.strength)
+    if isinstance(t, R.HostInt8Target):
+        cols = t.qdata.shape[1]
+        dense = K.dequantize_int8(t.qdata.to(DEV), t.scale.to(DEV), None, (1, cols), lora=lora)
+        rq, rs, _ = O.int8_requant(bf16_np(dense), cols, sr_mode=sr, seed=seed)
+        return [rq, rs]
+    if isinstance(t, R.HostFloat8Target):
+        cols = t.qdata.shape[1]
+        dense = K.dequantize_float8(t.qdata.to(DEV), t.scale.to(DEV), (1, cols), lora=lora)
+        rq, rs = O.fp8_requant(bf16_np(dense), cols, sr_mode=sr, seed=seed)
+        return [rq, rs]
+    pts = None if t.per_tensor_scale is None else t.per_tensor_scale.to(DEV)
+    dense = K.dequantize_nvfp4(t.qdata.to(DEV), t.scale.to(DEV), pts, swizzled=t.is_swizzled_scales, lora=lora)
+    rq, rs, rg = O.nvfp4_requant(bf16_np(dense), swizzled=t.is_swizzled_scales, two_level=pts is not None,
+                                 sr_mode=sr, seed=seed)
+    return [rq, rs] + ([rg] if rg is not None else [])
+
+
+def _as_np(x: torch.Tensor) -> np.ndarray:
+    x = x.detach().cpu().contiguous()
+    if x.dtype in (torch.float8_e4m3fn, torch.float8_e5m2, torch.int8):
+        x = x.view(torch.uint8) if x.dtype is not torch.int8 else x
+    return x.numpy().reshape(-1)
+
+
+@pytest.mark.parametrize("stochastic", [True, False])
+@pytest.mark.parametrize("swizzled", [False, True])
+def test_mixed_format_reloads_equal_the_oracle(stochastic: bool, swizzled: bool) -> None:
+    layers = _mixed_layers(3, swizzled=swizzled)
+    pipe = R.ReloadMergePipeline(layers, slots=2, stochastic=stochastic)
+    for layer, mi in [(0, 0), (1, 0), (2, 0), (0, 1), (1, 4)]:
+        got = pipe.reload(layer, mi)
+        got.wait()
+        for i, (w, t) in enumerate(zip(got.weights, layers[layer])):
+            want = _mixed_oracle(t, mi, stochastic)
+            have = [w.qdata, w.scale] + ([w.per_tensor_scale] if getattr(w, "per_tensor_scale", None) is not None
+                                         else [])
+            assert len(have) == len(want), f"layer {layer} target {i}"
+            for k, (h, e) in enumerate(zip(have, want)):
+                hv, ev = _as_np(h), np.asarray(e).reshape(-1)
+                if hv.dtype != ev.dtype:
+                    hv = hv.view(ev.dtype) if hv.itemsize == ev.itemsize else hv.astype(ev.dtype)
+                m = mismatch_report(hv, ev, f"layer {layer} target {i} ({type(t).__name__}) part {k}", 64)
+                assert not m, m
+        pipe.release(got)
+    pipe.synchronize()
+    # the stored weights are untouched: a reload of layer 0 with index 0 repeats the first result
+    again = pipe.reload(0, 0)
+    again.wait()
+    for w, t in zip(again.weights, layers[0]):
+        want = _mixed_oracle(t, 0, stochastic)
+        assert np.array_equal(_as_np(w.qdata).view(np.uint8), np.asarray(want[0]).reshape(-1).view(np.uint8))
