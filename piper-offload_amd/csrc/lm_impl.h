@@ -689,7 +689,9 @@ __device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const uint4& 
 
 // quantize and store one tile given its bf16-valued merged values m[16];
 // old[i] is any register the INT8 stochastic path may overwrite for pair i
-template <int KIND, bool SR>
+// SBF: INT8 qparams stored in bf16 (the reference rounds the quantize step's
+// v * RN(1 / s) to the qparam dtype, P/_triton_int8_lora.py:190-236)
+template <int KIND, bool SR, bool SBF = false>
 __device__ __forceinline__ void fast_quant_store_vals(const RowArgs& a, const FastLane& L, bool rok, int mt,
                                                       const RowQP& qp, const float (&m)[16], const uint32_t (&old)[8]) {
   if (!rok) return;
@@ -716,7 +718,7 @@ __device__ __forceinline__ void fast_quant_store_vals(const RowArgs& a, const Fa
       const float qmin = (float)a.qmin, qmax = (float)a.qmax;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const float x = __builtin_amdgcn_fmed3f(m[j] * qp.inv, qmin, qmax);
+        const float x = __builtin_amdgcn_fmed3f(SBF ? bf16r(m[j] * qp.inv) : m[j] * qp.inv, qmin, qmax);
         y[j] = f2u(x + 12582912.0f);  // low byte = rint(x) (two's complement)
       }
 #pragma unroll
@@ -737,7 +739,7 @@ __device__ __forceinline__ void fast_quant_store_vals(const RowArgs& a, const Fa
   store_b128_guarded((LM_GLOBAL lm_u32x4*)(L.out + (uint32_t)(mt * 64) + L.off), lm_u32x4{out[0], out[1], out[2], out[3]});
 }
 // the same from the packed bf16 pairs w[8] of a cached tile
-template <int KIND, bool SR>
+template <int KIND, bool SR, bool SBF = false>
 __device__ __forceinline__ void fast_quant_store(const RowArgs& a, const FastLane& L, bool rok, int mt,
                                                  const RowQP& qp, const uint32_t (&w)[8]) {
   float m[16];
@@ -746,7 +748,7 @@ __device__ __forceinline__ void fast_quant_store(const RowArgs& a, const FastLan
     m[2 * i] = bf16_lo(w[i]);
     m[2 * i + 1] = bf16_hi(w[i]);
   }
-  fast_quant_store_vals<KIND, SR>(a, L, rok, mt, qp, m, w);
+  fast_quant_store_vals<KIND, SR, SBF>(a, L, rok, mt, qp, m, w);
 }
 
 // Tiles of A^T operands a wave keeps in flight ahead of the arithmetic (the
@@ -759,8 +761,9 @@ constexpr int fast_prefetch() { return NKC == 1 ? 4 : 2; }
 // each: [half][lane][4 words], so the two 16-byte writes of a lane are
 // consecutive across lanes); tiles beyond CACHE + LCACHE are merged twice.
 template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0,
-          bool R16 = false>
+          bool R16 = false, bool SBF = false>
 __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
+  static_assert(!SBF || KIND == K_INT8, "bf16 qparams are an INT8 layout");
   __shared__ float sh_mx[16][NW];
   __shared__ lm_u32x4 lcache[LCACHE > 0 ? LCACHE : 1][NW][2][64];
   constexpr int PF = PF_ < CACHE ? PF_ : CACHE;
@@ -772,8 +775,9 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   const int ntiles = (int)(a.N >> 6);
   const FastLane L = fast_lane<NKC, R16>(a, rowc, lane);
   v4i16 bop[NKC];
-  load_bop<NKC>(a.bp, row, lane, bop);
-  const float s_in = rok ? ((const LM_GLOBAL float*)a.scale)[row] : 0.0f;
+  load_bop_g<NKC>(a.bp, row, lane, bop);
+  const float s_in = !rok ? 0.0f
+                     : SBF ? bf16_val(((const LM_GLOBAL uint16_t*)a.scale)[row]) : ((const LM_GLOBAL float*)a.scale)[row];
   uint32_t cache[CACHE][8];
   float amax = 0.0f;
   if (wave + (CACHE - 1) * NW < ntiles) {
@@ -836,17 +840,18 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   RowQP qp;
   if constexpr (KIND == K_INT8) {
     int zp;
-    qp = int8_qparams<BF16, F32, false>(-mx, mx, a.qmin, a.qmax, stored, zp);
-    if (writer) ((float*)a.scale_out)[row] = stored;
-    if (writer && a.zp_out) a.zp_out[row] = 0;
+    qp = int8_qparams<BF16, SBF ? BF16 : F32, false>(-mx, mx, a.qmin, a.qmax, stored, zp);
+    if (writer && SBF) ((LM_GLOBAL uint16_t*)a.scale_out)[row] = bf16_bits(stored);
+    if (writer && !SBF) ((LM_GLOBAL float*)a.scale_out)[row] = stored;
+    if (writer && a.zp_out) ((LM_GLOBAL int8_t*)a.zp_out)[row] = 0;
   } else {
     qp = fp8_qparams<BF16, KIND>(mx, stored);
-    if (writer) ((float*)a.scale_out)[row] = stored;
+    if (writer) ((LM_GLOBAL float*)a.scale_out)[row] = stored;
   }
 #pragma unroll
   for (int i = 0; i < CACHE; ++i) {
     const int mt = wave + i * NW;
-    if (mt < ntiles) fast_quant_store<KIND, SR>(a, L, rok, mt, qp, cache[i]);
+    if (mt < ntiles) fast_quant_store<KIND, SR, SBF>(a, L, rok, mt, qp, cache[i]);
   }
 #pragma unroll
   for (int l = 0; l < LCACHE; ++l) {
@@ -854,7 +859,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
     if (mt < ntiles) {
       const lm_u32x4 lo = lcache[l][wave][0][lane], hi = lcache[l][wave][1][lane];
       const uint32_t t[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-      fast_quant_store<KIND, SR>(a, L, rok, mt, qp, t);
+      fast_quant_store<KIND, SR, SBF>(a, L, rok, mt, qp, t);
     }
   }
   if (wave + (CACHE + LCACHE) * NW < ntiles) {
@@ -866,7 +871,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
       uint32_t t[8];
       float unused = 0.0f;
       fast_merged_tile<KIND, NKC>(a, cur.raw, cur.aop, bop, s_in, t, unused);
-      fast_quant_store<KIND, SR>(a, L, rok, mt, qp, t);
+      fast_quant_store<KIND, SR, SBF>(a, L, rok, mt, qp, t);
       cur = nxt;
     }
   }
@@ -877,9 +882,10 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
 template <int NKC, int CACHE>
 constexpr int fast_min_waves() { return (NKC == 1 && CACHE <= 8) || (NKC == 2 && CACHE <= 4) ? 4 : 1; }
 
-template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0>
+template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0,
+          bool SBF = false>
 __global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_rows_fast(RowArgs a) {
-  rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_, LCACHE>(a, (int64_t)blockIdx.x * 16);
+  rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_, LCACHE, false, SBF>(a, (int64_t)blockIdx.x * 16);
 }
 // The item that owns 16-row group t: the last of the `count` ascending first
 // groups begins[] that is <= t.  Every lane compares four entries per pass
@@ -906,14 +912,14 @@ __device__ __forceinline__ int stack_item_of(const int32_t* __restrict__ begins,
 }
 
 template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0,
-          bool R16 = false>
+          bool R16 = false, bool SBF = false>
 __global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_rows_fast_stack(const RowStackItem* __restrict__ items,
                                                                                              const int32_t* __restrict__ begins,
                                                                                              int count) {
   const int32_t t = (int32_t)blockIdx.x;
   const int it = __builtin_amdgcn_readfirstlane(stack_item_of(begins, count, t));
   const RowArgs a = items[it].a;
-  rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_, LCACHE, R16>(a, (int64_t)(t - begins[it]) * 16);
+  rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_, LCACHE, R16, SBF>(a, (int64_t)(t - begins[it]) * 16);
 }
 
 // ---- long rows in two passes ------------------------------------------------
@@ -1693,7 +1699,7 @@ static int run_rows_nkc(const RowArgs& a, int nkc, int scale_dt, hipStream_t st)
 // The fast kernels address codes, A^T operands and Philox counters with 32-bit
 // offsets: M N < 2^32 (4 GiB of codes per tensor) and N RPAD < 2^32.
 static inline bool rows_fast_ok(int kind, int cd, int sdt, bool asym, int nkc, int64_t M, int64_t N) {
-  return cd == LM_BF16 && nkc > 0 && (N % 64) == 0 && (kind != K_INT8 || (!asym && sdt == LM_F32)) &&
+  return cd == LM_BF16 && nkc > 0 && (N % 64) == 0 && (kind != K_INT8 || (!asym && (sdt == LM_F32 || sdt == LM_BF16))) &&
          M * N < (INT64_C(1) << 32) && N * 64 < (INT64_C(1) << 32);
 }
 
@@ -1727,22 +1733,22 @@ static inline int rows_long_mode(int nkc, bool sr, int64_t N) {
   return (nkc == 4 || !sr) ? ROWS_DEEP : ROWS_REGULAR;
 }
 
-template <int KIND, bool SR, int NKC>
+template <int KIND, bool SR, int NKC, bool SBF = false>
 static int launch_rows_fast(const RowArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)((a.M + 15) / 16));
   TimedLaunch timed("rows", st);
   const int mode = rows_long_mode(NKC, SR, a.N);
   if (mode == ROWS_WIDE) {
     if constexpr (NKC == 1)
-      hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<NKC, SR>(), ROW_WIDE_LDS>), grid,
-                         dim3(ROW_NW_WIDE * 64), 0, st, a);
+      hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<NKC, SR>(), ROW_WIDE_LDS, SBF>),
+                         grid, dim3(ROW_NW_WIDE * 64), 0, st, a);
   } else if (mode == ROWS_DEEP) {
     if constexpr (NKC == 4 || !SR)
-      hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_DEEP_CACHE, NKC == 4 ? 1 : 2>), grid,
+      hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_DEEP_CACHE, NKC == 4 ? 1 : 2, 0, SBF>), grid,
                          dim3(ROW_NW * 64), 0, st, a);
   } else {
     hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, row_reg_cache<NKC>(), fast_prefetch<NKC, SR>(),
-                                    row_lds_cache<NKC>()>),
+                                    row_lds_cache<NKC>(), SBF>),
                        grid, dim3(ROW_NW * 64), 0, st, a);
   }
   LAUNCH_CHECK();
@@ -1764,7 +1770,8 @@ static constexpr int SPLIT_IL = 1;
 // register cache at rank above 32, where the cached kernel runs one
 // workgroup per CU
 static inline bool rows_split_wanted(int kind, int cd, int sdt, bool asym, bool sr, int nkc, int64_t M, int64_t N) {
-  return rows_fast_ok(kind, cd, sdt, asym, nkc, M, N) && nkc == 4 && rows_long_mode(nkc, sr, N) == ROWS_DEEP;
+  return rows_fast_ok(kind, cd, sdt, asym, nkc, M, N) && sdt == LM_F32 && nkc == 4 &&
+         rows_long_mode(nkc, sr, N) == ROWS_DEEP;
 }
 template <int KIND, bool SR, int NKC, int RB, int TPW, bool QUANT, int IL = 0>
 static int launch_rows_split_pass(const RowArgs& a, hipStream_t st) {
@@ -1792,6 +1799,15 @@ static int run_rows(const RowArgs& a, int cd, int sdt, bool asym, bool sr, int n
     if (a.red) {  // the caller chose the two-pass kernels (rows_split_wanted: rank bucket 64) and had prep clear the slots
       if (nkc_bucket(nkc) != 4) return fail(LM_EINVAL, "two-pass rows need the rank-64 bucket");
       return sr ? launch_rows_split<KIND, true, 4>(a, st) : launch_rows_split<KIND, false, 4>(a, st);
+    }
+    if constexpr (KIND == K_INT8) {
+      if (sdt == LM_BF16) {
+        if (sr) {
+          NKC_SWITCH(nkc_bucket(nkc), return (launch_rows_fast<KIND, true, NKC_, true>(a, st)));
+        } else {
+          NKC_SWITCH(nkc_bucket(nkc), return (launch_rows_fast<KIND, false, NKC_, true>(a, st)));
+        }
+      }
     }
     if (sr) {
       NKC_SWITCH(nkc_bucket(nkc), return (launch_rows_fast<KIND, true, NKC_>(a, st)));

@@ -1,5 +1,6 @@
 // lm_stack.hip -- grouped multi-target (stack) entry points.
 #include "lm_nvfp4_fast.h"
+#include "lm_rows_stack.h"
 
 // ---------------------------------------------------------------------------
 // stacks
@@ -154,30 +155,8 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
     TimedLaunch timed("rows_stack", st);
     const RowStackItem* d0 = (const RowStackItem*)dev_rows;
     if (fast) {
-      if (tiles[0] > 0) {
-        const dim3 grid((unsigned)tiles[0]);
-#define RF(SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, row_reg_cache<NKC_>(), fast_prefetch<NKC_, SR_>(), row_lds_cache<NKC_>(), NKC_ == 1>), grid, block, 0, st, d0, dev_begins, n_regular))
-        if (sr) { RF(true); } else { RF(false); }
-#undef RF
-      }
-      if (tiles[1] > 0) {
-        const dim3 grid((unsigned)tiles[1]);
-        const RowStackItem* d1 = d0 + n_regular;
-        const int n_deep = count - n_regular;
-        if (nkc_bucket(nkc_max) == 1) {  // ROWS_WIDE: 16-wave workgroups
-          const dim3 wblock(ROW_NW_WIDE * 64);
-          if (sr)
-            hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, true, 1, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<1, true>(), ROW_WIDE_LDS, true>),
-                               grid, wblock, 0, st, d1, dev_begins + n_regular, n_deep);
-          else
-            hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, false, 1, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<1, false>(), ROW_WIDE_LDS, true>),
-                               grid, wblock, 0, st, d1, dev_begins + n_regular, n_deep);
-        } else {  // ROWS_DEEP
-#define RD(SR_, PF_) NKC_SWITCH(nkc_bucket(nkc_max), if constexpr (NKC_ != 1 && (NKC_ == 4 || !SR_)) hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, ROW_DEEP_CACHE, PF_>), grid, block, 0, st, d1, dev_begins + n_regular, n_deep))
-          if (sr) { RD(true, 1); } else if (nkc_max == 4) { RD(false, 1); } else { RD(false, 2); }
-#undef RD
-        }
-      }
+      rc = scale_dtype == LM_BF16 ? int8_stack_fast_launch_sbf(d0, dev_begins, n_regular, count, tiles, nkc_max, sr, st)
+                                  : int8_stack_fast_launch<false>(d0, dev_begins, n_regular, count, tiles, nkc_max, sr, st);
     } else {
       const dim3 grid((unsigned)tiles[0]);
 #define RS(CD_, SDT_, SR_) NKC_SWITCH(nkc_bucket(nkc_max), hipLaunchKernelGGL((k_rows_stack<K_INT8, CD_, SDT_, SR_, NKC_, ROW_NW, ROW_CACHE>), grid, block, 0, st, d0, count, scale_dtype))

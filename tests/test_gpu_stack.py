@@ -88,6 +88,38 @@ def test_int8_stack_and_per_target_merges_equal_the_oracle(shapes, sr):
     assert not errors, "\n".join(errors)
 
 
+@pytest.mark.parametrize("shapes", [[(64, 256), (40, 512), (128, 128), (16, 64)],
+                                    [(64, 256), (40, 14336), (16, 8192), (24, 4096)],
+                                    [(24, 4096), (8200, 4096), (40, 4096), (1000, 4096)],
+                                    LAYER])
+@pytest.mark.parametrize("sr", [False, True])
+def test_int8_stack_with_bf16_scales_equals_the_oracle(shapes, sr):
+    """bf16 qparams (TorchAO keeps scales in the model dtype): the fast row kernels round the quantize step's
+    v * RN(1 / s) to bf16 (P/_triton_int8_lora.py:190-236) and store bf16 scales."""
+    tg = _int8_targets(shapes, 16, 60)
+    errors = []
+    targets = []
+    for i, (q, s, b, a, strength, seed) in enumerate(tg):
+        s = s.to(torch.bfloat16)
+        cols = q.shape[1]
+        dense = K.dequantize_int8(q.to(DEV), s.to(DEV), None, (1, cols), lora=(b, a, strength))
+        rq, rs, _ = O.int8_requant(bf16_np(dense), cols, scale_dt=O.DT_BF16, sr_mode=_sr(sr), seed=seed if sr else 0)
+        pq, ps, _ = K.merge_int8_lora(q.to(DEV), s.to(DEV), None, (1, cols), b, a, strength, asymmetric=False,
+                                      reduce_range=False, rounding_seed=seed if sr else None)
+        errors += [f"per-target item {i} {m}" for m in (mismatch_report(pq.cpu().numpy(), rq, "codes", 64),
+                                                         mismatch_report(bf16_np(ps).reshape(-1), rs, "scales", 1))
+                   if m]
+        w = Int8Weight(q.clone().to(DEV), s.clone().to(DEV), (1, cols), torch.bfloat16)
+        targets.append((StackTarget(w, b, a, strength, seed), rq, rs))
+    merge_int8_stack([t for t, _, _ in targets], stochastic=sr)
+    for i, (t, rq, rs) in enumerate(targets):
+        assert t.weight.scale.dtype is torch.bfloat16
+        errors += [f"stack item {i} {m}" for m in (
+            mismatch_report(t.weight.qdata.cpu().numpy(), rq, "codes", 64),
+            mismatch_report(bf16_np(t.weight.scale).reshape(-1), rs, "scales", 1)) if m]
+    assert not errors, "\n".join(errors)
+
+
 def test_stack_plan_reuse_equals_the_oracle_twice():
     tg = _int8_targets([(64, 256), (32, 512), (16, 128)], 16, 40)
     targets = [StackTarget(Int8Weight(q.clone().to(DEV), s.clone().to(DEV), (1, q.shape[1]), torch.bfloat16),
