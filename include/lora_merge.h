@@ -281,22 +281,6 @@ int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, int32_t scale
 int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, int32_t swizzled, int32_t rounding_mode,
                          void* workspace, size_t workspace_bytes, void* stream);
 
-/* Status word of a stack workspace.  No reference counterpart: the
- * reference's per-target loop (P/merge.py:121-125) has no grouped launch
- * that could stall.  The uint32 at (char*)workspace + lm_stack_status_offset
- * (count) gets bit 0 set, and stays set, when a quant unit of the fused
- * NVFP4 launch gave up its bounded wait for the item's amax units: that unit
- * stored nothing, so part of the merge is missing.  The library never clears
- * it and never reads it (reading would synchronize): the caller zeroes it
- * once, copies it to the host asynchronously after a merge, and treats a
- * nonzero value as a failed merge (piper_offload_amd.stack does). */
-size_t lm_stack_status_offset(int32_t count);
-/* Test hook: the fused NVFP4 launch's wait budget (polls) and an extra count
- * of amax units it waits for (defaults 2^20 and 0).  A nonzero extra count
- * makes every wait give up after `spin_limit` polls, with every wave ending
- * normally. */
-int lm_debug_stack_wait(uint32_t spin_limit, uint32_t extra_need);
-
 /* ---------------- instrumentation -------------------------------------
  * No reference counterpart.  When enabled, every entry point brackets its
  * main kernel launches with hipEvents on the caller's stream, keyed by kernel

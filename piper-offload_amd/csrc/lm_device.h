@@ -91,13 +91,13 @@ DEV float dpp_f32(float x) {
 // max over all 64 lanes: after xor 1 and xor 2 a quad is uniform, so the
 // half-row mirror (lane i <-> 7 - i) pairs quad 0 with quad 1 and the row
 // mirror (i <-> 15 - i) pairs the two halves
-DEV float wave_max(float x) {
+DEV float row_max16(float x) {  // max over each 16-lane row
   x = __builtin_fmaxf(x, dpp_f32<0xB1>(x));   // quad_perm [1, 0, 3, 2]
   x = __builtin_fmaxf(x, dpp_f32<0x4E>(x));   // quad_perm [2, 3, 0, 1]
   x = __builtin_fmaxf(x, dpp_f32<0x141>(x));  // row_half_mirror
-  x = __builtin_fmaxf(x, dpp_f32<0x140>(x));  // row_mirror
-  return lanes_max32(lanes_max16(x));
+  return __builtin_fmaxf(x, dpp_f32<0x140>(x));  // row_mirror
 }
+DEV float wave_max(float x) { return lanes_max32(lanes_max16(row_max16(x))); }
 
 template <int DT>
 DEV float round_dt(float x) {

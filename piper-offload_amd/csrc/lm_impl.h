@@ -63,17 +63,24 @@ static inline int64_t mpad_of(int64_t M) { return (M + 15) / 16 * 16; }
 // reduction slots: 64 words for the block formats' per-tensor passes, then
 // (for the two-pass long-row kernels) Mpad words of row amax bits and Mpad
 // copies of the input row scales
+// then, for the pruned per-tensor amax of two-level NVFP4: the Euclidean norms
+// of B's rows and A's columns (Mpad + Npad floats), one upper bound of
+// max |merged| per 16-row x 128-column tile and one best-bound tile per
+// 128-row chunk (nv_bound_units)
 struct WsLayout {
-  size_t at_off, bp_off, red_off, total;
+  size_t at_off, bp_off, red_off, nrm_off, ub_off, total;
 };
 static inline int64_t red_words(int64_t M) { return 64 + 2 * mpad_of(M); }
+static inline int64_t ub_words(int64_t M, int64_t N) { return mpad_of(M) / 16 * (npad_of(N) / 128) + (M + 127) / 128; }
 static WsLayout ws_layout(int64_t M, int64_t N, int rank) {
   WsLayout w;
   int rp = rpad_of(rank);
   w.at_off = 0;
   w.bp_off = align256((size_t)npad_of(N) * rp * 2);
   w.red_off = w.bp_off + align256((size_t)mpad_of(M) * rp * 2);
-  w.total = w.red_off + align256((size_t)red_words(M) * 4);
+  w.nrm_off = w.red_off + align256((size_t)red_words(M) * 4);
+  w.ub_off = w.nrm_off + align256((size_t)(mpad_of(M) + npad_of(N)) * 4);
+  w.total = w.ub_off + align256((size_t)ub_words(M, N) * 4);
   return w;
 }
 
@@ -94,6 +101,9 @@ struct PrepItem {
   int64_t block_begin; // prefix of per-item k_prep_many workgroups
   int vec_b;           // B rows load 4 ranks at once (ldb, rank % 4 == 0, 8-byte aligned)
   int at_rows16;       // rank 16, At in the row kernels' tile order (at_rows16_offset)
+  float* nrm;          // with norms: ||B_i|| for rows [0, Mpad), then ||A_j|| for columns [0, Npad)
+  int norms;           // bf16 factors: compute nrm (the pruned NVFP4 amax bounds the delta by them)
+  float* ub;           // the item's tile-bound region (not written by prep)
 };
 
 // At for the per-row kernels at rank <= 16 (RPAD 16): per 64-column tile,
@@ -154,11 +164,39 @@ __device__ __forceinline__ void prep_unit(const PrepItem& it, int64_t u) {
     return;
   }
   u -= n_bp;
-  if (it.red) {  // unit u clears words [64 u, 64 u + 64) (nred is a multiple of 16)
-    LM_GLOBAL lm_u32x4* r = (LM_GLOBAL lm_u32x4*)it.red + 16 * u;
-    const int n4 = (int)((it.nred - 64 * u) >> 2) < 16 ? (int)((it.nred - 64 * u) >> 2) : 16;
-    for (int i = 0; i < n4; ++i) r[i] = lm_u32x4{0u, 0u, 0u, 0u};
+  const int64_t n_red = (it.nred + 63) / 64;
+  if (u < n_red) {
+    if (it.red) {  // unit u clears words [64 u, 64 u + 64) (nred is a multiple of 16)
+      LM_GLOBAL lm_u32x4* r = (LM_GLOBAL lm_u32x4*)it.red + 16 * u;
+      const int n4 = (int)((it.nred - 64 * u) >> 2) < 16 ? (int)((it.nred - 64 * u) >> 2) : 16;
+      for (int i = 0; i < n4; ++i) r[i] = lm_u32x4{0u, 0u, 0u, 0u};
+    }
+    return;
   }
+  u -= n_red;
+  // norms (bf16 factors): sqrt of the fp32 sum of squares, raised by 2^-16
+  // relative so that it bounds the true norm (the sum's rounding and the
+  // square root's error are far below that); padding rows and columns are 0
+  const LM_GLOBAL uint16_t* src;
+  int64_t stride;
+  bool live;
+  if (u < mpad) {
+    live = u < it.M;
+    src = (const LM_GLOBAL uint16_t*)it.b + (live ? u * it.ldb : 0);
+    stride = 1;
+  } else {
+    const int64_t col = u - mpad;
+    live = col < it.N;
+    src = (const LM_GLOBAL uint16_t*)it.a + (live ? col : 0);
+    stride = it.lda;
+  }
+  float ss = 0.0f;
+  if (live)
+    for (int k = 0; k < it.rank; ++k) {
+      const float v = u2f((uint32_t)src[k * stride] << 16);
+      ss = __builtin_fmaf(v, v, ss);
+    }
+  ((LM_GLOBAL float*)it.nrm)[u] = live ? __builtin_sqrtf(ss) * (1.0f + 0x1p-16f) : 0.0f;
 }
 
 // B rows can be read 4 ranks (8 bytes) at a time
@@ -167,7 +205,7 @@ static inline int prep_vec_b(const PrepItem& it) {
 }
 __host__ __device__ static inline int64_t prep_units(const PrepItem& it) {
   const int64_t npad = (it.N + 127) / 128 * 128, mpad = (it.M + 15) / 16 * 16;
-  return npad * it.rpad / 4 + mpad * it.rpad / 4 + (it.nred + 63) / 64;
+  return npad * it.rpad / 4 + mpad * it.rpad / 4 + (it.nred + 63) / 64 + (it.norms ? mpad + npad : 0);
 }
 
 static __global__ __launch_bounds__(256) void k_prep1(PrepItem it, int64_t total) {
@@ -1545,6 +1583,8 @@ struct Ctx {
   uint16_t* at = nullptr;
   uint16_t* bp = nullptr;
   uint32_t* red = nullptr;
+  float* nrm = nullptr;  // ws_layout's norms region
+  float* ub = nullptr;   // ws_layout's tile-bound region
   int nkc = 0;
 };
 
@@ -1563,7 +1603,7 @@ static inline int check_lora(const lm_lora* l, int64_t M, int64_t N) {
 // rows_split: the call runs the two-pass long-row kernels, whose row amax
 // slots the prep launch clears
 static inline int setup(Ctx& c, int64_t M, int64_t N, const lm_lora* l, void* ws, size_t wsb, void* stream,
-                        bool rows_split = false) {
+                        bool rows_split = false, bool norms = false) {
   c.st = (hipStream_t)stream;
   const int rank = l ? l->rank : 0;
   WsLayout w = ws_layout(M, N, rank);
@@ -1591,6 +1631,10 @@ static inline int setup(Ctx& c, int64_t M, int64_t N, const lm_lora* l, void* ws
   it.work_begin = 0;
   it.block_begin = 0;
   it.vec_b = prep_vec_b(it);
+  c.nrm = (float*)(base + w.nrm_off);
+  c.ub = (float*)(base + w.ub_off);
+  it.nrm = c.nrm;
+  it.norms = norms && l != nullptr && l->dtype == LM_BF16 ? 1 : 0;
   return launch_prep(it, c.st);
 }
 

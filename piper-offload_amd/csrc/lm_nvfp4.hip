@@ -14,8 +14,10 @@ static int nvfp4_common(const uint8_t* q, const uint8_t* scale, const float* pts
   if (!q_out || !scale_out) return fail(LM_EINVAL, "NVFP4 outputs must be non-null");
   if (two_level && !pts_out) return fail(LM_EINVAL, "two-level NVFP4 needs a per-tensor scale output");
   Ctx c;
-  if ((rc = setup(c, M, N, lora, ws, wsb, stream))) return rc;
   const int cd = lora ? lora->dtype : dense_dt;
+  // the pruned amax of a two-level fast merge bounds the delta by the factors' norms (prep)
+  const bool fast = lora && !dense && nv_fast_ok(cd, rpad_of(lora->rank) / 16, M, N);
+  if ((rc = setup(c, M, N, lora, ws, wsb, stream, false, fast && two_level))) return rc;
   const bool sr = is_sr(rnd);
   BlkArgs a = blk_args_base(c, M, N, lora, rnd);
   a.q = q;
@@ -27,7 +29,7 @@ static int nvfp4_common(const uint8_t* q, const uint8_t* scale, const float* pts
   a.aux_out = pts_out;
   a.swizzled = swz;
   if (swz && (rc = zero_swizzle_pad(scale_out, M, N / 16, c.st))) return rc;
-  if (lora && !dense && nv_fast_ok(cd, c.nkc, M, N)) {
+  if (fast) {
     NvArgs na;
     na.q = q;
     na.scale = scale;
@@ -38,6 +40,8 @@ static int nvfp4_common(const uint8_t* q, const uint8_t* scale, const float* pts
     na.at = c.at;
     na.bp = c.bp;
     na.red = c.red;
+    na.nrm = c.nrm;
+    na.ub = c.ub;
     na.M = M;
     na.N = N;
     na.strength = lora->strength;

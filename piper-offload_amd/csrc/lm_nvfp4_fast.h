@@ -16,16 +16,17 @@
 // A^T fragments read through per-lane pointers.
 //
 // Two-level tensors take two passes (P/_triton_nvfp4_lora.py:437-512, 327-366):
-//   k_nv_amax  -- max |merged| over the tensor into red[0] (float bits, so
-//                 atomicMax on uint orders them); the reference reduces
-//                 bf16(merged), and since RNE is monotone the max of the
-//                 rounded values is the rounded max of the unrounded ones;
+//   amax  -- max |bf16(merged)| over the tensor into red[0] (float bits, so
+//            atomicMax on uint orders them), found without merging every
+//            tile (the pruned amax below: bound, seed, refine); the
+//            reference reduces bf16(merged), and since RNE is monotone the
+//            max of the rounded values is the rounded max of the unrounded
+//            ones;
 //   k_nv_quant -- g = max(amax / 2688, eps); per block s = e4m3(clamp(
 //                 (bmax / 6) / g, 2^-6, 448)); codes = e2m1(merged * ((1/g)/s));
 //   The amax pass copies the input g into red[1] and the quant pass reads
 //   that copy, so the quant pass's first workgroup can write the output g
-//   even where it aliases the input.  For a round-to-nearest stack both
-//   passes run in one launch (k_nv_fused_stack).
+//   even where it aliases the input.
 // Single-level tensors skip the amax pass and divide by the block scale.
 #pragma once
 #include "lm_impl.h"
@@ -40,6 +41,8 @@ struct NvArgs {
   const uint16_t* at;
   const uint16_t* bp;
   uint32_t* red;           // red[0]: max |merged| bits (cleared by the prep kernel)
+  const float* nrm;        // ||B_i|| (Mpad rows), then ||A_j|| (Npad columns): the pruned amax
+  float* ub;               // per-tile bounds, then per-chunk best tiles: the pruned amax
   int64_t M, N;
   float strength;
   int swizzled;
@@ -47,8 +50,9 @@ struct NvArgs {
 };
 struct NvStackItem {
   NvArgs a;
-  int64_t tile_begin;  // prefix of 16-row groups (quant launches)
-  int64_t pair_begin;  // prefix of 32-row units (amax launch)
+  int64_t tile_begin;    // prefix of 16-row groups (quant launches)
+  int64_t bound_begin;   // prefix of 128-row chunks (pruned amax: bound and seed launches)
+  int64_t refine_begin;  // prefix of 512-tile chunks (pruned amax: refine launch)
 };
 
 constexpr int NV_NW = 8;
@@ -113,7 +117,7 @@ DEV void nv_load_tile(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
 
 // merged values of the lane's 32 columns, for max |merged| (the reference's
 // "update == 0 keeps the base" rule only changes the sign of a zero, so the
-// amax pass does not need it)
+// amax does not need it)
 template <int NKC, bool TWO>
 DEV void nv_merged_parts(const uint4& codes, uint32_t sc, const v4i16 (&aop)[8][NKC], const v4i16 (&bop)[NKC],
                          float strength, float gin, float (&m)[32]) {
@@ -275,228 +279,8 @@ DEV void nv_quant_tile(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&b
 // ---- pass bodies -------------------------------------------------------------
 // Rows past M load row M-1 (valid memory) and store nothing.
 // Tiles [t0, t1) of rows row0 .. row0+15 (the stack passes whole rows).
-// The amax pass keeps no register cache, so a wave merges 32 rows (two
-// 16-row groups) per macro tile: both groups' MFMAs share the tile's A^T
-// fragments, which halves the operand loads (L2) per element.  The pass is
-// bound by the texture-address unit (TA_BUSY ~85%, VALU ~63%) through its
-// code and scale loads, whose every instruction touches 16 rows: four
-// groups per wave, sharing the A^T loads further, measured the same.  Rows
-// row0 .. row0 + 31; the second group exists when row0 + 16 < M.
-// the copy of the input per-tensor scale in red[1]: a plain store when the
-// quant pass is a later launch, a device-scope atomic exchange when it runs in
-// the same launch (k_nv_fused_stack)
-DEV void nv_keep_gin(uint32_t* red, float gin, bool fused) {
-  if (fused) __hip_atomic_exchange(red + 1, f2u(gin), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else ((LM_GLOBAL uint32_t*)red)[1] = f2u(gin);
-}
-template <int NKC>
-struct NvAmaxIn {
-  uint4 codes[2];
-  uint32_t sc[2];
-  v4i16 aop[8][NKC];
-};
-template <int NKC>
-DEV void nv_amax_load(const NvLane<NKC>& l0, const NvLane<NKC>& l1, int mt, NvAmaxIn<NKC>& t) {
-  constexpr int RPAD = NKC * 16;
-  const lm_u32x4 c0 = *(const LM_GLOBAL lm_u32x4*)(l0.q + (int64_t)mt * 64);
-  const lm_u32x4 c1 = *(const LM_GLOBAL lm_u32x4*)(l1.q + (int64_t)mt * 64);
-  t.codes[0] = make_uint4(c0.x, c0.y, c0.z, c0.w);
-  t.codes[1] = make_uint4(c1.x, c1.y, c1.z, c1.w);
-  t.sc[0] = *(const LM_GLOBAL uint16_t*)(l0.sc + (int64_t)mt * l0.sc_stride);
-  t.sc[1] = *(const LM_GLOBAL uint16_t*)(l1.sc + (int64_t)mt * l1.sc_stride);
-  const LM_GLOBAL uint16_t* at = l0.at + (int64_t)mt * (128 * RPAD);
-#pragma unroll
-  for (int k = 0; k < 8; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, t.aop[k]);
-}
-template <int NKC>
-DEV void nv_amax_body_direct(const NvArgs& a, int64_t row0, int t0, int t1, bool fused) {
-  __shared__ float sh[NV_NW];
-  const int lane = threadIdx.x & 63, wave = wave_index(), rl = lane & 15;
-  const int64_t r0 = row0 + rl, r1 = row0 + 16 + rl;
-  const bool rok0 = r0 < a.M, rok1 = r1 < a.M;
-  const bool second = row0 + 16 < a.M;  // wave-uniform
-  const int ntiles = t1;
-  const float gin = *(const LM_GLOBAL float*)a.gin;
-  // the quant pass reads this copy: the per-tensor scale output may alias gin
-  if (row0 == 0 && t0 == 0 && threadIdx.x == 0) nv_keep_gin(a.red, gin, fused);
-  const float strength = a.strength;
-  // rows past M read row M - 1 (valid memory) and are left out of the max
-  const NvLane<NKC> l0 = nv_lane<NKC>(a, rok0 ? r0 : a.M - 1, lane);
-  const NvLane<NKC> l1 = nv_lane<NKC>(a, rok1 ? r1 : a.M - 1, lane);
-  v4i16 bop0[NKC], bop1[NKC];
-  load_bop_g<NKC>(a.bp, r0, lane, bop0);  // Bp holds ceil(M/16)*16 rows
-  if (second) {
-    load_bop_g<NKC>(a.bp, r1, lane, bop1);
-  } else {
-#pragma unroll
-    for (int k = 0; k < NKC; ++k) bop1[k] = (v4i16){0, 0, 0, 0};
-  }
-  float mx0 = 0.0f, mx1 = 0.0f;
-  if (t0 + wave < ntiles) {
-    NvAmaxIn<NKC> cur;
-    nv_amax_load<NKC>(l0, l1, t0 + wave, cur);
-    for (int mt = t0 + wave; mt < ntiles; mt += NV_NW) {
-      NvAmaxIn<NKC> nxt;
-      nv_amax_load<NKC>(l0, l1, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
-      float m[32];
-      nv_merged_parts<NKC, true>(cur.codes[0], cur.sc[0], cur.aop, bop0, strength, gin, m);
-#pragma unroll
-      for (int j = 0; j < 32; j += 2) mx0 = max3_abs(mx0, m[j], m[j + 1]);
-      if (second) {
-        nv_merged_parts<NKC, true>(cur.codes[1], cur.sc[1], cur.aop, bop1, strength, gin, m);
-#pragma unroll
-        for (int j = 0; j < 32; j += 2) mx1 = max3_abs(mx1, m[j], m[j + 1]);
-      }
-      cur = nxt;
-    }
-  }
-  float mx = __builtin_fmaxf(rok0 ? mx0 : 0.0f, rok1 ? mx1 : 0.0f);
-  mx = wave_max(mx);
-  if (lane == 0) sh[wave] = mx;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float r = sh[0];
-#pragma unroll
-    for (int w = 1; w < NV_NW; ++w) r = __builtin_fmaxf(r, sh[w]);
-    atomicMax(a.red, f2u(bf16r(r)));
-  }
-}
-
-// Plain (unswizzled) scales: the workgroup stages each step's codes and
-// scales through LDS.  A step is the 8 consecutive macro tiles its waves
-// take (wave w: tile ts + w) of the 32 rows.  The codes arrive as 512-byte
-// row segments (two rows per wave instruction) and the scales as 64-byte row
-// segments, one instruction for the whole step.  Loaded per lane, every
-// code and scale instruction touched 16 rows, which kept the
-// texture-address unit busy.  The next step's bytes are requested into
-// registers while the current one is merged.  Row pitches are padded (528
-// and 68 bytes) so that the lanes' LDS reads of one row group do not share
-// banks.
-constexpr int NV_CPITCH = 528, NV_SPITCH = 68;
-template <int NKC>
-DEV void nv_amax_body_lds(const NvArgs& a, int64_t row0, int t0, int t1, bool fused) {
-  constexpr int RPAD = NKC * 16;
-  __shared__ float sh[NV_NW];
-  // two buffers: step s reads buffer s & 1 while the next step's bytes go to
-  // the other one, so a step needs one barrier
-  __shared__ __attribute__((aligned(16))) uint8_t lcodes[2][32 * NV_CPITCH];
-  __shared__ __attribute__((aligned(16))) uint8_t lsc[2][32 * NV_SPITCH];
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(), rl = lane & 15, g = lane >> 4;
-  const int ntiles = t1;
-  const int steps = (ntiles - t0 + NV_NW - 1) / NV_NW;  // workgroup-uniform
-  const int64_t half = a.N >> 1, scols = a.N >> 4;
-  const float gin = *(const LM_GLOBAL float*)a.gin;
-  // the quant pass reads this copy: the per-tensor scale output may alias gin
-  if (row0 == 0 && t0 == 0 && threadIdx.x == 0) nv_keep_gin(a.red, gin, fused);
-  const float strength = a.strength;
-  const bool second = row0 + 16 < a.M;  // workgroup-uniform
-  // staging: thread tid loads code chunks q = tid, tid + 512 (row q >> 5,
-  // 16-byte chunk q & 31 of the row's 512-byte step segment); threads 0..255
-  // load the scales of row tid >> 3, tile tid & 7 (8 bytes)
-  const LM_GLOBAL uint8_t* qb = (const LM_GLOBAL uint8_t*)a.q;
-  const LM_GLOBAL uint8_t* sb = (const LM_GLOBAL uint8_t*)a.scale;
-  auto rowc = [&](int r) { const int64_t row = row0 + r; return row < a.M ? row : a.M - 1; };
-  lm_u32x4 sc0, sc1;
-  lm_u32x2 ss;
-  auto stage = [&](int ts) {
-    const int qa = tid, qq = tid + 512;
-    const int ta = ts + ((qa & 31) >> 2), tq = ts + ((qq & 31) >> 2);
-    const int tca = ta < ntiles ? ta : ntiles - 1, tcq = tq < ntiles ? tq : ntiles - 1;
-    sc0 = *(const LM_GLOBAL lm_u32x4*)(qb + rowc(qa >> 5) * half + (int64_t)tca * 64 + (qa & 3) * 16);
-    sc1 = *(const LM_GLOBAL lm_u32x4*)(qb + rowc(qq >> 5) * half + (int64_t)tcq * 64 + (qq & 3) * 16);
-    if (tid < 256) {
-      const int tt = ts + (tid & 7), tc = tt < ntiles ? tt : ntiles - 1;
-      ss = *(const LM_GLOBAL lm_u32x2*)(sb + rowc(tid >> 3) * scols + (int64_t)tc * 8);
-    }
-  };
-  auto publish = [&](int b) {
-    *(lm_u32x4*)(lcodes[b] + (tid >> 5) * NV_CPITCH + (tid & 31) * 16) = sc0;
-    *(lm_u32x4*)(lcodes[b] + ((tid + 512) >> 5) * NV_CPITCH + (tid & 31) * 16) = sc1;
-    if (tid < 256) {
-      uint32_t* d = (uint32_t*)(lsc[b] + (tid >> 3) * NV_SPITCH + (tid & 7) * 8);
-      d[0] = ss.x;
-      d[1] = ss.y;
-    }
-  };
-  // per wave: its tile's A^T fragments (from L2), one step ahead
-  const int p = lane & 15;
-  const LM_GLOBAL uint16_t* atl = (const LM_GLOBAL uint16_t*)a.at + (int64_t)(32 * (p >> 2) + (p & 3)) * RPAD + g * (NKC * 4);
-  auto load_aop = [&](int ts, v4i16 (&aop)[8][NKC]) {
-    const int mt = ts + wave, mtc = mt < ntiles ? mt : ntiles - 1;
-    const LM_GLOBAL uint16_t* at = atl + (int64_t)mtc * (128 * RPAD);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, aop[k]);
-  };
-  v4i16 bop0[NKC], bop1[NKC];
-  load_bop_g<NKC>(a.bp, row0 + rl, lane, bop0);  // Bp holds ceil(M/16)*16 rows
-  if (second) {
-    load_bop_g<NKC>(a.bp, row0 + 16 + rl, lane, bop1);
-  } else {
-#pragma unroll
-    for (int k = 0; k < NKC; ++k) bop1[k] = (v4i16){0, 0, 0, 0};
-  }
-  float mx0 = 0.0f, mx1 = 0.0f;
-  v4i16 aop[8][NKC];
-  stage(t0);
-  load_aop(t0, aop);
-  publish(0);
-  __syncthreads();
-  for (int s = 0; s < steps; ++s) {
-    const uint8_t* lc = lcodes[s & 1];
-    const uint8_t* ls = lsc[s & 1];
-    const int ts = t0 + s * NV_NW;
-    if (s + 1 < steps) stage(ts + NV_NW);
-    v4i16 nxt[8][NKC];
-    load_aop(ts + NV_NW, nxt);
-    if (ts + wave < ntiles) {
-      const int cofs = wave * 64 + 16 * g, sofs = wave * 8 + 2 * g;
-      float m[32];
-      {
-        const lm_u32x4 c = *(const lm_u32x4*)(lc + rl * NV_CPITCH + cofs);
-        const uint32_t scv = *(const uint16_t*)(ls + rl * NV_SPITCH + sofs);
-        nv_merged_parts<NKC, true>(make_uint4(c.x, c.y, c.z, c.w), scv, aop, bop0, strength, gin, m);
-#pragma unroll
-        for (int j = 0; j < 32; j += 2) mx0 = max3_abs(mx0, m[j], m[j + 1]);
-      }
-      if (second) {
-        const lm_u32x4 c = *(const lm_u32x4*)(lc + (16 + rl) * NV_CPITCH + cofs);
-        const uint32_t scv = *(const uint16_t*)(ls + (16 + rl) * NV_SPITCH + sofs);
-        nv_merged_parts<NKC, true>(make_uint4(c.x, c.y, c.z, c.w), scv, aop, bop1, strength, gin, m);
-#pragma unroll
-        for (int j = 0; j < 32; j += 2) mx1 = max3_abs(mx1, m[j], m[j + 1]);
-      }
-    }
-    // the other buffer was last read in step s - 1, before the barrier that
-    // ended it; after this one, step s + 1 may read it
-    if (s + 1 < steps) publish((s + 1) & 1);
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-#pragma unroll
-      for (int c = 0; c < NKC; ++c) aop[k][c] = nxt[k][c];
-  }
-  const bool rok0 = row0 + rl < a.M, rok1 = row0 + 16 + rl < a.M;
-  float mx = __builtin_fmaxf(rok0 ? mx0 : 0.0f, rok1 ? mx1 : 0.0f);
-  mx = wave_max(mx);
-  if (lane == 0) sh[wave] = mx;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float r = sh[0];
-#pragma unroll
-    for (int w = 1; w < NV_NW; ++w) r = __builtin_fmaxf(r, sh[w]);
-    atomicMax(a.red, f2u(bf16r(r)));
-  }
-}
-// (the staged loads need 16-byte aligned codes and 8-byte aligned scales)
-// fused: the amax pass runs in the same launch as the quant pass
-// (k_nv_fused_stack), which reads the copy of gin as an atomic
-template <int NKC>
-DEV void nv_amax_body(const NvArgs& a, int64_t row0, int t0, int t1, bool fused = false) {
-  if (a.swizzled || (((uintptr_t)a.q) & 15) != 0 || (((uintptr_t)a.scale) & 7) != 0)
-    nv_amax_body_direct<NKC>(a, row0, t0, t1, fused);
-  else
-    nv_amax_body_lds<NKC>(a, row0, t0, t1, fused);
-}
+// the copy of the input per-tensor scale in red[1], which the quant pass reads
+DEV void nv_keep_gin(uint32_t* red, float gin) { ((LM_GLOBAL uint32_t*)red)[1] = f2u(gin); }
 
 // amax_bits, gin_bits: red[0] and red[1] as the amax pass left them (the
 // max |merged| and the copy of the input per-tensor scale); two-level only
@@ -533,12 +317,17 @@ DEV void nv_quant_body(const NvArgs& a, int64_t row0, int t0, int t1, const floa
   }
 }
 
-template <bool PAIRS = false>
+// the item of launch unit t: the last item whose prefix (of the launch's
+// kind of unit) is <= t
+enum : int { NV_TILES = 0, NV_BOUND = 1, NV_REFINE = 2 };
+template <int KIND = NV_TILES>
 DEV int nv_find(const NvStackItem* __restrict__ items, int count, int64_t t) {
   int lo = 0, hi = count - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if ((PAIRS ? items[mid].pair_begin : items[mid].tile_begin) <= t) lo = mid;
+    const NvStackItem& m = items[mid];
+    const int64_t b = KIND == NV_BOUND ? m.bound_begin : KIND == NV_REFINE ? m.refine_begin : m.tile_begin;
+    if (b <= t) lo = mid;
     else hi = mid - 1;
   }
   return lo;
@@ -547,8 +336,6 @@ DEV int nv_find(const NvStackItem* __restrict__ items, int count, int64_t t) {
 // ---- kernels: single tensor (args by value) and grouped (descriptor table) ---
 // One workgroup per 16 rows (tile_begin counts 16-row groups).
 __host__ __device__ static inline int64_t nv_units(int64_t M, int64_t /*N*/) { return (M + 15) / 16; }
-// the amax pass: one workgroup per 32 rows
-__host__ __device__ static inline int64_t nv_pairs(int64_t M) { return (M + 31) / 32; }
 
 // Single tensors: blocks are independent once the global scale is known, so a
 // workgroup owns 16 rows x NV_CHUNK macro tiles (blockIdx.y picks the chunk).
@@ -561,10 +348,6 @@ DEV int nv_chunk_end(const NvArgs& a) {
   const int t1 = ((int)blockIdx.y + 1) * NV_CHUNK, nt = (int)(a.N >> 7);
   return t1 < nt ? t1 : nt;
 }
-template <int NKC>
-__global__ __launch_bounds__(NV_NW * 64) void k_nv_amax(NvArgs a) {
-  nv_amax_body<NKC>(a, (int64_t)blockIdx.x * 32, (int)blockIdx.y * NV_CHUNK, nv_chunk_end(a));
-}
 template <int NKC, bool SR, bool TWO>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant(NvArgs a) {
   __shared__ float rtab[8];
@@ -573,13 +356,6 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant(NvArgs a) {
   const LM_GLOBAL uint32_t* red = (const LM_GLOBAL uint32_t*)a.red;
   nv_quant_body<NKC, TWO, SR>(a, (int64_t)blockIdx.x * 16, (int)blockIdx.y * NV_CHUNK, nv_chunk_end(a), rtab,
                               TWO ? red[0] : 0u, TWO ? red[1] : 0u);
-}
-template <int NKC>
-__global__ __launch_bounds__(NV_NW * 64) void k_nv_amax_stack(const NvStackItem* __restrict__ items, int count) {
-  const int i = nv_find<true>(items, count, blockIdx.x);
-  const NvArgs a = items[i].a;
-  if (a.gin == nullptr) return;  // single-level item: no global scale to find
-  nv_amax_body<NKC>(a, ((int64_t)blockIdx.x - items[i].pair_begin) * 32, 0, (int)(a.N >> 7));
 }
 // TWO: every item of the launch is two-level (the host splits a mixed stack)
 template <int NKC, bool SR, bool TWO>
@@ -593,132 +369,235 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant_stack(const NvStackItem
   nv_quant_body<NKC, TWO, SR>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16, 0, (int)(a.N >> 7), rtab,
                               TWO ? red[0] : 0u, TWO ? red[1] : 0u);
 }
-// ---- grouped two-level stack in one launch ------------------------------------
-// The amax and quant passes of a round-to-nearest stack in one grid (the
-// host keeps two launches for stochastic rounding, where they measured
-// faster).  A workgroup takes the next ticket from a counter, so tickets are
-// handed out in order to running workgroups.  The tickets run through
-// segments, each covering all amax units (32 rows) or all quant units (16
-// rows) of one item.  An item's quant segment is placed at least
-// NV_LOOKAHEAD tickets after its last amax unit.  A quant unit waits until
-// the item's amax units have all published (red[2] counts them), which by
-// then they normally have.
-//   - Waiting cannot deadlock: every ticket before a quant unit's was taken
-//     by a running workgroup, and amax units wait on nothing.  The wait is
-//     bounded all the same (NV_SPIN_LIMIT polls); a unit that gives up sets
-//     the stack workspace's status word (lm_stack_status_offset) and stores
-//     nothing.
-//   - The texture-address-bound amax units and the quant units share the CUs
-//     instead of running one launch after the other.
-//   - An item's codes and scales are read twice within about NV_LOOKAHEAD
-//     units of work (~40 MB of 4096-column rows), so the second read can hit
-//     the 256 MB Infinity Cache.  (Measured per step on the 8B-shaped stack:
-//     4.35-4.37 ms at 512 tickets, 4.42 at 1024, 4.45 at 2048, 4.84 at 4096;
-//     4.84 at 256 and 5.45 at 128, where quant units wait; two launches
-//     4.76.  FETCH_SIZE, which counts L2 misses whether or not the Infinity
-//     Cache holds the line, reads the same as with two launches.)
-// Items must not share buffers (an item may be in place): a quant unit may
-// run while other items' amax units still read.
-struct NvSeg {
-  int32_t item;          // descriptor index
-  int32_t quant;         // 0: amax units, 1: quant units
-  int64_t ticket_begin;  // first ticket of the segment
-};
-constexpr int64_t NV_LOOKAHEAD = 512;
-constexpr uint32_t NV_SPIN_LIMIT = 1u << 20;  // polls of up to ~3 us: a few seconds
-// The fused launch's bounded wait: a quant unit polls at most spin_limit
-// times for need + extra_need finished amax units (extra_need is 0 except
-// under lm_debug_stack_wait, which lets a test make every wait give up while
-// each wave still ends normally).  A unit that gives up stores nothing and
-// sets bit 0 of the caller-visible status word.
-struct NvWait {
-  uint32_t* status;      // sticky status word of the stack workspace
-  uint32_t spin_limit;
-  uint32_t extra_need;
-};
-
-// rank 16: both passes fit 128 VGPRs, two workgroups per CU
-template <int NKC>
-constexpr int nv_fused_min_waves() { return NKC == 1 ? 4 : 1; }
-template <int NKC>
-__global__ __launch_bounds__(NV_NW * 64, nv_fused_min_waves<NKC>()) void k_nv_fused_stack(const NvStackItem* __restrict__ items,
-                                                                  const NvSeg* __restrict__ segs, int nseg,
-                                                                  uint32_t* ctl, NvWait wt) {
-  __shared__ float rtab[8];
-  // [0] the ticket (read by every thread after the first barrier), [1] [2]
-  // the amax words, [3] the quant unit's go / give-up flag: separate slots, so
-  // no thread can read a ticket that the flag has overwritten
-  __shared__ uint32_t sh_w[4];
-  if (threadIdx.x < 8) rtab[threadIdx.x] = kRcpE4M3[threadIdx.x];
-  if (threadIdx.x == 0) sh_w[0] = atomicAdd(ctl, 1u);
-  __syncthreads();
-  const int64_t t = sh_w[0];
-  int lo = 0, hi = nseg - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (segs[mid].ticket_begin <= t) lo = mid;
-    else hi = mid - 1;
-  }
-  const NvSeg sg = segs[lo];
-  const NvArgs& a = items[sg.item].a;
-  const int64_t unit = t - sg.ticket_begin;
-  uint32_t* red = a.red;
-  if (!sg.quant) {
-    nv_amax_body<NKC>(a, unit * 32, 0, (int)(a.N >> 7), true);
-    // Thread 0 made this unit's atomicMax (and unit 0's exchange of the gin
-    // copy), both device-scope atomics; once they are acknowledged, count the
-    // unit.  Everything a quant unit reads from red is an atomic, so no
-    // cache write-back or invalidation is needed (agent-scope release and
-    // acquire fences write back / invalidate the whole L2 of an XCD, which
-    // slowed the launch by a third).
-    if (threadIdx.x == 0) {
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // (flat atomics count in both)
-      __hip_atomic_fetch_add(red + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    return;
-  }
-  if (threadIdx.x == 0) {
-    const uint32_t need = (uint32_t)nv_pairs(a.M) + wt.extra_need;
-    uint32_t polls = 0;
-    uint32_t done = __hip_atomic_load(red + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    while (done < need && polls < wt.spin_limit) {
-      // back off: many waiting workgroups polling one counter slow every
-      // other access (small stacks, where most quant units do wait)
-      const uint32_t reps = polls < 16 ? 1u : (polls < 64 ? 4u : 16u);
-      for (uint32_t k = 0; k < reps; ++k) __builtin_amdgcn_s_sleep(8);
-      ++polls;
-      done = __hip_atomic_load(red + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    const bool ok = done >= need;
-    if (!ok) __hip_atomic_fetch_or(wt.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sh_w[3] = ok ? 1u : 0u;
-    sh_w[1] = __hip_atomic_load(red + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sh_w[2] = __hip_atomic_load(red + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (sh_w[3] == 0u) return;
-  nv_quant_body<NKC, true, false>(a, unit * 16, 0, (int)(a.N >> 7), rtab, sh_w[1], sh_w[2]);
+// ---- the pruned per-tensor amax (two-level) ---------------------------------
+// max |merged| over a tensor without merging every element.  For element
+// (i, j) of a block b, with bs_b = bf16(e4m3(s_b) g) its dequant scale:
+//   |base| = |bf16(e2m1 * bs_b)| <= bf16(6 bs_b)           (|e2m1| <= 6, RNE monotone)
+//   |delta| <= sum_k |B_ik A_kj| <= ||B_i|| ||A_j||          (Cauchy-Schwarz; the
+//              MFMA's fp32 sum of exact bf16 products adds < r 2^-23 relative)
+//   |merged| = |bf16(fma(delta, strength, base))| <= (|base| + |delta| |strength|)(1 + 2^-8)
+// so one bound per 16-row x 128-column tile needs only the tile's 128 scale
+// bytes, its rows' and columns' norms (prep) and the input global scale:
+//   ub = (bf16(6 bf16(e4m3(maxcode) |g|)) + max||B_i|| max||A_j|| |strength| (1 + 2^-10)) (1 + 2^-6)
+// (generous margins, plus 2^-120 for subnormal results; a NaN scale code or a
+// non-finite bound gives +inf).  Three launches then find the exact maximum:
+//   bound  -- every tile's ub; per 128-row chunk the tile with the largest ub;
+//   seed   -- each chunk's best tile merged exactly: atomicMax into red[0];
+//   refine -- every tile whose ub >= red[0] (as read) merged exactly.
+// Skipping is exact: red[0] only ever holds the exact maximum of some merged
+// tile, so a tile with ub < red[0] <= amax holds no element that could raise
+// it.  With weights ~N(0, s) the bound sits a fraction of s above the stored
+// block maximum, and about 1-2% of the tiles of a large tensor are merged.
+constexpr int NV_BOUND_ROWS = 8 * 16;     // rows per bound / seed chunk (one 16-row group per wave)
+constexpr int NV_REFINE_TILES = 8 * 64;   // tiles per refine workgroup (64 per wave)
+constexpr int NV_BOUND_MAX_TILES = 1024;  // tile columns whose norms a bound workgroup keeps in LDS at a time
+__host__ __device__ static inline int64_t nv_tcols(int64_t N) { return N >> 7; }
+__host__ __device__ static inline int64_t nv_bound_units(int64_t M) { return (M + NV_BOUND_ROWS - 1) / NV_BOUND_ROWS; }
+__host__ __device__ static inline int64_t nv_tile_count(int64_t M, int64_t N) { return ((M + 15) / 16) * nv_tcols(N); }
+__host__ __device__ static inline int64_t nv_refine_units(int64_t M, int64_t N) {
+  return (nv_tile_count(M, N) + NV_REFINE_TILES - 1) / NV_REFINE_TILES;
 }
 
-// Ticket order of the fused launch over the `n` two-level descriptors h[0,n):
-// amax segments in item order, each item's quant segment as soon as
-// NV_LOOKAHEAD tickets have followed its last amax unit (or no amax is left).
-// Returns the number of tickets; segs holds 2 n entries.
-static inline int64_t nv_schedule(const NvStackItem* h, int n, NvSeg* segs, int64_t* a_end) {
-  int64_t ticket = 0;
-  int ia = 0, iq = 0, k = 0;
-  while (iq < n) {
-    if (ia < n && (ia <= iq || ticket - a_end[iq] < NV_LOOKAHEAD)) {
-      segs[k++] = NvSeg{ia, 0, ticket};
-      ticket += nv_pairs(h[ia].a.M);
-      a_end[ia++] = ticket;
-    } else {
-      segs[k++] = NvSeg{iq, 1, ticket};
-      ticket += nv_units(h[iq].a.M, h[iq].a.N);
-      ++iq;
+DEV float nv_tile_bound(uint32_t maxcode, bool nan, float bnmax, float anmax, float gin, float strength) {
+  const float bs = bf16r(fp8_value<E4M3>(maxcode) * __builtin_fabsf(gin));
+  const float base = bf16r(6.0f * bs);
+  const float d = bnmax * anmax * __builtin_fabsf(strength) * (1.0f + 0x1p-10f);
+  const float ub = (base + d) * (1.0f + 0x1p-6f) + 0x1p-120f;
+  return (nan || !(ub <= 3.0e38f)) ? __builtin_inff() : ub;
+}
+
+// bound: one workgroup per 128-row chunk, wave w its 16-row group; lane l
+// owns tile columns l, l + 64, ...: it reads the 8 scale bytes of each of the
+// 16 rows (one 8-byte load per row; a wave's loads cover 512 contiguous bytes
+// of a row in the plain layout) and keeps their largest magnitude code, so the
+// bound needs no cross-lane work.  Rows past M repeat the last row, so all 16
+// loads are unconditional and in flight together.  A NaN code (0x7f) is the largest
+// magnitude, so the maximum also flags it.
+DEV uint32_t nv_code_max4(uint32_t m, uint32_t w) {
+  // per-byte maximum of m (bytes <= 0x7f) and w's magnitude codes: for 7-bit
+  // bytes (x | 0x80) - y keeps bit 7 set exactly where x >= y, with no borrow
+  // between bytes
+  const uint32_t x = w & 0x7f7f7f7fu;
+  const uint32_t ge = ((x | 0x80808080u) - m) & 0x80808080u;
+  const uint32_t sel = (ge << 1) - (ge >> 7);  // 0xff in the bytes where x >= m
+  return (x & sel) | (m & ~sel);
+}
+DEV void nv_bound_body(const NvArgs& a, int64_t chunk) {
+  __shared__ float sh_an[NV_BOUND_MAX_TILES];  // max ||A_j|| per tile column
+  __shared__ float sh_best[NV_NW];
+  __shared__ int sh_mt[NV_NW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
+  const int ntn = (int)nv_tcols(a.N);
+  const int64_t mpad = (a.M + 15) / 16 * 16;  // (the host's mpad_of)
+  const float gin = *(const LM_GLOBAL float*)a.gin;
+  // the quant pass reads this copy: the per-tensor scale output may alias gin
+  if (chunk == 0 && tid == 0) nv_keep_gin(a.red, gin);
+  const LM_GLOBAL float* an = (const LM_GLOBAL float*)a.nrm + mpad;
+  const int64_t row0 = chunk * NV_BOUND_ROWS + 16 * wave;
+  const int nrows = a.M - row0 < 16 ? (int)(a.M - row0) : 16;  // <= 0: the wave has no rows
+  const float bnmax = wave_max(lane < nrows ? ((const LM_GLOBAL float*)a.nrm)[row0 + lane] : 0.0f);
+  const int64_t scols = a.N >> 4;
+  LM_GLOBAL float* ubp = (LM_GLOBAL float*)a.ub + (row0 >> 4) * ntn;
+  float best = -1.0f;
+  int best_mt = 0;
+  // strips of NV_BOUND_MAX_TILES tile columns, whose column norms the workgroup keeps in LDS
+  for (int s0 = 0; s0 < ntn; s0 += NV_BOUND_MAX_TILES) {
+    const int s1 = ntn - s0 < NV_BOUND_MAX_TILES ? ntn : s0 + NV_BOUND_MAX_TILES;
+    if (s0 > 0) __syncthreads();  // the previous strip's norms are no longer read
+    // column norms: tile column t is threads 16 t' .. 16 t' + 15 of a pass, 8 columns each
+    for (int t0 = s0; t0 < s1; t0 += NV_NW * 64 / 16) {
+      const int t = t0 + (tid >> 4);
+      float m = 0.0f;
+      if (t < s1) {
+        const lm_u32x4 v0 = *(const LM_GLOBAL lm_u32x4*)(an + (int64_t)t * 128 + (tid & 15) * 8);
+        const lm_u32x4 v1 = *(const LM_GLOBAL lm_u32x4*)(an + (int64_t)t * 128 + (tid & 15) * 8 + 4);
+        m = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(u2f(v0.x), u2f(v0.y)), __builtin_fmaxf(u2f(v0.z), u2f(v0.w))),
+                            __builtin_fmaxf(__builtin_fmaxf(u2f(v1.x), u2f(v1.y)), __builtin_fmaxf(u2f(v1.z), u2f(v1.w))));
+      }
+      m = row_max16(m);
+      if (t < s1 && (tid & 15) == 0) sh_an[t - s0] = m;
+    }
+    __syncthreads();
+    for (int mt = s0 + lane; nrows > 0 && mt < s1; mt += 64) {
+      // 32-bit offsets from the scale base (an item's scales are < 2^31
+      // bytes): a wave-uniform row part plus the lane's column part, so the
+      // loads take the base in scalar registers and one VGPR of offset
+      uint32_t cm = 0u;
+      const LM_GLOBAL uint8_t* sb = (const LM_GLOBAL uint8_t*)a.scale;
+      if (!a.swizzled) {
+        const uint32_t off = (uint32_t)mt * 8u;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t ro = (uint32_t)((row0 + (r < nrows ? r : nrows - 1)) * scols);
+          const lm_u32x2 w = *(const LM_GLOBAL lm_u32x2*)(sb + (ro + off));
+          cm = nv_code_max4(nv_code_max4(cm, w.x), w.y);
+        }
+      } else {
+        // 128x4 swizzle: the scale columns 4 c .. 4 c + 3 of a row are 4
+        // consecutive bytes and column block c + 1 starts 512 bytes later, so
+        // the lane's 8 columns are words at row part + 1024 mt and + 512
+        const uint32_t off = (uint32_t)mt * 1024u;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t ro = (uint32_t)blocked_offset(row0 + (r < nrows ? r : nrows - 1), 0, scols, true);
+          const uint32_t w0 = *(const LM_GLOBAL uint32_t*)(sb + (ro + off));
+          const uint32_t w1 = *(const LM_GLOBAL uint32_t*)(sb + (ro + off + 512u));
+          cm = nv_code_max4(nv_code_max4(cm, w0), w1);
+        }
+      }
+      const uint32_t c2 = (cm & 0xffu) > ((cm >> 8) & 0xffu) ? (cm & 0xffu) : ((cm >> 8) & 0xffu);
+      const uint32_t c3 = ((cm >> 16) & 0xffu) > (cm >> 24) ? ((cm >> 16) & 0xffu) : (cm >> 24);
+      const uint32_t cmax = c2 > c3 ? c2 : c3;
+      const float ub = nv_tile_bound(cmax, cmax == 0x7fu, bnmax, sh_an[mt - s0], gin, a.strength);
+      ubp[mt] = ub;
+      if (ub > best) {
+        best = ub;
+        best_mt = mt;
+      }
     }
   }
-  return ticket;
+  if (nrows > 0) {  // wave-uniform
+    // the wave's best tile: the largest bound, the lowest lane among equals
+    const float wb = wave_max(best);
+    const uint64_t who = __ballot(best == wb);
+    const int src = (int)__builtin_ctzll(who);
+    best_mt = __builtin_amdgcn_readlane(best_mt, src);
+    best = wb;
+  }
+  if (lane == 0) {
+    sh_best[wave] = best;
+    sh_mt[wave] = best_mt;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int w = 0;
+    for (int k = 1; k < NV_NW; ++k)
+      if (sh_best[k] > sh_best[w]) w = k;
+    // the chunk's best tile, as its index in the item's tile grid
+    const int64_t best_tile = ((chunk * NV_BOUND_ROWS + 16 * w) >> 4) * ntn + sh_mt[w];
+    ((LM_GLOBAL int32_t*)a.ub)[nv_tile_count(a.M, a.N) + chunk] = (int32_t)best_tile;
+  }
+}
+
+// max |bf16(merged)| over tile `tile` (16 rows x 128 columns), by one wave,
+// with the quant pass's merge arithmetic (rows past M left out)
+template <int NKC>
+DEV float nv_tile_exact(const NvArgs& a, int64_t tile, float gin) {
+  const int lane = threadIdx.x & 63;
+  const int ntn = (int)nv_tcols(a.N);
+  const int64_t row0 = (tile / ntn) * 16, row = row0 + (lane & 15);
+  const int mt = (int)(tile % ntn);
+  const bool rok = row < a.M;
+  const NvLane<NKC> l = nv_lane<NKC>(a, rok ? row : a.M - 1, lane);
+  v4i16 bop[NKC];
+  load_bop_g<NKC>(a.bp, row, lane, bop);  // Bp holds ceil(M/16)*16 rows
+  NvTileIn<NKC> t;
+  nv_load_tile<NKC>(l, mt, t);
+  float m[32];
+  nv_merged<NKC, true>(t, bop, a.strength, gin, m);
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; j += 2) mx = max3_abs(mx, m[j], m[j + 1]);
+  return bf16r(wave_max(rok ? mx : 0.0f));
+}
+
+// seed: wave w of workgroup u merges the best tile of chunk 8 u + w
+template <int NKC>
+DEV void nv_seed_body(const NvArgs& a, int64_t chunk) {
+  if (chunk >= nv_bound_units(a.M)) return;  // wave-uniform
+  const float gin = *(const LM_GLOBAL float*)a.gin;
+  const int64_t tile = ((const LM_GLOBAL int32_t*)a.ub)[nv_tile_count(a.M, a.N) + chunk];
+  const float mx = nv_tile_exact<NKC>(a, tile, gin);
+  if ((threadIdx.x & 63) == 0) atomicMax(a.red, f2u(mx));
+}
+
+// refine: wave w of chunk c checks tiles 512 c + 64 w + lane against the
+// current lower bound and merges, one at a time, those that reach it
+template <int NKC>
+DEV void nv_refine_body(const NvArgs& a, int64_t chunk) {
+  const int lane = threadIdx.x & 63, wave = wave_index();
+  const int64_t ntiles = nv_tile_count(a.M, a.N);
+  const int64_t t = chunk * NV_REFINE_TILES + 64 * wave + lane;
+  const float ub = t < ntiles ? ((const LM_GLOBAL float*)a.ub)[t] : -1.0f;
+  const float lb = u2f(__hip_atomic_load(a.red, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  uint64_t todo = __ballot(ub >= lb);
+  if (todo == 0) return;
+  const float gin = *(const LM_GLOBAL float*)a.gin;
+  float mx = 0.0f;
+  while (todo) {
+    const int k = __builtin_ctzll(todo);
+    todo &= todo - 1;
+    mx = __builtin_fmaxf(mx, nv_tile_exact<NKC>(a, chunk * NV_REFINE_TILES + 64 * wave + k, gin));
+  }
+  if (lane == 0) atomicMax(a.red, f2u(mx));
+}
+
+static __global__ __launch_bounds__(NV_NW * 64) void k_nv_bound(NvArgs a) { nv_bound_body(a, blockIdx.x); }
+template <int NKC>
+__global__ __launch_bounds__(NV_NW * 64) void k_nv_seed(NvArgs a) {
+  nv_seed_body<NKC>(a, (int64_t)blockIdx.x * NV_NW + wave_index());
+}
+template <int NKC>
+__global__ __launch_bounds__(NV_NW * 64) void k_nv_refine(NvArgs a) { nv_refine_body<NKC>(a, blockIdx.x); }
+// stacks: the bound and seed launches count 128-row chunks of the two-level
+// items (bound_begin), the seed launch 8 chunks per workgroup; the refine
+// launch counts 512-tile chunks (refine_begin)
+static __global__ __launch_bounds__(NV_NW * 64) void k_nv_bound_stack(const NvStackItem* __restrict__ items, int count) {
+  const int i = nv_find<NV_BOUND>(items, count, blockIdx.x);
+  nv_bound_body(items[i].a, (int64_t)blockIdx.x - items[i].bound_begin);
+}
+template <int NKC>
+__global__ __launch_bounds__(NV_NW * 64) void k_nv_seed_stack(const NvStackItem* __restrict__ items, int count,
+                                                              int64_t chunks) {
+  const int64_t c = (int64_t)blockIdx.x * NV_NW + wave_index();  // wave-uniform
+  if (c >= chunks) return;
+  const int i = nv_find<NV_BOUND>(items, count, c);
+  nv_seed_body<NKC>(items[i].a, c - items[i].bound_begin);
+}
+template <int NKC>
+__global__ __launch_bounds__(NV_NW * 64) void k_nv_refine_stack(const NvStackItem* __restrict__ items, int count) {
+  const int i = nv_find<NV_REFINE>(items, count, blockIdx.x);
+  nv_refine_body<NKC>(items[i].a, (int64_t)blockIdx.x - items[i].refine_begin);
 }
 
 // bf16 factors, a rank bucket, whole macro tiles
@@ -727,13 +606,19 @@ static inline bool nv_fast_ok(int cd, int nkc, int64_t M, int64_t N) {
   return cd == LM_BF16 && nkc > 0 && (N % 128) == 0 && M * N <= (int64_t(1) << 35);
 }
 
-// single tensor: amax (two-level), then quant on `st`
+// single tensor: the pruned amax (two-level; prep gave it the factors' norms),
+// then quant on `st`
 static int nv_fast_run(const NvArgs& a, int nkc, bool sr, hipStream_t st) {
   const dim3 grid((unsigned)nv_units(a.M, a.N), (unsigned)(((a.N >> 7) + NV_CHUNK - 1) / NV_CHUNK)), block(NV_NW * 64);
   if (a.gin) {
+    if (a.nrm == nullptr || a.ub == nullptr) return fail(LM_EINVAL, "nvfp4 two-level merge without its norm workspace");
     TimedLaunch timed("nvfp4", st);
-    const dim3 agrid((unsigned)nv_pairs(a.M), grid.y);
-    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_amax<NKC_>), agrid, block, 0, st, a));
+    const int64_t chunks = nv_bound_units(a.M);
+    hipLaunchKernelGGL(k_nv_bound, dim3((unsigned)chunks), block, 0, st, a);
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_seed<NKC_>), dim3((unsigned)((chunks + NV_NW - 1) / NV_NW)),
+                                                   block, 0, st, a));
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_refine<NKC_>), dim3((unsigned)nv_refine_units(a.M, a.N)),
+                                                   block, 0, st, a));
     LAUNCH_CHECK();
   }
   {

@@ -5,22 +5,11 @@
 // ---------------------------------------------------------------------------
 // stacks
 // ---------------------------------------------------------------------------
-// Stack workspace: the descriptor tables, then one 256-byte block whose first
-// word is the caller-visible status word (never cleared by the library), then
-// 256 bytes of slack, then the per-item regions.
-static size_t stack_status_off(int32_t count) {
+// Stack workspace: the descriptor tables, 256 bytes of slack, then the
+// per-item regions.
+extern "C" size_t lm_stack_workspace_extra(int32_t count) {
   return align256((size_t)count * sizeof(PrepItem)) + align256((size_t)count * sizeof(RowStackItem)) +
-         align256((size_t)count * sizeof(BlkArgs));
-}
-extern "C" size_t lm_stack_workspace_extra(int32_t count) { return stack_status_off(count) + 512; }
-extern "C" size_t lm_stack_status_offset(int32_t count) { return stack_status_off(count); }
-
-// test hook for the fused NVFP4 launch's bounded wait (see NvWait)
-static uint32_t g_spin_limit = NV_SPIN_LIMIT, g_extra_need = 0;
-extern "C" int lm_debug_stack_wait(uint32_t spin_limit, uint32_t extra_need) {
-  g_spin_limit = spin_limit;
-  g_extra_need = extra_need;
-  return LM_OK;
+         align256((size_t)count * sizeof(BlkArgs)) + 256;
 }
 
 static int stack_layout(const lm_stack_item* items, int32_t count, void* ws, size_t wsb, PrepItem* preps,
@@ -44,6 +33,8 @@ static int stack_layout(const lm_stack_item* items, int32_t count, void* ws, siz
     p.at = (uint16_t*)(base + cursor + w.at_off);
     p.bp = (uint16_t*)(base + cursor + w.bp_off);
     p.red = (uint32_t*)(base + cursor + w.red_off);
+    p.nrm = (float*)(base + cursor + w.nrm_off);
+    p.ub = (float*)(base + cursor + w.ub_off);
     p.nred = 64;
     p.vec_b = prep_vec_b(p);
     cursor += w.total;
@@ -177,41 +168,28 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
   return rc;
 }
 
-// Grouped NVFP4 merge.  Two-level items: round-to-nearest runs amax and
-// quant in one fused launch (k_nv_fused_stack), stochastic rounding one amax
-// launch and one quant launch.  Measured on the 8B-shaped stack (MI355X): the
-// fused launch takes round-to-nearest from 4.76 to 4.36 ms per step, but
-// stochastic rounding from 5.07 to 5.11 ms: its quant units keep the VALU
-// busy on their own (Philox), so the amax units' memory-bound phases have
-// nothing to hide behind.  Single-level items: one quant launch.
-// `dev_items` is workspace for the descriptor table (the BlkArgs region of
-// lm_stack_workspace_extra), `dev_segs` for the fused launch's ticket
-// segments (the RowStackItem region, unused by NVFP4).
+// Grouped NVFP4 merge.  Two-level items: the pruned amax (bound, seed and
+// refine launches over all of them), then one quant launch; single-level
+// items: one quant launch.  `dev_items` is workspace for the descriptor table
+// (the BlkArgs region of lm_stack_workspace_extra).
 static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swizzled, bool sr, const PrepItem* preps,
-                         uint8_t* dev_items, uint8_t* dev_segs, uint32_t* status, hipStream_t st) {
+                         uint8_t* dev_items, hipStream_t st) {
   static_assert(sizeof(NvStackItem) <= sizeof(BlkArgs), "NVFP4 stack descriptors must fit the workspace slot");
-  static_assert(2 * sizeof(NvSeg) <= sizeof(RowStackItem), "NVFP4 ticket segments must fit the workspace slot");
   NvStackItem* h = (NvStackItem*)calloc(count, sizeof(NvStackItem));
-  NvSeg* segs = (NvSeg*)calloc(2 * (size_t)count, sizeof(NvSeg));
-  int64_t* a_end = (int64_t*)calloc(count, sizeof(int64_t));
-  if (!h || !segs || !a_end) {
-    free(h);
-    free(segs);
-    free(a_end);
-    return fail(LM_EINVAL, "host allocation failed");
-  }
+  if (!h) return fail(LM_EINVAL, "host allocation failed");
   // two-level items first, then single-level ones; each group numbers its
   // 16-row units from 0 and gets its own quant launch
   int n_two = 0;
   for (int i = 0; i < count; ++i) n_two += items[i].aux != nullptr ? 1 : 0;
   int64_t tiles[2] = {0, 0};
-  int64_t pairs = 0;  // 32-row amax units of the two-level items
+  int64_t bounds = 0, refines = 0;  // the pruned amax: 128-row bound chunks, 512-tile refine chunks
   int slot[2] = {0, n_two};
   int rc = LM_OK;
   for (int i = 0; i < count && rc == LM_OK; ++i) {
     const lm_stack_item& s = items[i];
     if (!s.q || !s.scale || !s.q_out || !s.scale_out) rc = fail(LM_EINVAL, "stack item %d has a null pointer", i);
     if (s.aux && !s.aux_out) rc = fail(LM_EINVAL, "stack item %d: two-level NVFP4 needs a per-tensor scale output", i);
+    if (s.aux && !preps[i].norms) rc = fail(LM_EINVAL, "stack item %d: two-level NVFP4 without its norm workspace", i);
     const int grp = s.aux != nullptr ? 0 : 1;
     NvStackItem& it = h[slot[grp]++];
     NvArgs& a = it.a;
@@ -224,6 +202,8 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
     a.at = preps[i].at;
     a.bp = preps[i].bp;
     a.red = preps[i].red;
+    a.nrm = preps[i].norms ? preps[i].nrm : nullptr;
+    a.ub = preps[i].ub;
     a.M = s.M;
     a.N = s.N;
     a.strength = s.lora.strength;
@@ -231,44 +211,39 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
     a.seed = s.seed;
     it.tile_begin = tiles[grp];
     tiles[grp] += nv_units(s.M, s.N);
-    it.pair_begin = pairs;
-    if (grp == 0) pairs += nv_pairs(s.M);
+    it.bound_begin = bounds;
+    it.refine_begin = refines;
+    if (grp == 0) {
+      bounds += nv_bound_units(s.M);
+      refines += nv_refine_units(s.M, s.N);
+    }
     if (rc == LM_OK && swizzled) rc = zero_swizzle_pad((uint8_t*)s.scale_out, s.M, s.N / 16, st);
   }
   if (rc == LM_OK) rc = lm_stage_h2d(dev_items, h, sizeof(NvStackItem) * count, st);
-  int64_t tickets = 0;
-  const bool fused = !sr;
-  if (rc == LM_OK && n_two > 0 && fused) {
-    tickets = nv_schedule(h, n_two, segs, a_end);
-    if (tickets != pairs + tiles[0] || tickets > 0x7fffffff) rc = fail(LM_EUNSUPPORTED, "nvfp4 stack too large for one launch");
-    if (rc == LM_OK) rc = lm_stage_h2d(dev_segs, segs, sizeof(NvSeg) * 2 * n_two, st);
-  }
+  if (rc == LM_OK && (bounds > 0x7fffffff || refines > 0x7fffffff))
+    rc = fail(LM_EUNSUPPORTED, "nvfp4 stack too large for one launch");
   const int nkc = preps[0].rpad / 16;
   const dim3 block(NV_NW * 64);
   const NvStackItem* d = (const NvStackItem*)dev_items;
-  if (rc == LM_OK && n_two > 0 && !fused) {
+  if (rc == LM_OK && n_two > 0) {
     TimedLaunch timed("nvfp4", st);
-    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_amax_stack<NKC_>), dim3((unsigned)pairs), block, 0, st, d, n_two));
+    hipLaunchKernelGGL(k_nv_bound_stack, dim3((unsigned)bounds), block, 0, st, d, n_two);
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_seed_stack<NKC_>), dim3((unsigned)((bounds + NV_NW - 1) / NV_NW)),
+                                                   block, 0, st, d, n_two, bounds));
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_refine_stack<NKC_>), dim3((unsigned)refines), block, 0, st, d,
+                                                   n_two));
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 amax launch: %s", hipGetErrorString(e));
+    if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 pruned amax launches: %s", hipGetErrorString(e));
   }
-  if (rc == LM_OK && n_two > 0 && !fused) {
+  if (rc == LM_OK && n_two > 0) {
     TimedLaunch timed("nvfp4", st);
-    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, true, true>), dim3((unsigned)tiles[0]), block, 0,
-                                                   st, d, n_two));
+#define NQ2(SR_)                                                                                                      \
+  NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, SR_, true>), dim3((unsigned)tiles[0]), block, 0, \
+                                                 st, d, n_two))
+    if (sr) { NQ2(true); } else { NQ2(false); }
+#undef NQ2
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 quant launch: %s", hipGetErrorString(e));
-  }
-  if (rc == LM_OK && n_two > 0 && fused) {
-    // ticket counter: red[3] of the first two-level item (cleared by the
-    // prep launch); a quant unit that gives up waiting sets *status
-    uint32_t* ctl = h[0].a.red + 3;
-    const NvWait wt{status, g_spin_limit, g_extra_need};
-    TimedLaunch timed("nvfp4", st);
-    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_fused_stack<NKC_>), dim3((unsigned)tickets), block, 0, st, d,
-                                                   (const NvSeg*)dev_segs, 2 * n_two, ctl, wt));
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 fused launch: %s", hipGetErrorString(e));
   }
   if (rc == LM_OK && tiles[1] > 0) {
     TimedLaunch timed("nvfp4", st);
@@ -281,8 +256,6 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 quant launch: %s", hipGetErrorString(e));
   }
   free(h);
-  free(segs);
-  free(a_end);
   return rc;
 }
 
@@ -302,16 +275,16 @@ extern "C" int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, i
   PrepItem* preps = (PrepItem*)calloc(count, sizeof(PrepItem));
   if (!preps) return fail(LM_EINVAL, "host allocation failed");
   int rc = stack_layout(items, count, workspace, workspace_bytes, preps, cursor);
+  // two-level items with bf16 factors: the factors' norms for the pruned amax
+  for (int i = 0; rc == LM_OK && i < count; ++i) preps[i].norms = items[i].aux && items[i].lora.dtype == LM_BF16 ? 1 : 0;
   if (rc == LM_OK) rc = stack_prep(preps, count, base, st);
   bool fast = rc == LM_OK;
   for (int i = 0; fast && i < count; ++i)
     fast = nv_fast_ok(items[i].lora.dtype, preps[i].rpad / 16, items[i].M, items[i].N) &&
            nkc_bucket(preps[i].rpad / 16) == nkc_bucket(preps[0].rpad / 16) && check_nvfp4(items[i].M, items[i].N) == 0;
   if (fast) {
-    uint8_t* dev_segs = base + align256((size_t)count * sizeof(PrepItem));
-    rc = nv_stack_fast(items, count, swizzled, rounding_mode == LM_ROUND_STOCHASTIC, preps,
-                       dev_segs + align256((size_t)count * sizeof(RowStackItem)), dev_segs,
-                       (uint32_t*)(base + stack_status_off(count)), st);
+    uint8_t* dev_blk = base + align256((size_t)count * sizeof(PrepItem)) + align256((size_t)count * sizeof(RowStackItem));
+    rc = nv_stack_fast(items, count, swizzled, rounding_mode == LM_ROUND_STOCHASTIC, preps, dev_blk, st);
     free(preps);
     return rc;
   }

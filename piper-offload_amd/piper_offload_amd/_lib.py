@@ -70,8 +70,6 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lm_last_error": (ctypes.c_char_p, []),
     "lm_workspace_size": (_SZ, [_I64, _I64, _I32]),
     "lm_stack_workspace_extra": (_SZ, [_I32]),
-    "lm_stack_status_offset": (_SZ, [_I32]),
-    "lm_debug_stack_wait": (_I32, [ctypes.c_uint32, ctypes.c_uint32]),
     "lm_int8_merge": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _L, _R, _P, _SZ, _P]),
     "lm_int8_merge_noalloc": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _L, _R, _P]),
     "lm_int8_requant": (_I32, [_P, _I32, _P, _P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _R, _P, _SZ, _P]),

@@ -222,11 +222,8 @@ class ReloadMergePipeline:
         return Reloaded(layer, slot, bufs, ready)
 
     def synchronize(self) -> None:
-        """Wait for every issued merge; raise ``RuntimeError`` if a grouped NVFP4 merge was incomplete."""
+        """Wait for every issued merge."""
         self.merge_stream.synchronize()
-        for plans in self._plans.values():
-            for plan, _ in plans:
-                plan.synchronize()
 
     def release(self, reloaded: Reloaded, stream: torch.cuda.Stream | None = None) -> None:
         """The consumer on ``stream`` (default: current) is done with ``reloaded``'s slot.

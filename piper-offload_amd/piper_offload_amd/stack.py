@@ -18,7 +18,7 @@ import torch
 
 from . import _lib as L
 
-__all__ = ["StackPlan", "StackTarget", "check_stack_status", "merge_int8_stack", "merge_nvfp4_stack"]
+__all__ = ["StackPlan", "StackTarget", "merge_int8_stack", "merge_nvfp4_stack"]
 
 
 @dataclass(slots=True)
@@ -41,9 +41,9 @@ def _byte_range(t: torch.Tensor) -> tuple[int, int]:
 
 
 def _reject_shared_buffers(targets: Sequence[StackTarget]) -> None:
-    """Items of one grouped launch must not share storage: a fused NVFP4 launch quantizes one item while
-    others are still being read, so two items over the same bytes (one weight twice, views of one fused
-    tensor, one shared per-tensor scale) would give results that depend on scheduling."""
+    """Items of one grouped launch must not share storage: the launch merges its items in place at the same
+    time, so two items over the same bytes (one weight twice, views of one fused tensor, one shared
+    per-tensor scale) would read each other's outputs, with results that depend on scheduling."""
     spans = []
     for i, t in enumerate(targets):
         w = t.weight
@@ -104,14 +104,6 @@ class StackPlan:
     table).  A merge therefore makes its stream wait for the previous merge's
     completion event, so merges issued on different streams run one after the
     other instead of overwriting buffers an earlier launch still reads.
-
-    NVFP4 merges may run as one fused launch whose quant units wait, bounded,
-    for their item's amax units.  A unit that gives up stores nothing and sets
-    the workspace's status word.  After each NVFP4 merge the word is copied to
-    pinned host memory on the merge's stream; the next :meth:`merge` checks the
-    copy once it has arrived, and :meth:`synchronize` waits for it.  Either
-    raises ``RuntimeError`` if the word was set.  No host synchronization is
-    added to a merge.
     """
 
     def __init__(self, targets: Sequence[StackTarget], kind: str) -> None:
@@ -141,38 +133,11 @@ class StackPlan:
             self._ws = L.workspace(self._ws_bytes, self.device)
         self._ws_ptr = L.aligned_ptr(self._ws)
         self._last: torch.cuda.Event | None = None  # completion of the previous merge
-        # the workspace's status word (written only by fused NVFP4 launches), zeroed once here
-        off = self._ws_ptr - self._ws.data_ptr() + int(L.lib().lm_stack_status_offset(len(self.targets)))
-        self._status_dev = self._ws[off:off + 4].view(torch.int32)
-        self._status_host: torch.Tensor | None = None
-        self._status_evt: torch.cuda.Event | None = None  # the copy of the word after the last NVFP4 merge
-        if kind == "nvfp4":
-            self._status_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
-            with torch.cuda.device(self.device):
-                self._status_dev.zero_()
-
-    def _check_status(self, wait: bool) -> None:
-        """Raise if a finished NVFP4 merge's fused launch gave up a wait; ``wait`` blocks until the
-        last merge's copy of the status word has arrived."""
-        evt = self._status_evt
-        if evt is None or (not wait and not evt.query()):
-            return
-        evt.synchronize()
-        self._status_evt = None
-        assert self._status_host is not None
-        if int(self._status_host[0]) != 0:
-            with torch.cuda.device(self.device):
-                self._status_dev.zero_()
-            self._status_host.zero_()
-            raise RuntimeError("NVFP4 stack merge incomplete: a quantization unit of the fused launch gave up "
-                               "waiting for its tensor's amax pass and stored nothing; the merged weights of that "
-                               "call are not valid")
 
     def synchronize(self) -> None:
-        """Wait for the last merge and raise ``RuntimeError`` if it was incomplete."""
+        """Wait for the last merge."""
         if self._last is not None:
             self._last.synchronize()
-        self._check_status(wait=True)
 
     def merge(self, seeds: Sequence[int] | None = None, *, stochastic: bool = True) -> None:
         """Merge every target once; ``seeds`` (one per target) replace the targets' seeds."""
@@ -181,7 +146,6 @@ class StackPlan:
                 raise ValueError("one seed per target is required")
             for it, seed in zip(self._arr, seeds):
                 it.seed = int(seed)
-        self._check_status(wait=False)
         lib = L.lib()
         mode = L.LM_ROUND_STOCHASTIC if stochastic else L.LM_ROUND_NEAREST
         with torch.cuda.device(self.device):
@@ -198,13 +162,6 @@ class StackPlan:
             # the caching allocator must not hand the workspace to another stream
             # while this merge may still read it
             self._ws.record_stream(current)
-            if rc == L.LM_OK and self.kind == "nvfp4":
-                if self._status_evt is not None:  # an earlier copy still in flight: it lands first
-                    self._status_evt.synchronize()
-                    self._check_status(wait=True)
-                self._status_host.copy_(self._status_dev, non_blocking=True)
-                self._status_evt = torch.cuda.Event()
-                self._status_evt.record(current)
             if rc == L.LM_OK:
                 self._last = torch.cuda.Event()
                 self._last.record(current)
@@ -218,40 +175,13 @@ def merge_int8_stack(targets: Sequence[StackTarget], *, stochastic: bool = True)
     merge_once(targets, "int8", stochastic=stochastic)
 
 
-_pending: list[StackPlan] = []  # one-shot NVFP4 merges whose status word has not been checked yet
-
-
-def check_stack_status(wait: bool = True) -> None:
-    """Check the one-shot NVFP4 stack merges issued so far (``merge_nvfp4_stack``): raise ``RuntimeError`` if
-    one of them was incomplete.  ``wait=False`` checks only those that have finished."""
-    keep = []
-    try:
-        while _pending:
-            plan = _pending.pop(0)
-            if not wait and plan._status_evt is not None and not plan._status_evt.query():
-                keep.append(plan)
-                continue
-            plan._check_status(wait=True)
-    finally:
-        _pending[:0] = keep
-
-
 def merge_once(targets: Sequence[StackTarget], kind: str, *, stochastic: bool) -> None:
-    """One grouped merge of ``targets`` with their own seeds, through a plan used once.  An NVFP4 plan is kept
-    until its status word has been checked: by the next one-shot merge once it has finished, or by
-    :func:`check_stack_status`."""
-    check_stack_status(wait=False)
-    plan = StackPlan(targets, kind)
-    plan.merge([t.seed for t in targets], stochastic=stochastic)
-    if kind == "nvfp4":
-        _pending.append(plan)
+    """One grouped merge of ``targets`` with their own seeds, through a plan used once."""
+    StackPlan(targets, kind).merge([t.seed for t in targets], stochastic=stochastic)
 
 
 def merge_nvfp4_stack(targets: Sequence[StackTarget], *, stochastic: bool = True) -> None:
-    """Merge many NVFP4 weights in place with grouped launches over all targets.
-
-    Asynchronous, like every merge here: a fused launch that gave up a wait is reported by the next
-    one-shot stack merge once that merge has finished, or by :func:`check_stack_status`."""
+    """Merge many NVFP4 weights in place with grouped launches over all targets."""
     if not targets:
         return
     merge_once(targets, "nvfp4", stochastic=stochastic)

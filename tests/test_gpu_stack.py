@@ -9,7 +9,7 @@ wrong: the grouped kernels, the single-target kernels, or both.  The dense
 merge itself is checked against the oracle within the floating-point
 contract in the per-format tests.
 
-The last two tests run config 5 at full size: all 224 targets of the
+Two tests run config 5 at full size: all 224 targets of the
 32-layer 8B-shaped stack in one grouped call, sampled targets against the
 oracle and every target against its single-target merge and by properties
 computed with torch on the GPU (code range, the scale recipe, two-neighbour
@@ -367,50 +367,50 @@ def test_stack_plan_merges_on_two_streams_run_in_order():
         assert torch.equal(t.weight.scale.cpu().reshape(-1), rs.reshape(-1))
 
 
-# ---- the fused NVFP4 launch's bounded wait ---------------------------------------
-def test_nvfp4_fused_stack_give_up_is_reported():
-    """Force every quant unit of the fused round-to-nearest launch to give up its bounded wait (the test
-    hook asks for amax units that never come, with a budget of 4 polls, so every wave still ends
-    normally): the merge must be reported incomplete at the next check, and a normal merge afterwards
-    must match the oracle again."""
-    from piper_offload_amd import _lib
-    from piper_offload_amd.stack import check_stack_status
+# ---- the pruned per-tensor amax of two-level NVFP4 ---------------------------------
+def _pruned_case(case: str, swizzled: bool):  # noqa: ANN202
+    """(weight, b, a, strength) of one two-level target that stresses the pruned amax (bound, seed, refine)."""
+    if case == "wide":  # more than 1024 tile columns: the bound pass takes its column norms in strips
+        rows, cols = 20, 1026 * 128
+        b, a = lora_factors(rows, cols, 16, 41)
+        return _nvfp4_weight(rows, cols, 42, True, swizzled), b.to(DEV), a.to(DEV), 1.0
+    if case == "loose":
+        # The tile of rows 0-15, columns 0-127 has the largest bound (||B_i|| ||A_j|| = 1) but a zero delta
+        # (B_i and A_j are orthogonal), so the seed merges it and finds only its base values; the largest
+        # merged value is in rows 16-31, columns 128-255 (base weights x3), which only the refine pass sees.
+        rows, cols = 64, 512
+        w = normal_bf16((rows, cols), 0.02, 43)
+        w[16:32, 128:256] *= 3
+        q, sc, pts = O.nvfp4_requant(bf16_np(w), swizzled=swizzled, two_level=True)
+        wt = NVFP4Weight(torch.from_numpy(q).to(DEV), torch.from_numpy(sc).view(torch.float8_e4m3fn).to(DEV),
+                         torch.from_numpy(pts.reshape(())).to(DEV), 16, torch.bfloat16, swizzled)
+        b = torch.zeros((rows, 16), dtype=torch.bfloat16)
+        a = torch.zeros((16, cols), dtype=torch.bfloat16)
+        b[:16, 0] = 1.0
+        a[1, :128] = 1.0
+        return wt, b.to(DEV), a.to(DEV), 1.0
+    # "delta": the update dominates the base weights, so the bounds are loose everywhere and many tiles
+    # are merged exactly; negative strength
+    rows, cols = 96, 1024
+    b, a = lora_factors(rows, cols, 16, 44, a_std=0.5, b_std=0.5)
+    return _nvfp4_weight(rows, cols, 45, True, swizzled), b.to(DEV), a.to(DEV), -30.0
 
-    lib = _lib.lib()
-    shapes = [(256, 512), (128, 1024), (64, 256)]
-    targets, expected = [], []
-    for i, (rows, cols) in enumerate(shapes):
-        b, a = lora_factors(rows, cols, 16, 700 + i)
-        b, a = b.to(DEV), a.to(DEV)
-        w = _nvfp4_weight(rows, cols, 710 + i, True, False)
-        targets.append(StackTarget(w, b, a, 1.0, derive_seed(f"give_up.{i}.weight", 0)))
-    plan = StackPlan(targets, "nvfp4")
-    before = [t.weight.qdata.clone() for t in targets]
-    assert lib.lm_debug_stack_wait(4, 1 << 20) == 0
-    try:
-        plan.merge(stochastic=False)
-    finally:
-        assert lib.lm_debug_stack_wait(1 << 20, 0) == 0
-    with pytest.raises(RuntimeError, match="incomplete"):
-        plan.synchronize()
-    # nothing was quantized: the codes are untouched
-    for t, q0 in zip(targets, before):
-        assert torch.equal(t.weight.qdata, q0)
-    plan.synchronize()  # the error was reported once and the status word cleared
-    for t in targets:
-        expected.append(_nvfp4_oracle(t.weight, t.b, t.a, t.strength, t.seed, False))
-    plan.merge(stochastic=False)
-    plan.synchronize()
-    errors = []
-    for i, (t, exp) in enumerate(zip(targets, expected)):
-        errors += _nvfp4_errors("stack", i, t.weight.qdata, t.weight.scale, t.weight.per_tensor_scale, exp)
+
+@pytest.mark.parametrize("case", ["wide", "loose", "delta"])
+@pytest.mark.parametrize("swizzled", [False, True])
+@pytest.mark.parametrize("sr", [False, True])
+def test_nvfp4_pruned_amax_edge_cases(case, swizzled, sr):
+    w, b, a, strength = _pruned_case(case, swizzled)
+    seed = derive_seed(f"pruned.{case}.weight", 3)
+    expected = _nvfp4_oracle(w, b, a, strength, seed, sr)
+    pq, ps, ppts = K.merge_nvfp4_lora(w.qdata, w.scale, w.per_tensor_scale, 16, swizzled, b, a, strength,
+                                      rounding_seed=seed if sr else None)
+    errors = _nvfp4_errors("per-target", 0, pq, ps, ppts, expected)
+    # the same target in a stack, after a regular one
+    w0 = _nvfp4_weight(64, 256, 46, True, swizzled)
+    b0, a0 = (x.to(DEV) for x in lora_factors(64, 256, 16, 47))
+    exp0 = _nvfp4_oracle(w0, b0, a0, 1.0, seed + 1, sr)
+    merge_nvfp4_stack([StackTarget(w0, b0, a0, 1.0, seed + 1), StackTarget(w, b, a, strength, seed)], stochastic=sr)
+    errors += _nvfp4_errors("stack", 0, w0.qdata, w0.scale, w0.per_tensor_scale, exp0)
+    errors += _nvfp4_errors("stack", 1, w.qdata, w.scale, w.per_tensor_scale, expected)
     assert not errors, "\n".join(errors)
-    # the one-shot path reports through check_stack_status
-    assert lib.lm_debug_stack_wait(4, 1 << 20) == 0
-    try:
-        merge_nvfp4_stack(targets, stochastic=False)
-    finally:
-        assert lib.lm_debug_stack_wait(1 << 20, 0) == 0
-    with pytest.raises(RuntimeError, match="incomplete"):
-        check_stack_status()
-    check_stack_status()
