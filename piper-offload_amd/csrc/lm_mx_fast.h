@@ -86,7 +86,7 @@ DEV void mx_load_tile(const MxLane<ELEM, NKC>& l, int mt, MxTileIn<ELEM, NKC>& t
 
 template <int ELEM, int NKC, bool SR>
 DEV void mx_tile(const MxArgs& a, const MxTileIn<ELEM, NKC>& in, const v4i16 (&bop)[NKC], int64_t row, int mt,
-                 int lane, uint8_t* qo, uint8_t* so) {
+                 int lane, uint8_t* qo, uint8_t* so, bool rok) {
   constexpr float L = MxTraits<ELEM>::maxpos;
   float d[32];
 #pragma unroll
@@ -147,7 +147,7 @@ DEV void mx_tile(const MxArgs& a, const MxTileIn<ELEM, NKC>& in, const v4i16 (&b
         words[k] = wd;
       }
     }
-    *(uint4*)(qo + (int64_t)mt * 64) = make_uint4(words[0], words[1], words[2], words[3]);
+    if (rok) *(uint4*)(qo + (int64_t)mt * 64) = make_uint4(words[0], words[1], words[2], words[3]);
   } else {
     uint32_t wv[8];
 #pragma unroll
@@ -155,11 +155,13 @@ DEV void mx_tile(const MxArgs& a, const MxTileIn<ELEM, NKC>& in, const v4i16 (&b
       if constexpr (SR) wv[i] = sr_fp8_nword<ELEM>(x + 4 * i, nw + 2 * i);
       else wv[i] = fp8_pack4<ELEM>(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
     }
-    uint4* dst = (uint4*)(qo + (int64_t)mt * 128);
-    dst[0] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
-    dst[1] = make_uint4(wv[4], wv[5], wv[6], wv[7]);
+    if (rok) {
+      uint4* dst = (uint4*)(qo + (int64_t)mt * 128);
+      dst[0] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+      dst[1] = make_uint4(wv[4], wv[5], wv[6], wv[7]);
+    }
   }
-  so[0] = (uint8_t)enc;
+  if (rok) so[0] = (uint8_t)enc;
 }
 
 // Chunks of 16 tiles: for MXFP4 [14336, 4096] whole 32-tile rows measured
@@ -184,7 +186,8 @@ __global__ __launch_bounds__(NV_NW * 64) void k_mx_fast(MxArgs a) {
   for (int mt = t0 + wave; mt < ntiles; mt += NV_NW) {
     MxTileIn<ELEM, NKC> nxt;
     mx_load_tile<ELEM, NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
-    if (rok) mx_tile<ELEM, NKC, SR>(a, cur, bop, row, mt, lane, l.q, l.sc + (int64_t)mt * l.sc_stride);
+    // every lane merges (the MFMAs read all lanes' operands); rows past M store nothing
+    mx_tile<ELEM, NKC, SR>(a, cur, bop, row, mt, lane, l.q, l.sc + (int64_t)mt * l.sc_stride, rok);
     cur = nxt;
   }
 }

@@ -77,42 +77,60 @@ struct NvTileIn {
   v4i16 aop[8][NKC];
 };
 
-// Per-lane base pointers; every per-tile address is base + mt * stride, and
-// the A^T fragments of a tile use immediate offsets.  Scales: mt advances the
-// scale column by 8, which is 8 bytes in the plain layout and 2 col-blocks =
-// 1024 bytes in the 128x4 swizzle (P/_triton_nvfp4_lora.py:88-104).
-template <int NKC>
+// Per-lane addresses: a wave-uniform base (scalar registers) plus a 32-bit
+// lane offset, so the loads and stores take the base as an SGPR pair and the
+// per-tile offset needs one 32-bit add (nv_fast_ok bounds N so that a 16-row
+// group's codes and an item's scales and A^T fit 32-bit offsets).  Every
+// per-tile offset is lane offset + mt * stride, and the A^T fragments of a
+// tile use immediate offsets.  Scales: mt advances the scale column by 8,
+// which is 8 bytes in the plain layout and 2 col-blocks = 1024 bytes in the
+// 128x4 swizzle (P/_triton_nvfp4_lora.py:88-104).  The output codes and
+// scales share the input's layout, so the stores reuse q_off and sc_off.
 // (global-address-space pointers: the stack kernels read them from a
 // descriptor table, and flat accesses would make every wait a full one)
+template <int NKC>
 struct NvLane {
-  const LM_GLOBAL uint8_t* q;
-  const LM_GLOBAL uint8_t* sc;
-  const LM_GLOBAL uint16_t* at;
-  int64_t sc_stride;
+  const LM_GLOBAL uint8_t* q;   // codes of the 16-row group's first row
+  const LM_GLOBAL uint8_t* sc;  // the item's scales
+  const LM_GLOBAL uint8_t* at;  // the item's A^T (bytes)
+  uint32_t q_off, sc_off, at_off, sc_stride;
 };
 
+// row0: the 16-row group's first row (wave-uniform); rowc: the lane's row,
+// clamped to M - 1
 template <int NKC>
-DEV NvLane<NKC> nv_lane(const NvArgs& a, int64_t rowc, int lane) {
+DEV NvLane<NKC> nv_lane(const NvArgs& a, int64_t row0, int64_t rowc, int lane) {
   constexpr int RPAD = NKC * 16;
   const int p = lane & 15, g = lane >> 4;
   NvLane<NKC> l;
-  l.q = (const LM_GLOBAL uint8_t*)a.q + rowc * (a.N >> 1) + 16 * g;
-  l.sc = (const LM_GLOBAL uint8_t*)a.scale + blocked_offset(rowc, 2 * g, a.N >> 4, a.swizzled);
-  l.sc_stride = a.swizzled ? 1024 : 8;
-  l.at = (const LM_GLOBAL uint16_t*)a.at + (int64_t)(32 * (p >> 2) + (p & 3)) * RPAD + g * (NKC * 4);
+  l.q = (const LM_GLOBAL uint8_t*)a.q + row0 * (a.N >> 1);
+  l.q_off = (uint32_t)((rowc - row0) * (a.N >> 1)) + 16u * (uint32_t)g;
+  l.sc = (const LM_GLOBAL uint8_t*)a.scale;
+  l.sc_off = (uint32_t)blocked_offset(rowc, 2 * g, a.N >> 4, a.swizzled);
+  l.sc_stride = a.swizzled ? 1024u : 8u;
+  l.at = (const LM_GLOBAL uint8_t*)a.at;
+  l.at_off = 2u * ((uint32_t)(32 * (p >> 2) + (p & 3)) * RPAD + (uint32_t)g * (NKC * 4));
   return l;
 }
 
 template <int NKC>
-DEV void nv_load_tile(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
-  constexpr int RPAD = NKC * 16;
-  const lm_u32x4 c = *(const LM_GLOBAL lm_u32x4*)(l.q + (int64_t)mt * 64);
+DEV void nv_load_codes(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
+  const lm_u32x4 c = *(const LM_GLOBAL lm_u32x4*)(l.q + (l.q_off + (uint32_t)mt * 64u));
   t.codes = make_uint4(c.x, c.y, c.z, c.w);
   // the lane's scale column is even: both blocks' scales are adjacent bytes
-  t.sc = *(const LM_GLOBAL uint16_t*)(l.sc + (int64_t)mt * l.sc_stride);
-  const LM_GLOBAL uint16_t* at = l.at + (int64_t)mt * (128 * RPAD);
+  t.sc = *(const LM_GLOBAL uint16_t*)(l.sc + (l.sc_off + (uint32_t)mt * l.sc_stride));
+}
+template <int NKC>
+DEV void nv_load_aop(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
+  constexpr int RPAD = NKC * 16;
+  const LM_GLOBAL uint16_t* at = (const LM_GLOBAL uint16_t*)(l.at + (l.at_off + (uint32_t)mt * (256u * RPAD)));
 #pragma unroll
   for (int k = 0; k < 8; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, t.aop[k]);
+}
+template <int NKC>
+DEV void nv_load_tile(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
+  nv_load_codes<NKC>(l, mt, t);
+  nv_load_aop<NKC>(l, mt, t);
 }
 
 // merged values of the lane's 32 columns, for max |merged| (the reference's
@@ -254,12 +272,15 @@ DEV void nv_quant_block(const NvArgs& a, int64_t row, int mt, int lane, float gq
 }
 
 // merge + quantize one tile, block by block, then one 16-byte code store and
-// one 2-byte scale store
+// one 2-byte scale store (qo, so: the outputs' bases, at the lane offsets of
+// l), by lanes whose row is < M.  Every lane runs the merge: an MFMA reads
+// its operands from all 64 lanes whatever the exec mask, so the operand
+// loads must not be skipped for the rows past M (a load under a lane
+// condition leaves those lanes' registers stale).
 template <int NKC, bool TWO, bool SR>
 DEV void nv_quant_tile(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float gin, int64_t row,
                        int mt, int lane, float gq, float inv_g, const float* rtab, LM_GLOBAL uint8_t* qo,
-                       LM_GLOBAL uint8_t* so,
-                       int64_t so_stride) {
+                       LM_GLOBAL uint8_t* so, const NvLane<NKC>& l, bool rok) {
   uint32_t words[4];
   uint32_t scb = 0;
   {
@@ -272,8 +293,10 @@ DEV void nv_quant_tile(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&b
     nv_merged_block<NKC, TWO, 1>(in, bop, a.strength, gin, m);
     nv_quant_block<TWO, SR, 1>(a, row, mt, lane, gq, inv_g, rtab, m, words, scb);
   }
-  *(LM_GLOBAL lm_u32x4*)(qo + (int64_t)mt * 64) = lm_u32x4{words[0], words[1], words[2], words[3]};
-  *(LM_GLOBAL uint16_t*)(so + (int64_t)mt * so_stride) = (uint16_t)scb;
+  if (rok) {
+    *(LM_GLOBAL lm_u32x4*)(qo + (l.q_off + (uint32_t)mt * 64u)) = lm_u32x4{words[0], words[1], words[2], words[3]};
+    *(LM_GLOBAL uint16_t*)(so + (l.sc_off + (uint32_t)mt * l.sc_stride)) = (uint16_t)scb;
+  }
 }
 
 // ---- pass bodies -------------------------------------------------------------
@@ -301,19 +324,26 @@ DEV void nv_quant_body(const NvArgs& a, int64_t row0, int t0, int t1, const floa
     inv_g = 1.0f / gq;
     if (row0 == 0 && t0 == 0 && threadIdx.x == 0 && a.gout != nullptr) *(LM_GLOBAL float*)a.gout = gq;
   }
-  const NvLane<NKC> l = nv_lane<NKC>(a, rowc, lane);
-  LM_GLOBAL uint8_t* qo = (LM_GLOBAL uint8_t*)a.q_out + rowc * (a.N >> 1) + 16 * (lane >> 4);
-  LM_GLOBAL uint8_t* so = (LM_GLOBAL uint8_t*)a.scale_out + blocked_offset(rowc, 2 * (lane >> 4), a.N >> 4, a.swizzled);
+  const NvLane<NKC> l = nv_lane<NKC>(a, row0, rowc, lane);
+  LM_GLOBAL uint8_t* qo = (LM_GLOBAL uint8_t*)a.q_out + row0 * (a.N >> 1);
+  LM_GLOBAL uint8_t* so = (LM_GLOBAL uint8_t*)a.scale_out;
   v4i16 bop[NKC];
   load_bop_g<NKC>(a.bp, row, lane, bop);
   if (t0 + wave >= ntiles) return;
+  // The next tile's codes and scales (HBM) are requested before the current
+  // tile is merged; its A^T fragments (L2) at the top of its own iteration.
+  // Prefetching the fragments too held 16 more VGPRs (103 against 87 for
+  // round-to-nearest): 8B-shaped stack 3.72 -> 3.53 ms per step without it
+  // (round-to-nearest), 4.06 -> 3.92 (stochastic).
   NvTileIn<NKC> cur;
-  nv_load_tile<NKC>(l, t0 + wave, cur);
+  nv_load_codes<NKC>(l, t0 + wave, cur);
   for (int mt = t0 + wave; mt < ntiles; mt += NV_NW) {
+    nv_load_aop<NKC>(l, mt, cur);
     NvTileIn<NKC> nxt;
-    nv_load_tile<NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
-    if (rok) nv_quant_tile<NKC, TWO, SR>(a, cur, bop, gin, row, mt, lane, gq, inv_g, rtab, qo, so, l.sc_stride);
-    cur = nxt;
+    nv_load_codes<NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
+    nv_quant_tile<NKC, TWO, SR>(a, cur, bop, gin, row, mt, lane, gq, inv_g, rtab, qo, so, l, rok);
+    cur.codes = nxt.codes;
+    cur.sc = nxt.sc;
   }
 }
 
@@ -528,7 +558,7 @@ DEV float nv_tile_exact(const NvArgs& a, int64_t tile, float gin) {
   const int64_t row0 = (tile / ntn) * 16, row = row0 + (lane & 15);
   const int mt = (int)(tile % ntn);
   const bool rok = row < a.M;
-  const NvLane<NKC> l = nv_lane<NKC>(a, rok ? row : a.M - 1, lane);
+  const NvLane<NKC> l = nv_lane<NKC>(a, row0, rok ? row : a.M - 1, lane);
   v4i16 bop[NKC];
   load_bop_g<NKC>(a.bp, row, lane, bop);  // Bp holds ceil(M/16)*16 rows
   NvTileIn<NKC> t;
@@ -601,9 +631,10 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_refine_stack(const NvStackIte
 }
 
 // bf16 factors, a rank bucket, whole macro tiles
-// (M N <= 2^35: the stochastic-rounding counters, offset / 8, fit 32 bits)
+// (M N <= 2^35: the stochastic-rounding counters, offset / 8, fit 32 bits;
+// M N / 16 < 2^31 and N <= 2^22: scale, A^T and 16-row code offsets fit 32 bits)
 static inline bool nv_fast_ok(int cd, int nkc, int64_t M, int64_t N) {
-  return cd == LM_BF16 && nkc > 0 && (N % 128) == 0 && M * N <= (int64_t(1) << 35);
+  return cd == LM_BF16 && nkc > 0 && (N % 128) == 0 && M * N <= (int64_t(1) << 35) && N <= (int64_t(1) << 22);
 }
 
 // single tensor: the pruned amax (two-level; prep gave it the factors' norms),
