@@ -201,7 +201,7 @@ class Int8Stack(Workload):
 
 
 class Nvfp4Stack(Workload):
-    family = "nvfp4"  # amax pass + quant pass of the two-level merge
+    family = "nvfp4"  # the pruned-amax launches + the quant launch of the two-level merge
 
     def __init__(self, layers: int, stochastic: bool) -> None:
         from piper_offload_amd.stack import StackTarget
