@@ -190,12 +190,39 @@ __device__ __forceinline__ void prep_unit(const PrepItem& it, int64_t u) {
     src = (const LM_GLOBAL uint16_t*)it.a + (live ? col : 0);
     stride = it.lda;
   }
+  // (B rows 8 bytes per load, A columns unrolled by 8, so that a thread's
+  // loads are in flight together: with one 2-byte load per rank step the 8B
+  // NVFP4 stack's prep launch took 108 us, now 60 us)
   float ss = 0.0f;
-  if (live)
-    for (int k = 0; k < it.rank; ++k) {
+  if (live && stride == 1 && it.vec_b) {  // a B row, 4 ranks (8 bytes) per load
+    const LM_GLOBAL lm_u32x2* s2 = (const LM_GLOBAL lm_u32x2*)src;
+    for (int k4 = 0; k4 < it.rank / 4; k4 += 4) {
+      lm_u32x2 w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = k4 + j < it.rank / 4 ? s2[k4 + j] : lm_u32x2{0u, 0u};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float v0 = bf16_lo(w[j].x), v1 = bf16_hi(w[j].x), v2 = bf16_lo(w[j].y), v3 = bf16_hi(w[j].y);
+        ss = __builtin_fmaf(v0, v0, ss);
+        ss = __builtin_fmaf(v1, v1, ss);
+        ss = __builtin_fmaf(v2, v2, ss);
+        ss = __builtin_fmaf(v3, v3, ss);
+      }
+    }
+  } else if (live) {
+    int k = 0;
+    for (; k + 8 <= it.rank; k += 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = u2f((uint32_t)src[(k + j) * stride] << 16);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(v[j], v[j], ss);
+    }
+    for (; k < it.rank; ++k) {
       const float v = u2f((uint32_t)src[k * stride] << 16);
       ss = __builtin_fmaf(v, v, ss);
     }
+  }
   ((LM_GLOBAL float*)it.nrm)[u] = live ? __builtin_sqrtf(ss) * (1.0f + 0x1p-16f) : 0.0f;
 }
 
