@@ -64,14 +64,13 @@ static inline int64_t mpad_of(int64_t M) { return (M + 15) / 16 * 16; }
 // (for the two-pass long-row kernels) Mpad words of row amax bits and Mpad
 // copies of the input row scales
 // then, for the pruned per-tensor amax of two-level NVFP4: the Euclidean norms
-// of B's rows and A's columns (Mpad + Npad floats), one upper bound of
-// max |merged| per 16-row x 128-column tile and one best-bound tile per
-// 128-row chunk (nv_bound_units)
+// of B's rows and A's columns (Mpad + Npad floats) and one upper bound of
+// max |merged| per 16-row x 128-column tile
 struct WsLayout {
   size_t at_off, bp_off, red_off, nrm_off, ub_off, total;
 };
 static inline int64_t red_words(int64_t M) { return 64 + 2 * mpad_of(M); }
-static inline int64_t ub_words(int64_t M, int64_t N) { return mpad_of(M) / 16 * (npad_of(N) / 128) + (M + 127) / 128; }
+static inline int64_t ub_words(int64_t M, int64_t N) { return mpad_of(M) / 16 * (npad_of(N) / 128); }
 static WsLayout ws_layout(int64_t M, int64_t N, int rank) {
   WsLayout w;
   int rp = rpad_of(rank);

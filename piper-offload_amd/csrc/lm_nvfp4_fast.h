@@ -18,7 +18,7 @@
 // Two-level tensors take two passes (P/_triton_nvfp4_lora.py:437-512, 327-366):
 //   amax  -- max |bf16(merged)| over the tensor into red[0] (float bits, so
 //            atomicMax on uint orders them), found without merging every
-//            tile (the pruned amax below: bound, seed, refine); the
+//            tile (the pruned amax below: bound with seed, refine); the
 //            reference reduces bf16(merged), and since RNE is monotone the
 //            max of the rounded values is the rounded max of the unrounded
 //            ones;
@@ -42,7 +42,7 @@ struct NvArgs {
   const uint16_t* bp;
   uint32_t* red;           // red[0]: max |merged| bits (cleared by the prep kernel)
   const float* nrm;        // ||B_i|| (Mpad rows), then ||A_j|| (Npad columns): the pruned amax
-  float* ub;               // per-tile bounds, then per-chunk best tiles: the pruned amax
+  float* ub;               // per-tile bounds: the pruned amax
   int64_t M, N;
   float strength;
   int swizzled;
@@ -51,7 +51,7 @@ struct NvArgs {
 struct NvStackItem {
   NvArgs a;
   int64_t tile_begin;    // prefix of 16-row groups (quant launches)
-  int64_t bound_begin;   // prefix of 128-row chunks (pruned amax: bound and seed launches)
+  int64_t bound_begin;   // prefix of 128-row chunks (pruned amax: bound launch)
   int64_t refine_begin;  // prefix of 512-tile chunks (pruned amax: refine launch)
 };
 
@@ -410,15 +410,16 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant_stack(const NvStackItem
 // bytes, its rows' and columns' norms (prep) and the input global scale:
 //   ub = (bf16(6 bf16(e4m3(maxcode) |g|)) + max||B_i|| max||A_j|| |strength| (1 + 2^-10)) (1 + 2^-6)
 // (generous margins, plus 2^-120 for subnormal results; a NaN scale code or a
-// non-finite bound gives +inf).  Three launches then find the exact maximum:
-//   bound  -- every tile's ub; per 128-row chunk the tile with the largest ub;
-//   seed   -- each chunk's best tile merged exactly: atomicMax into red[0];
+// non-finite bound gives +inf).  Two launches then find the exact maximum:
+//   bound  -- every tile's ub; then (seed) each 128-row chunk's tile with the
+//             largest ub merged exactly by the chunk's wave 0: atomicMax
+//             into red[0];
 //   refine -- every tile whose ub >= red[0] (as read) merged exactly.
 // Skipping is exact: red[0] only ever holds the exact maximum of some merged
 // tile, so a tile with ub < red[0] <= amax holds no element that could raise
 // it.  With weights ~N(0, s) the bound sits a fraction of s above the stored
-// block maximum, and about 1-2% of the tiles of a large tensor are merged.
-constexpr int NV_BOUND_ROWS = 8 * 16;     // rows per bound / seed chunk (one 16-row group per wave)
+// block maximum; on the 8B-shaped stack about 0.5% of the tiles are merged.
+constexpr int NV_BOUND_ROWS = 8 * 16;     // rows per bound chunk (one 16-row group per wave)
 constexpr int NV_REFINE_TILES = 8 * 64;   // tiles per refine workgroup (64 per wave)
 constexpr int NV_BOUND_MAX_TILES = 1024;  // tile columns whose norms a bound workgroup keeps in LDS at a time
 __host__ __device__ static inline int64_t nv_tcols(int64_t N) { return N >> 7; }
@@ -452,7 +453,8 @@ DEV uint32_t nv_code_max4(uint32_t m, uint32_t w) {
   const uint32_t sel = (ge << 1) - (ge >> 7);  // 0xff in the bytes where x >= m
   return (x & sel) | (m & ~sel);
 }
-DEV void nv_bound_body(const NvArgs& a, int64_t chunk) {
+// returns the chunk's tile with the largest bound (the same in every thread)
+DEV int64_t nv_bound_body(const NvArgs& a, int64_t chunk) {
   __shared__ float sh_an[NV_BOUND_MAX_TILES];  // max ||A_j|| per tile column
   __shared__ float sh_best[NV_NW];
   __shared__ int sh_mt[NV_NW];
@@ -539,14 +541,12 @@ DEV void nv_bound_body(const NvArgs& a, int64_t chunk) {
     sh_mt[wave] = best_mt;
   }
   __syncthreads();
-  if (tid == 0) {
-    int w = 0;
-    for (int k = 1; k < NV_NW; ++k)
-      if (sh_best[k] > sh_best[w]) w = k;
-    // the chunk's best tile, as its index in the item's tile grid
-    const int64_t best_tile = ((chunk * NV_BOUND_ROWS + 16 * w) >> 4) * ntn + sh_mt[w];
-    ((LM_GLOBAL int32_t*)a.ub)[nv_tile_count(a.M, a.N) + chunk] = (int32_t)best_tile;
-  }
+  // the chunk's best tile, as its index in the item's tile grid: the largest
+  // bound, the lowest wave among equals (every thread reads the same slots)
+  int w = 0;
+  for (int k = 1; k < NV_NW; ++k)
+    if (sh_best[k] > sh_best[w]) w = k;
+  return ((chunk * NV_BOUND_ROWS + 16 * w) >> 4) * ntn + sh_mt[w];
 }
 
 // max |bf16(merged)| over tile `tile` (16 rows x 128 columns), by one wave,
@@ -571,13 +571,14 @@ DEV float nv_tile_exact(const NvArgs& a, int64_t tile, float gin) {
   return bf16r(wave_max(rok ? mx : 0.0f));
 }
 
-// seed: wave w of workgroup u merges the best tile of chunk 8 u + w
+// bound + seed: the chunk's bounds, then wave 0 merges the chunk's best tile
+// exactly and folds its maximum into red[0] (red[0] then only ever holds the
+// exact maximum of some merged tile)
 template <int NKC>
-DEV void nv_seed_body(const NvArgs& a, int64_t chunk) {
-  if (chunk >= nv_bound_units(a.M)) return;  // wave-uniform
-  const float gin = *(const LM_GLOBAL float*)a.gin;
-  const int64_t tile = ((const LM_GLOBAL int32_t*)a.ub)[nv_tile_count(a.M, a.N) + chunk];
-  const float mx = nv_tile_exact<NKC>(a, tile, gin);
+DEV void nv_bound_seed(const NvArgs& a, int64_t chunk) {
+  const int64_t best = nv_bound_body(a, chunk);
+  if (wave_index() != 0) return;  // wave-uniform; no barrier follows
+  const float mx = nv_tile_exact<NKC>(a, best, *(const LM_GLOBAL float*)a.gin);
   if ((threadIdx.x & 63) == 0) atomicMax(a.red, f2u(mx));
 }
 
@@ -602,27 +603,16 @@ DEV void nv_refine_body(const NvArgs& a, int64_t chunk) {
   if (lane == 0) atomicMax(a.red, f2u(mx));
 }
 
-static __global__ __launch_bounds__(NV_NW * 64) void k_nv_bound(NvArgs a) { nv_bound_body(a, blockIdx.x); }
 template <int NKC>
-__global__ __launch_bounds__(NV_NW * 64) void k_nv_seed(NvArgs a) {
-  nv_seed_body<NKC>(a, (int64_t)blockIdx.x * NV_NW + wave_index());
-}
+__global__ __launch_bounds__(NV_NW * 64) void k_nv_bound(NvArgs a) { nv_bound_seed<NKC>(a, blockIdx.x); }
 template <int NKC>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_refine(NvArgs a) { nv_refine_body<NKC>(a, blockIdx.x); }
-// stacks: the bound and seed launches count 128-row chunks of the two-level
-// items (bound_begin), the seed launch 8 chunks per workgroup; the refine
-// launch counts 512-tile chunks (refine_begin)
-static __global__ __launch_bounds__(NV_NW * 64) void k_nv_bound_stack(const NvStackItem* __restrict__ items, int count) {
-  const int i = nv_find<NV_BOUND>(items, count, blockIdx.x);
-  nv_bound_body(items[i].a, (int64_t)blockIdx.x - items[i].bound_begin);
-}
+// stacks: the bound launch counts 128-row chunks of the two-level items
+// (bound_begin), the refine launch 512-tile chunks (refine_begin)
 template <int NKC>
-__global__ __launch_bounds__(NV_NW * 64) void k_nv_seed_stack(const NvStackItem* __restrict__ items, int count,
-                                                              int64_t chunks) {
-  const int64_t c = (int64_t)blockIdx.x * NV_NW + wave_index();  // wave-uniform
-  if (c >= chunks) return;
-  const int i = nv_find<NV_BOUND>(items, count, c);
-  nv_seed_body<NKC>(items[i].a, c - items[i].bound_begin);
+__global__ __launch_bounds__(NV_NW * 64) void k_nv_bound_stack(const NvStackItem* __restrict__ items, int count) {
+  const int i = nv_find<NV_BOUND>(items, count, blockIdx.x);
+  nv_bound_seed<NKC>(items[i].a, (int64_t)blockIdx.x - items[i].bound_begin);
 }
 template <int NKC>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_refine_stack(const NvStackItem* __restrict__ items, int count) {
@@ -645,9 +635,7 @@ static int nv_fast_run(const NvArgs& a, int nkc, bool sr, hipStream_t st) {
     if (a.nrm == nullptr || a.ub == nullptr) return fail(LM_EINVAL, "nvfp4 two-level merge without its norm workspace");
     TimedLaunch timed("nvfp4", st);
     const int64_t chunks = nv_bound_units(a.M);
-    hipLaunchKernelGGL(k_nv_bound, dim3((unsigned)chunks), block, 0, st, a);
-    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_seed<NKC_>), dim3((unsigned)((chunks + NV_NW - 1) / NV_NW)),
-                                                   block, 0, st, a));
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_bound<NKC_>), dim3((unsigned)chunks), block, 0, st, a));
     NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_refine<NKC_>), dim3((unsigned)nv_refine_units(a.M, a.N)),
                                                    block, 0, st, a));
     LAUNCH_CHECK();

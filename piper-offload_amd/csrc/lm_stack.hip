@@ -168,7 +168,7 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
   return rc;
 }
 
-// Grouped NVFP4 merge.  Two-level items: the pruned amax (bound, seed and
+// Grouped NVFP4 merge.  Two-level items: the pruned amax (bound-and-seed and
 // refine launches over all of them), then one quant launch; single-level
 // items: one quant launch.  `dev_items` is workspace for the descriptor table
 // (the BlkArgs region of lm_stack_workspace_extra).
@@ -227,9 +227,8 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
   const NvStackItem* d = (const NvStackItem*)dev_items;
   if (rc == LM_OK && n_two > 0) {
     TimedLaunch timed("nvfp4", st);
-    hipLaunchKernelGGL(k_nv_bound_stack, dim3((unsigned)bounds), block, 0, st, d, n_two);
-    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_seed_stack<NKC_>), dim3((unsigned)((bounds + NV_NW - 1) / NV_NW)),
-                                                   block, 0, st, d, n_two, bounds));
+    NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_bound_stack<NKC_>), dim3((unsigned)bounds), block, 0, st, d,
+                                                   n_two));
     NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_refine_stack<NKC_>), dim3((unsigned)refines), block, 0, st, d,
                                                    n_two));
     hipError_t e = hipGetLastError();
