@@ -99,7 +99,7 @@ struct PrepItem {
   int64_t work_begin;  // prefix of per-item work units (k_prep1: 0)
   int64_t block_begin; // prefix of per-item k_prep_many workgroups
   int vec_b;           // B rows load 4 ranks at once (ldb, rank % 4 == 0, 8-byte aligned)
-  int at_rows16;       // rank 16, At in the row kernels' tile order (at_rows16_offset)
+  int at_order;        // At order: AT_PLAIN, AT_ROWS16 (row kernels, rank 16), AT_NV16 (NVFP4 kernels, rank 16)
   float* nrm;          // with norms: ||B_i|| for rows [0, Mpad), then ||A_j|| for columns [0, Npad)
   int norms;           // bf16 factors: compute nrm (the pruned NVFP4 amax bounds the delta by them)
   float* ub;           // the item's tile-bound region (not written by prep)
@@ -115,6 +115,17 @@ __host__ __device__ inline int64_t at_rows16_offset(int64_t col, int g) {
   const int c = (int)(col & 63), k = (c >> 2) & 3, lane = ((c >> 4) << 2) + (c & 3) + 16 * g;
   return (col >> 6) * 1024 + (((k >> 1) * 64 + lane) * 2 + (k & 1)) * 4;
 }
+// At for the NVFP4 kernels at rank <= 16 (RPAD 16): per 128-column macro
+// tile, 2048 elements ordered [kp][lane][kk][i], so that lane l's A^T
+// fragments of the tile's 8 MFMAs (k = 2 kp + kk) arrive in four 16-byte
+// loads, each load of the wave covering 1 KiB contiguously.  Lane
+// l = p + 16 g takes column 32 (p >> 2) + 4 k + (p & 3) of the tile at ranks
+// 4 g + i (the columns and ranks of the plain order).
+__host__ __device__ inline int64_t at_nv16_offset(int64_t col, int g) {
+  const int c = (int)(col & 127), r = c & 31, k = r >> 2, lane = ((c >> 5) << 2) + (r & 3) + 16 * g;
+  return (col >> 7) * 2048 + ((k >> 1) * 64 + lane) * 8 + (k & 1) * 4;
+}
+enum : int { AT_PLAIN = 0, AT_ROWS16 = 1, AT_NV16 = 2 };
 
 __device__ __forceinline__ void prep_unit(const PrepItem& it, int64_t u) {
   // units: [0, Npad*rpad/4) for At, then [.., + Mpad*rpad/4) for Bp, then 1
@@ -136,7 +147,8 @@ __device__ __forceinline__ void prep_unit(const PrepItem& it, int64_t u) {
       v[i] = (k < it.rank && col < it.N) ? ((const LM_GLOBAL uint16_t*)it.a)[(int64_t)k * it.lda + col] : (uint16_t)0;
     }
     const lm_u32x2 w = {(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16)};
-    const int64_t off = it.at_rows16 ? at_rows16_offset(col, g) : col * it.rpad + (g * nkc + kc) * 4;
+    const int64_t off = it.at_order == AT_ROWS16 ? at_rows16_offset(col, g)
+                      : it.at_order == AT_NV16 ? at_nv16_offset(col, g) : col * it.rpad + (g * nkc + kc) * 4;
     *(LM_GLOBAL lm_u32x2*)((LM_GLOBAL uint16_t*)it.at + off) = w;
     return;
   }
@@ -1629,7 +1641,7 @@ static inline int check_lora(const lm_lora* l, int64_t M, int64_t N) {
 // rows_split: the call runs the two-pass long-row kernels, whose row amax
 // slots the prep launch clears
 static inline int setup(Ctx& c, int64_t M, int64_t N, const lm_lora* l, void* ws, size_t wsb, void* stream,
-                        bool rows_split = false, bool norms = false) {
+                        bool rows_split = false, bool norms = false, int at_order = AT_PLAIN) {
   c.st = (hipStream_t)stream;
   const int rank = l ? l->rank : 0;
   WsLayout w = ws_layout(M, N, rank);
@@ -1657,6 +1669,7 @@ static inline int setup(Ctx& c, int64_t M, int64_t N, const lm_lora* l, void* ws
   it.work_begin = 0;
   it.block_begin = 0;
   it.vec_b = prep_vec_b(it);
+  it.at_order = at_order;
   c.nrm = (float*)(base + w.nrm_off);
   c.ub = (float*)(base + w.ub_off);
   it.nrm = c.nrm;

@@ -17,7 +17,9 @@ static int nvfp4_common(const uint8_t* q, const uint8_t* scale, const float* pts
   const int cd = lora ? lora->dtype : dense_dt;
   // the pruned amax of a two-level fast merge bounds the delta by the factors' norms (prep)
   const bool fast = lora && !dense && nv_fast_ok(cd, rpad_of(lora->rank) / 16, M, N);
-  if ((rc = setup(c, M, N, lora, ws, wsb, stream, false, fast && two_level))) return rc;
+  if ((rc = setup(c, M, N, lora, ws, wsb, stream, false, fast && two_level,
+                  fast && nkc_bucket(rpad_of(lora->rank) / 16) == 1 ? AT_NV16 : AT_PLAIN)))
+    return rc;
   const bool sr = is_sr(rnd);
   BlkArgs a = blk_args_base(c, M, N, lora, rnd);
   a.q = q;

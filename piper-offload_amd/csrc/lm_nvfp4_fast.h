@@ -2,10 +2,11 @@
 // factors, N % 128 == 0, one or two scale levels, plain or 128x4-swizzled
 // block scales.  P/ = the reference's src/piper_offload/.
 //
-// Work decomposition: a 512-thread workgroup owns 16 rows (and, for single
-// tensors, a chunk of 16 macro tiles); wave w walks the 128-column macro tiles
-// w, w + 8, ... of its range, so at any time the workgroup streams 8
-// consecutive tiles (512 contiguous bytes) of each of its rows.
+// Work decomposition: a 512-thread quant workgroup owns 32 rows, two 16-row
+// groups (and, for single tensors, a chunk of 32 macro tiles); wave w walks
+// the 128-column macro tiles w, w + 8, ... of its range for both groups, so
+// at any time the workgroup streams 8 consecutive tiles (512 contiguous
+// bytes) of each of its rows.
 // (Measured on MI355X with copy kernels of the same footprint: ~5.3 TB/s for
 // NVFP4 row lengths, against ~3.7 TB/s for 128-row workgroups whose waves
 // share one tile.)  A lane holds row (lane & 15) and the 32 consecutive
@@ -50,7 +51,7 @@ struct NvArgs {
 };
 struct NvStackItem {
   NvArgs a;
-  int64_t tile_begin;    // prefix of 16-row groups (quant launches)
+  int64_t tile_begin;    // prefix of 32-row units (quant launches)
   int64_t bound_begin;   // prefix of 128-row chunks (pruned amax: bound launch)
   int64_t refine_begin;  // prefix of 512-tile chunks (pruned amax: refine launch)
 };
@@ -109,7 +110,8 @@ DEV NvLane<NKC> nv_lane(const NvArgs& a, int64_t row0, int64_t rowc, int lane) {
   l.sc_off = (uint32_t)blocked_offset(rowc, 2 * g, a.N >> 4, a.swizzled);
   l.sc_stride = a.swizzled ? 1024u : 8u;
   l.at = (const LM_GLOBAL uint8_t*)a.at;
-  l.at_off = 2u * ((uint32_t)(32 * (p >> 2) + (p & 3)) * RPAD + (uint32_t)g * (NKC * 4));
+  // rank 16: the AT_NV16 order, 16 bytes per lane and fragment pair
+  l.at_off = NKC == 1 ? 16u * (uint32_t)lane : 2u * ((uint32_t)(32 * (p >> 2) + (p & 3)) * RPAD + (uint32_t)g * (NKC * 4));
   return l;
 }
 
@@ -123,9 +125,21 @@ DEV void nv_load_codes(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
 template <int NKC>
 DEV void nv_load_aop(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
   constexpr int RPAD = NKC * 16;
-  const LM_GLOBAL uint16_t* at = (const LM_GLOBAL uint16_t*)(l.at + (l.at_off + (uint32_t)mt * (256u * RPAD)));
+  if constexpr (NKC == 1) {
+    // AT_NV16: four 16-byte loads, each 1 KiB contiguous across the wave
+    // (eight 8-byte loads, one per MFMA, kept the texture-address unit busy)
+    const LM_GLOBAL uint8_t* at = l.at + (l.at_off + (uint32_t)mt * (256u * RPAD));
 #pragma unroll
-  for (int k = 0; k < 8; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, t.aop[k]);
+    for (int kp = 0; kp < 4; ++kp) {
+      const lm_u32x4 w = *(const LM_GLOBAL lm_u32x4*)(at + 1024 * kp);
+      t.aop[2 * kp][0] = __builtin_bit_cast(v4i16, lm_u32x2{w.x, w.y});
+      t.aop[2 * kp + 1][0] = __builtin_bit_cast(v4i16, lm_u32x2{w.z, w.w});
+    }
+  } else {
+    const LM_GLOBAL uint16_t* at = (const LM_GLOBAL uint16_t*)(l.at + (l.at_off + (uint32_t)mt * (256u * RPAD)));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, t.aop[k]);
+  }
 }
 template <int NKC>
 DEV void nv_load_tile(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
@@ -324,26 +338,53 @@ DEV void nv_quant_body(const NvArgs& a, int64_t row0, int t0, int t1, const floa
     inv_g = 1.0f / gq;
     if (row0 == 0 && t0 == 0 && threadIdx.x == 0 && a.gout != nullptr) *(LM_GLOBAL float*)a.gout = gq;
   }
+  // Two 16-row groups per wave (rows row0 .. row0 + 31): each tile's A^T
+  // fragments are loaded once for both.  The quant pass was bound by the
+  // texture-address unit (TA_BUSY 0.83 of cycles, round to nearest), and
+  // the fragments were most of its address work.
+  // The second group exists when row0 + 16 < M; its lane offsets are taken
+  // from its own first row, so they are only formed (and its loads issued)
+  // when it exists: with row0 + 16 >= M the clamped row M - 1 would lie
+  // before that row and the 32-bit offset would wrap.
+  const int64_t rowB = row0 + 16 + rl;
+  const bool rokB = rowB < a.M;
+  const int64_t rowcB = rokB ? rowB : a.M - 1;
+  const bool hasB = row0 + 16 < a.M;  // wave-uniform
   const NvLane<NKC> l = nv_lane<NKC>(a, row0, rowc, lane);
+  const NvLane<NKC> lB = nv_lane<NKC>(a, hasB ? row0 + 16 : row0, hasB ? rowcB : rowc, lane);
   LM_GLOBAL uint8_t* qo = (LM_GLOBAL uint8_t*)a.q_out + row0 * (a.N >> 1);
+  LM_GLOBAL uint8_t* qoB = (LM_GLOBAL uint8_t*)a.q_out + (row0 + 16) * (a.N >> 1);
   LM_GLOBAL uint8_t* so = (LM_GLOBAL uint8_t*)a.scale_out;
-  v4i16 bop[NKC];
+  v4i16 bop[NKC], bopB[NKC];
   load_bop_g<NKC>(a.bp, row, lane, bop);
+  load_bop_g<NKC>(a.bp, rowcB, lane, bopB);  // Bp holds ceil(M/16)*16 rows
   if (t0 + wave >= ntiles) return;
   // The next tile's codes and scales (HBM) are requested before the current
   // tile is merged; its A^T fragments (L2) at the top of its own iteration.
   // Prefetching the fragments too held 16 more VGPRs (103 against 87 for
-  // round-to-nearest): 8B-shaped stack 3.72 -> 3.53 ms per step without it
-  // (round-to-nearest), 4.06 -> 3.92 (stochastic).
-  NvTileIn<NKC> cur;
+  // round-to-nearest, one row group): 8B-shaped stack 3.72 -> 3.53 ms per
+  // step without it (round-to-nearest), 4.06 -> 3.92 (stochastic).
+  NvTileIn<NKC> cur, curB;
   nv_load_codes<NKC>(l, t0 + wave, cur);
+  if (hasB) nv_load_codes<NKC>(lB, t0 + wave, curB);
   for (int mt = t0 + wave; mt < ntiles; mt += NV_NW) {
-    nv_load_aop<NKC>(l, mt, cur);
-    NvTileIn<NKC> nxt;
-    nv_load_codes<NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
+    nv_load_aop<NKC>(l, mt, cur);  // the fragments depend on the lane and tile only
+    NvTileIn<NKC> nxt, nxtB;
+    const int mn = mt + NV_NW < ntiles ? mt + NV_NW : mt;
+    nv_load_codes<NKC>(l, mn, nxt);
+    if (hasB) nv_load_codes<NKC>(lB, mn, nxtB);
     nv_quant_tile<NKC, TWO, SR>(a, cur, bop, gin, row, mt, lane, gq, inv_g, rtab, qo, so, l, rok);
+    if (hasB) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int c = 0; c < NKC; ++c) curB.aop[k][c] = cur.aop[k][c];
+      nv_quant_tile<NKC, TWO, SR>(a, curB, bopB, gin, rowB, mt, lane, gq, inv_g, rtab, qoB, so, lB, rokB);
+    }
     cur.codes = nxt.codes;
     cur.sc = nxt.sc;
+    curB.codes = nxtB.codes;
+    curB.sc = nxtB.sc;
   }
 }
 
@@ -364,14 +405,14 @@ DEV int nv_find(const NvStackItem* __restrict__ items, int count, int64_t t) {
 }
 
 // ---- kernels: single tensor (args by value) and grouped (descriptor table) ---
-// One workgroup per 16 rows (tile_begin counts 16-row groups).
-__host__ __device__ static inline int64_t nv_units(int64_t M, int64_t /*N*/) { return (M + 15) / 16; }
+// One quant workgroup per 32 rows (tile_begin counts 32-row units).
+__host__ __device__ static inline int64_t nv_units(int64_t M, int64_t /*N*/) { return (M + 31) / 32; }
 
 // Single tensors: blocks are independent once the global scale is known, so a
-// workgroup owns 16 rows x NV_CHUNK macro tiles (blockIdx.y picks the chunk).
-// 32 tiles keep 4096-column rows whole: for [14336, 4096] that measured
-// 0.0519 ms per step (RTN) against 0.0546 with chunks of 16 tiles (1792
-// workgroups instead of 896), and 0.069 with chunks of 8; stochastic
+// workgroup owns 32 rows x NV_CHUNK macro tiles (blockIdx.y picks the chunk).
+// With 16-row workgroups, 32 tiles (whole 4096-column rows) measured 0.0519
+// ms per step (RTN, [14336, 4096]) against 0.0546 with chunks of 16 tiles
+// (1792 workgroups instead of 896), and 0.069 with chunks of 8; stochastic
 // rounding 0.0612 against 0.0618.
 constexpr int NV_CHUNK = 4 * NV_NW;
 DEV int nv_chunk_end(const NvArgs& a) {
@@ -384,7 +425,7 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant(NvArgs a) {
   if (threadIdx.x < 8) rtab[threadIdx.x] = kRcpE4M3[threadIdx.x];
   __syncthreads();
   const LM_GLOBAL uint32_t* red = (const LM_GLOBAL uint32_t*)a.red;
-  nv_quant_body<NKC, TWO, SR>(a, (int64_t)blockIdx.x * 16, (int)blockIdx.y * NV_CHUNK, nv_chunk_end(a), rtab,
+  nv_quant_body<NKC, TWO, SR>(a, (int64_t)blockIdx.x * 32, (int)blockIdx.y * NV_CHUNK, nv_chunk_end(a), rtab,
                               TWO ? red[0] : 0u, TWO ? red[1] : 0u);
 }
 // TWO: every item of the launch is two-level (the host splits a mixed stack)
@@ -396,7 +437,7 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant_stack(const NvStackItem
   const int i = nv_find(items, count, blockIdx.x);
   const NvArgs& a = items[i].a;
   const LM_GLOBAL uint32_t* red = (const LM_GLOBAL uint32_t*)a.red;
-  nv_quant_body<NKC, TWO, SR>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 16, 0, (int)(a.N >> 7), rtab,
+  nv_quant_body<NKC, TWO, SR>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 32, 0, (int)(a.N >> 7), rtab,
                               TWO ? red[0] : 0u, TWO ? red[1] : 0u);
 }
 // ---- the pruned per-tensor amax (two-level) ---------------------------------

@@ -102,7 +102,7 @@ extern "C" int lm_int8_merge_stack(const lm_stack_item* items, int32_t count, in
   int slot[2] = {0, n_regular};
   // rank 16 on the fast kernels: A^T in the row kernels' tile order
   const bool r16 = fast && nkc_bucket(nkc_max) == 1;
-  for (int i = 0; i < count; ++i) preps[i].at_rows16 = r16 ? 1 : 0;
+  for (int i = 0; i < count; ++i) preps[i].at_order = r16 ? AT_ROWS16 : AT_PLAIN;
   for (int i = 0; rc == LM_OK && i < count; ++i) {
     const lm_stack_item& s = items[i];
     if (s.lora.dtype != cd) rc = fail(LM_EUNSUPPORTED, "all stack items must share one factor dtype");
@@ -274,14 +274,18 @@ extern "C" int lm_nvfp4_merge_stack(const lm_stack_item* items, int32_t count, i
   PrepItem* preps = (PrepItem*)calloc(count, sizeof(PrepItem));
   if (!preps) return fail(LM_EINVAL, "host allocation failed");
   int rc = stack_layout(items, count, workspace, workspace_bytes, preps, cursor);
-  // two-level items with bf16 factors: the factors' norms for the pruned amax
-  for (int i = 0; rc == LM_OK && i < count; ++i) preps[i].norms = items[i].aux && items[i].lora.dtype == LM_BF16 ? 1 : 0;
-  if (rc == LM_OK) rc = stack_prep(preps, count, base, st);
   bool fast = rc == LM_OK;
   for (int i = 0; fast && i < count; ++i)
     fast = nv_fast_ok(items[i].lora.dtype, preps[i].rpad / 16, items[i].M, items[i].N) &&
            nkc_bucket(preps[i].rpad / 16) == nkc_bucket(preps[0].rpad / 16) && check_nvfp4(items[i].M, items[i].N) == 0;
-  if (fast) {
+  // two-level items with bf16 factors: the factors' norms for the pruned
+  // amax; rank 16 on the fast kernels: A^T in their macro-tile order
+  for (int i = 0; rc == LM_OK && i < count; ++i) {
+    preps[i].norms = items[i].aux && items[i].lora.dtype == LM_BF16 ? 1 : 0;
+    preps[i].at_order = fast && nkc_bucket(preps[0].rpad / 16) == 1 ? AT_NV16 : AT_PLAIN;
+  }
+  if (rc == LM_OK) rc = stack_prep(preps, count, base, st);
+  if (fast && rc == LM_OK) {
     uint8_t* dev_blk = base + align256((size_t)count * sizeof(PrepItem)) + align256((size_t)count * sizeof(RowStackItem));
     rc = nv_stack_fast(items, count, swizzled, rounding_mode == LM_ROUND_STOCHASTIC, preps, dev_blk, st);
     free(preps);
