@@ -27,8 +27,13 @@ extern "C" int lm_mx_merge(uint8_t* q, uint8_t* scale, int64_t M, int64_t N, int
   if ((rc = check_lora(lora, M, N))) return rc;
   if ((rc = check_rounding(rounding))) return rc;
   Ctx c;
-  if ((rc = setup(c, M, N, lora, workspace, workspace_bytes, stream))) return rc;
-  if (mx_fast_ok(lora->dtype, c.nkc, M, N)) {
+  const int nkc = rpad_of(lora->rank) / 16;
+  const bool fast = mx_fast_ok(lora->dtype, nkc, M, N);
+  // rank 16 on the fast kernel: A^T in its macro-tile order
+  if ((rc = setup(c, M, N, lora, workspace, workspace_bytes, stream, false, false,
+                  fast && nkc_bucket(nkc) == 1 ? AT_NV16 : AT_PLAIN)))
+    return rc;
+  if (fast) {
     MxArgs ma;
     ma.q = q;
     ma.scale = scale;

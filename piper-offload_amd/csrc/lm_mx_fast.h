@@ -2,10 +2,13 @@
 // e8m0 block-32 scales, plain or 128x4-swizzled) for bf16 factors and
 // N % 128 == 0.  P/ = the reference's src/piper_offload/.
 //
-// Same decomposition as the NVFP4 kernels: a 512-thread workgroup owns 16
-// rows and a chunk of MX_CHUNK macro tiles (blockIdx.y), wave w walks the
-// 128-column macro tiles chunk + w, chunk + w + 8, ..., and a lane holds row
-// (lane & 15) and the 32 columns 32*(lane >> 4) .. +31 of a macro tile --
+// Same decomposition as the NVFP4 quant pass: a 512-thread workgroup owns 32
+// rows (two 16-row groups; 16 rows with stochastic rounding) and a chunk of
+// MX_CHUNK macro tiles (blockIdx.y), wave w walks the 128-column macro tiles
+// chunk + w, chunk + w + 8, ... for its groups, which share each tile's A^T
+// fragments (at rank 16 four 16-byte loads in the AT_NV16 order), and a
+// lane holds row (lane & 15) of
+// its group and the 32 columns 32*(lane >> 4) .. +31 of a macro tile --
 // exactly one MX block, so the block max, the shared exponent and the codes
 // never leave the lane (P/_triton_mx_lora.py:333-425 does one
 // pass: merge, block amax, scale, encode, all in place).
@@ -48,40 +51,65 @@ struct MxTileIn {
   v4i16 aop[8][NKC];
 };
 
+// A lane's addresses: wave-uniform bases plus 32-bit lane offsets (codes
+// relative to the 16-row group's first row, scales and A^T to the item).
+// Per-tile strides: codes advance 64 (fp4) / 128 (fp8) bytes per macro tile;
+// the scale column advances by 4: 4 bytes plain, one 512-byte col-block
+// swizzled.
 template <int ELEM, int NKC>
 struct MxLane {
-  uint8_t* q;
-  uint8_t* sc;
-  const uint16_t* at;
-  int64_t sc_stride;
+  LM_GLOBAL uint8_t* q;         // codes of the group's first row (in place: read and written)
+  LM_GLOBAL uint8_t* sc;        // the item's scales (in place)
+  const LM_GLOBAL uint8_t* at;  // the item's A^T (bytes)
+  uint32_t q_off, sc_off, at_off, sc_stride;
 };
 
-// per-tile strides: codes advance 64 (fp4) / 128 (fp8) bytes per macro tile;
-// the scale column advances by 4: 4 bytes plain, one 512-byte col-block swizzled
+// row0: the 16-row group's first row (wave-uniform, < M); rowc: the lane's
+// row clamped to M - 1 (>= row0)
 template <int ELEM, int NKC>
-DEV MxLane<ELEM, NKC> mx_lane(const MxArgs& a, int64_t rowc, int lane) {
+DEV MxLane<ELEM, NKC> mx_lane(const MxArgs& a, int64_t row0, int64_t rowc, int lane) {
   constexpr int RPAD = NKC * 16;
   constexpr int LB = MxTraits<ELEM>::lane_bytes;
   const int p = lane & 15, g = lane >> 4;
+  const int64_t rowbytes = ELEM == E2M1 ? (a.N >> 1) : a.N;
   MxLane<ELEM, NKC> l;
-  l.q = a.q + rowc * (ELEM == E2M1 ? (a.N >> 1) : a.N) + LB * g;
-  l.sc = a.scale + blocked_offset(rowc, g, a.N >> 5, a.swizzled);
-  l.sc_stride = a.swizzled ? 512 : 4;
-  l.at = a.at + (int64_t)(32 * (p >> 2) + (p & 3)) * RPAD + g * (NKC * 4);
+  l.q = (LM_GLOBAL uint8_t*)a.q + row0 * rowbytes;
+  l.q_off = (uint32_t)((rowc - row0) * rowbytes) + (uint32_t)(LB * g);
+  l.sc = (LM_GLOBAL uint8_t*)a.scale;
+  l.sc_off = (uint32_t)blocked_offset(rowc, g, a.N >> 5, a.swizzled);
+  l.sc_stride = a.swizzled ? 512u : 4u;
+  l.at = (const LM_GLOBAL uint8_t*)a.at;
+  l.at_off = NKC == 1 ? 16u * (uint32_t)lane : 2u * ((uint32_t)(32 * (p >> 2) + (p & 3)) * RPAD + (uint32_t)g * (NKC * 4));
   return l;
 }
 
 template <int ELEM, int NKC>
-DEV void mx_load_tile(const MxLane<ELEM, NKC>& l, int mt, MxTileIn<ELEM, NKC>& t) {
-  constexpr int RPAD = NKC * 16;
+DEV void mx_load_codes(const MxLane<ELEM, NKC>& l, int mt, MxTileIn<ELEM, NKC>& t) {
   constexpr int LB = MxTraits<ELEM>::lane_bytes;
-  const uint8_t* q = l.q + (int64_t)mt * (4 * LB);
+  const LM_GLOBAL uint8_t* q = l.q + (l.q_off + (uint32_t)mt * (4u * LB));
 #pragma unroll
-  for (int i = 0; i < LB / 16; ++i) t.codes[i] = *(const uint4*)(q + 16 * i);
-  t.sc = l.sc[(int64_t)mt * l.sc_stride];
-  const uint16_t* at = l.at + (int64_t)mt * (128 * RPAD);
+  for (int i = 0; i < LB / 16; ++i) {
+    const lm_u32x4 c = *(const LM_GLOBAL lm_u32x4*)(q + 16 * i);
+    t.codes[i] = make_uint4(c.x, c.y, c.z, c.w);
+  }
+  t.sc = l.sc[l.sc_off + (uint32_t)mt * l.sc_stride];
+}
+template <int ELEM, int NKC>
+DEV void mx_load_aop(const MxLane<ELEM, NKC>& l, int mt, MxTileIn<ELEM, NKC>& t) {
+  constexpr int RPAD = NKC * 16;
+  if constexpr (NKC == 1) {  // AT_NV16
+    const LM_GLOBAL uint8_t* at = l.at + (l.at_off + (uint32_t)mt * (256u * RPAD));
 #pragma unroll
-  for (int k = 0; k < 8; ++k) load_kchunks<NKC>(at + 4 * k * RPAD, t.aop[k]);
+    for (int kp = 0; kp < 4; ++kp) {
+      const lm_u32x4 w = *(const LM_GLOBAL lm_u32x4*)(at + 1024 * kp);
+      t.aop[2 * kp][0] = __builtin_bit_cast(v4i16, lm_u32x2{w.x, w.y});
+      t.aop[2 * kp + 1][0] = __builtin_bit_cast(v4i16, lm_u32x2{w.z, w.w});
+    }
+  } else {
+    const LM_GLOBAL uint16_t* at = (const LM_GLOBAL uint16_t*)(l.at + (l.at_off + (uint32_t)mt * (256u * RPAD)));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) load_kchunks_g<NKC>(at + 4 * k * RPAD, t.aop[k]);
+  }
 }
 
 template <int ELEM, int NKC, bool SR>
@@ -164,41 +192,78 @@ DEV void mx_tile(const MxArgs& a, const MxTileIn<ELEM, NKC>& in, const v4i16 (&b
   if (rok) so[0] = (uint8_t)enc;
 }
 
-// Chunks of 16 tiles: for MXFP4 [14336, 4096] whole 32-tile rows measured
-// 0.0398 ms per step (stochastic) against 0.0379 (round-to-nearest 0.0326
-// against 0.0330).
+// Chunks of 16 tiles: for MXFP4 [14336, 4096] with 16-row workgroups, whole
+// 32-tile rows measured 0.0398 ms per step (stochastic) against 0.0379
+// (round-to-nearest 0.0326 against 0.0330).
 constexpr int MX_CHUNK = 2 * NV_NW;
+// Rows per workgroup: round to nearest takes two 16-row groups per wave
+// (MXFP4 [14336, 4096]: 0.0325-0.0368 -> 0.028 ms per step, where the
+// A^T address work bound it); stochastic rounding keeps one, since it is
+// VALU-bound and the second group's registers cost it 2%.
+template <bool SR>
+constexpr int mx_rows_per_wg() { return SR ? 16 : 32; }
 template <int ELEM, int NKC, bool SR>
 __global__ __launch_bounds__(NV_NW * 64) void k_mx_fast(MxArgs a) {
   // (the per-lane wave index: wave_index() measured 2.7% slower here)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, rl = lane & 15;
-  const int64_t row = (int64_t)blockIdx.x * 16 + rl;
-  const bool rok = row < a.M;
-  const int64_t rowc = rok ? row : a.M - 1;  // in-bounds loads; results dropped
+  const int64_t row0 = (int64_t)blockIdx.x * mx_rows_per_wg<SR>();
+  const int64_t row = row0 + rl, rowB = row0 + 16 + rl;
+  const bool rok = row < a.M, rokB = rowB < a.M;
+  const int64_t rowc = rok ? row : a.M - 1, rowcB = rokB ? rowB : a.M - 1;  // in-bounds loads; results dropped
+  // the second group exists when row0 + 16 < M; its offsets are relative to
+  // its first row, so they are formed (and its loads issued) only then
+  const bool hasB = mx_rows_per_wg<SR>() == 32 && row0 + 16 < a.M;  // wave-uniform
   const int t0 = (int)blockIdx.y * MX_CHUNK;  // this workgroup's chunk of macro tiles
   const int ntiles = (int)((a.N >> 7) < t0 + MX_CHUNK ? (a.N >> 7) : t0 + MX_CHUNK);
-  const MxLane<ELEM, NKC> l = mx_lane<ELEM, NKC>(a, rowc, lane);
-  v4i16 bop[NKC];
+  const MxLane<ELEM, NKC> l = mx_lane<ELEM, NKC>(a, row0, rowc, lane);
+  const MxLane<ELEM, NKC> lB = mx_lane<ELEM, NKC>(a, hasB ? row0 + 16 : row0, hasB ? rowcB : rowc, lane);
+  v4i16 bop[NKC], bopB[NKC];
   load_bop<NKC>(a.bp, row, lane, bop);  // Bp holds ceil(M/16)*16 rows
+  load_bop<NKC>(a.bp, rowcB, lane, bopB);
   if (t0 + wave >= ntiles) return;
-  MxTileIn<ELEM, NKC> cur;
-  mx_load_tile<ELEM, NKC>(l, t0 + wave, cur);
+  // the next tile's codes and scales are requested before the current tile
+  // is merged; its A^T fragments at the top of its own iteration
+  MxTileIn<ELEM, NKC> cur, curB;
+  mx_load_codes<ELEM, NKC>(l, t0 + wave, cur);
+  if (hasB) mx_load_codes<ELEM, NKC>(lB, t0 + wave, curB);
+  constexpr int LB = MxTraits<ELEM>::lane_bytes;
   for (int mt = t0 + wave; mt < ntiles; mt += NV_NW) {
-    MxTileIn<ELEM, NKC> nxt;
-    mx_load_tile<ELEM, NKC>(l, mt + NV_NW < ntiles ? mt + NV_NW : mt, nxt);
+    mx_load_aop<ELEM, NKC>(l, mt, cur);
+    MxTileIn<ELEM, NKC> nxt, nxtB;
+    const int mn = mt + NV_NW < ntiles ? mt + NV_NW : mt;
+    mx_load_codes<ELEM, NKC>(l, mn, nxt);
+    if (hasB) mx_load_codes<ELEM, NKC>(lB, mn, nxtB);
     // every lane merges (the MFMAs read all lanes' operands); rows past M store nothing
-    mx_tile<ELEM, NKC, SR>(a, cur, bop, row, mt, lane, l.q, l.sc + (int64_t)mt * l.sc_stride, rok);
-    cur = nxt;
+    mx_tile<ELEM, NKC, SR>(a, cur, bop, row, mt, lane, (uint8_t*)(l.q + l.q_off),
+                           (uint8_t*)(l.sc + (l.sc_off + (uint32_t)mt * l.sc_stride)), rok);
+    if (hasB) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int c = 0; c < NKC; ++c) curB.aop[k][c] = cur.aop[k][c];
+      mx_tile<ELEM, NKC, SR>(a, curB, bopB, rowB, mt, lane, (uint8_t*)(lB.q + lB.q_off),
+                             (uint8_t*)(lB.sc + (lB.sc_off + (uint32_t)mt * lB.sc_stride)), rokB);
+    }
+#pragma unroll
+    for (int i = 0; i < LB / 16; ++i) {
+      cur.codes[i] = nxt.codes[i];
+      curB.codes[i] = nxtB.codes[i];
+    }
+    cur.sc = nxt.sc;
+    curB.sc = nxtB.sc;
   }
 }
 
-// (M N <= 2^35: the stochastic-rounding counters, offset / 8, fit 32 bits)
+// (M N <= 2^35: the stochastic-rounding counters, offset / 8, fit 32 bits;
+// M N / 32 < 2^31 and N <= 2^22: scale, A^T and 16-row code offsets fit 32 bits)
 static inline bool mx_fast_ok(int cd, int nkc, int64_t M, int64_t N) {
-  return cd == LM_BF16 && nkc > 0 && (N % 128) == 0 && M * N <= (int64_t(1) << 35);
+  return cd == LM_BF16 && nkc > 0 && (N % 128) == 0 && M * N <= (int64_t(1) << 35) && N <= (int64_t(1) << 22);
 }
 
 static int mx_fast_run(const MxArgs& a, int elem, int nkc, bool sr, hipStream_t st) {
-  const dim3 grid((unsigned)((a.M + 15) / 16), (unsigned)(((a.N >> 7) + MX_CHUNK - 1) / MX_CHUNK)), block(NV_NW * 64);
+  const int rows = sr ? mx_rows_per_wg<true>() : mx_rows_per_wg<false>();
+  const dim3 grid((unsigned)((a.M + rows - 1) / rows), (unsigned)(((a.N >> 7) + MX_CHUNK - 1) / MX_CHUNK)),
+      block(NV_NW * 64);
   TimedLaunch timed("mx", st);
 #define MXL(E_, SR_) NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_mx_fast<E_, NKC_, SR_>), grid, block, 0, st, a))
   if (elem == LM_E2M1) { if (sr) { MXL(E2M1, true); } else { MXL(E2M1, false); } }
