@@ -11,8 +11,9 @@
 // NVFP4 row lengths, against ~3.7 TB/s for 128-row workgroups whose waves
 // share one tile.)  A lane holds row (lane & 15) and the 32 consecutive
 // columns 32*(lane >> 4) .. +31 of a macro tile: two NVFP4 blocks, i.e. one
-// 16-byte code load and one 2-byte scale load, so block reductions never
-// leave the lane.  The delta of a macro tile is 8 x NKC
+// 16-byte code load and one 2-byte scale read (from LDS where a stack's
+// scales are staged there, below), so block reductions never leave the
+// lane.  The delta of a macro tile is 8 x NKC
 // v_mfma_f32_16x16x16_bf16 (tile_delta's SPAN = 32 orientation), with the
 // A^T fragments read through per-lane pointers.
 //
@@ -95,7 +96,20 @@ struct NvLane {
   const LM_GLOBAL uint8_t* sc;  // the item's scales
   const LM_GLOBAL uint8_t* at;  // the item's A^T (bytes)
   uint32_t q_off, sc_off, at_off, sc_stride;
+  uint32_t lsc_off;             // the lane's scale pair in the staged block (tile t0)
 };
+
+// Block scales staged in LDS (stacks in the plain layout whose rows have at
+// most NV_LSC_TILES macro tiles): the quant workgroup reads its 32 rows'
+// scale bytes of tiles [t0, t1) with 8-byte loads that cover whole lines,
+// each lane reads and writes its 2 bytes per tile in LDS, and the workgroup
+// writes the block back after its last tile.  Per tile and row group that
+// takes the 2-byte scale load and store off the texture-address unit, which
+// bounds round-to-nearest, and the partial-line scale traffic off HBM.  A
+// row's bytes sit NV_LSC_STRIDE apart: 8 * 129, so the 16 rows a load reads
+// fall in distinct banks.
+constexpr int NV_LSC_TILES = 128;
+constexpr int NV_LSC_STRIDE = 8 * (NV_LSC_TILES + 1);
 
 // row0: the 16-row group's first row (wave-uniform); rowc: the lane's row,
 // clamped to M - 1
@@ -112,15 +126,17 @@ DEV NvLane<NKC> nv_lane(const NvArgs& a, int64_t row0, int64_t rowc, int lane) {
   l.at = (const LM_GLOBAL uint8_t*)a.at;
   // rank 16: the AT_NV16 order, 16 bytes per lane and fragment pair
   l.at_off = NKC == 1 ? 16u * (uint32_t)lane : 2u * ((uint32_t)(32 * (p >> 2) + (p & 3)) * RPAD + (uint32_t)g * (NKC * 4));
+  l.lsc_off = 0u;
   return l;
 }
 
-template <int NKC>
-DEV void nv_load_codes(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
+template <int NKC, bool LSC = false>
+DEV void nv_load_codes(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t, const uint8_t* lsc = nullptr, int t0 = 0) {
   const lm_u32x4 c = *(const LM_GLOBAL lm_u32x4*)(l.q + (l.q_off + (uint32_t)mt * 64u));
   t.codes = make_uint4(c.x, c.y, c.z, c.w);
   // the lane's scale column is even: both blocks' scales are adjacent bytes
-  t.sc = *(const LM_GLOBAL uint16_t*)(l.sc + (l.sc_off + (uint32_t)mt * l.sc_stride));
+  if constexpr (LSC) t.sc = *(const uint16_t*)(lsc + (l.lsc_off + 8u * (uint32_t)(mt - t0)));
+  else t.sc = *(const LM_GLOBAL uint16_t*)(l.sc + (l.sc_off + (uint32_t)mt * l.sc_stride));
 }
 template <int NKC>
 DEV void nv_load_aop(const NvLane<NKC>& l, int mt, NvTileIn<NKC>& t) {
@@ -291,10 +307,10 @@ DEV void nv_quant_block(const NvArgs& a, int64_t row, int mt, int lane, float gq
 // its operands from all 64 lanes whatever the exec mask, so the operand
 // loads must not be skipped for the rows past M (a load under a lane
 // condition leaves those lanes' registers stale).
-template <int NKC, bool TWO, bool SR>
+template <int NKC, bool TWO, bool SR, bool LSC = false>
 DEV void nv_quant_tile(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&bop)[NKC], float gin, int64_t row,
                        int mt, int lane, float gq, float inv_g, const float* rtab, LM_GLOBAL uint8_t* qo,
-                       LM_GLOBAL uint8_t* so, const NvLane<NKC>& l, bool rok) {
+                       LM_GLOBAL uint8_t* so, const NvLane<NKC>& l, bool rok, uint8_t* lsc = nullptr, int t0 = 0) {
   uint32_t words[4];
   uint32_t scb = 0;
   {
@@ -307,9 +323,39 @@ DEV void nv_quant_tile(const NvArgs& a, const NvTileIn<NKC>& in, const v4i16 (&b
     nv_merged_block<NKC, TWO, 1>(in, bop, a.strength, gin, m);
     nv_quant_block<TWO, SR, 1>(a, row, mt, lane, gq, inv_g, rtab, m, words, scb);
   }
+  // (the staged slot was read for this tile only, by this lane; rows past M
+  // are not written back)
+  if constexpr (LSC) *(uint16_t*)(lsc + (l.lsc_off + 8u * (uint32_t)(mt - t0))) = (uint16_t)scb;
   if (rok) {
     *(LM_GLOBAL lm_u32x4*)(qo + (l.q_off + (uint32_t)mt * 64u)) = lm_u32x4{words[0], words[1], words[2], words[3]};
-    *(LM_GLOBAL uint16_t*)(so + (l.sc_off + (uint32_t)mt * l.sc_stride)) = (uint16_t)scb;
+    if constexpr (!LSC) *(LM_GLOBAL uint16_t*)(so + (l.sc_off + (uint32_t)mt * l.sc_stride)) = (uint16_t)scb;
+  }
+}
+
+// the staged block: rows row0 .. row0 + 31 (rows past M repeat row M - 1),
+// tiles [t0, t1), 8 bytes each; wave w moves rows w, w + 8, ...
+DEV void nv_lsc_load(const NvArgs& a, int64_t row0, int t0, int t1, uint8_t* lsc) {
+  const int lane = threadIdx.x & 63, wave = wave_index();
+  const LM_GLOBAL uint8_t* sb = (const LM_GLOBAL uint8_t*)a.scale + 8 * t0;
+  const int64_t scols = a.N >> 4;
+#pragma unroll
+  for (int i = 0; i < 32 / NV_NW; ++i) {
+    const int r = wave + NV_NW * i;
+    const int64_t rr = row0 + r < a.M ? row0 + r : a.M - 1;
+    for (int c = lane; c < t1 - t0; c += 64)
+      *(lm_u32x2*)(lsc + r * NV_LSC_STRIDE + 8 * c) = *(const LM_GLOBAL lm_u32x2*)(sb + (rr * scols + 8 * c));
+  }
+}
+DEV void nv_lsc_store(const NvArgs& a, int64_t row0, int t0, int t1, const uint8_t* lsc) {
+  const int lane = threadIdx.x & 63, wave = wave_index();
+  LM_GLOBAL uint8_t* sb = (LM_GLOBAL uint8_t*)a.scale_out + 8 * t0;
+  const int64_t scols = a.N >> 4;
+#pragma unroll
+  for (int i = 0; i < 32 / NV_NW; ++i) {
+    const int r = wave + NV_NW * i;
+    if (row0 + r >= a.M) break;  // wave-uniform
+    for (int c = lane; c < t1 - t0; c += 64)
+      *(LM_GLOBAL lm_u32x2*)(sb + ((row0 + r) * scols + 8 * c)) = *(const lm_u32x2*)(lsc + r * NV_LSC_STRIDE + 8 * c);
   }
 }
 
@@ -321,9 +367,14 @@ DEV void nv_keep_gin(uint32_t* red, float gin) { ((LM_GLOBAL uint32_t*)red)[1] =
 
 // amax_bits, gin_bits: red[0] and red[1] as the amax pass left them (the
 // max |merged| and the copy of the input per-tensor scale); two-level only
-template <int NKC, bool TWO, bool SR>
+template <int NKC, bool TWO, bool SR, bool LSC = false>
 DEV void nv_quant_body(const NvArgs& a, int64_t row0, int t0, int t1, const float* rtab, uint32_t amax_bits,
                        uint32_t gin_bits) {
+  __shared__ __attribute__((aligned(16))) uint8_t lsc[LSC ? 32 * NV_LSC_STRIDE : 16];
+  if constexpr (LSC) {
+    nv_lsc_load(a, row0, t0, t1, lsc);
+    __syncthreads();
+  }
   const int lane = threadIdx.x & 63, wave = wave_index(), rl = lane & 15;
   const int64_t row = row0 + rl;
   const bool rok = row < a.M;
@@ -350,41 +401,50 @@ DEV void nv_quant_body(const NvArgs& a, int64_t row0, int t0, int t1, const floa
   const bool rokB = rowB < a.M;
   const int64_t rowcB = rokB ? rowB : a.M - 1;
   const bool hasB = row0 + 16 < a.M;  // wave-uniform
-  const NvLane<NKC> l = nv_lane<NKC>(a, row0, rowc, lane);
-  const NvLane<NKC> lB = nv_lane<NKC>(a, hasB ? row0 + 16 : row0, hasB ? rowcB : rowc, lane);
+  NvLane<NKC> l = nv_lane<NKC>(a, row0, rowc, lane);
+  NvLane<NKC> lB = nv_lane<NKC>(a, hasB ? row0 + 16 : row0, hasB ? rowcB : rowc, lane);
+  l.lsc_off = (uint32_t)(rl * NV_LSC_STRIDE + 2 * (lane >> 4));
+  lB.lsc_off = l.lsc_off + 16u * NV_LSC_STRIDE;
   LM_GLOBAL uint8_t* qo = (LM_GLOBAL uint8_t*)a.q_out + row0 * (a.N >> 1);
   LM_GLOBAL uint8_t* qoB = (LM_GLOBAL uint8_t*)a.q_out + (row0 + 16) * (a.N >> 1);
   LM_GLOBAL uint8_t* so = (LM_GLOBAL uint8_t*)a.scale_out;
   v4i16 bop[NKC], bopB[NKC];
   load_bop_g<NKC>(a.bp, row, lane, bop);
   load_bop_g<NKC>(a.bp, rowcB, lane, bopB);  // Bp holds ceil(M/16)*16 rows
-  if (t0 + wave >= ntiles) return;
-  // The next tile's codes and scales (HBM) are requested before the current
-  // tile is merged; its A^T fragments (L2) at the top of its own iteration.
-  // Prefetching the fragments too held 16 more VGPRs (103 against 87 for
-  // round-to-nearest, one row group): 8B-shaped stack 3.72 -> 3.53 ms per
-  // step without it (round-to-nearest), 4.06 -> 3.92 (stochastic).
-  NvTileIn<NKC> cur, curB;
-  nv_load_codes<NKC>(l, t0 + wave, cur);
-  if (hasB) nv_load_codes<NKC>(lB, t0 + wave, curB);
-  for (int mt = t0 + wave; mt < ntiles; mt += NV_NW) {
-    nv_load_aop<NKC>(l, mt, cur);  // the fragments depend on the lane and tile only
-    NvTileIn<NKC> nxt, nxtB;
-    const int mn = mt + NV_NW < ntiles ? mt + NV_NW : mt;
-    nv_load_codes<NKC>(l, mn, nxt);
-    if (hasB) nv_load_codes<NKC>(lB, mn, nxtB);
-    nv_quant_tile<NKC, TWO, SR>(a, cur, bop, gin, row, mt, lane, gq, inv_g, rtab, qo, so, l, rok);
-    if (hasB) {
+  // (with LSC every wave reaches the write-back barrier, tiles or not)
+  if (t0 + wave < ntiles) {
+    // The next tile's codes and scales (HBM) are requested before the current
+    // tile is merged; its A^T fragments (L2) at the top of its own iteration.
+    // Prefetching the fragments too held 16 more VGPRs (103 against 87 for
+    // round-to-nearest, one row group): 8B-shaped stack 3.72 -> 3.53 ms per
+    // step without it (round-to-nearest), 4.06 -> 3.92 (stochastic).
+    NvTileIn<NKC> cur, curB;
+    nv_load_codes<NKC, LSC>(l, t0 + wave, cur, lsc, t0);
+    if (hasB) nv_load_codes<NKC, LSC>(lB, t0 + wave, curB, lsc, t0);
+    for (int mt = t0 + wave; mt < ntiles; mt += NV_NW) {
+      nv_load_aop<NKC>(l, mt, cur);  // the fragments depend on the lane and tile only
+      NvTileIn<NKC> nxt, nxtB;
+      const int mn = mt + NV_NW < ntiles ? mt + NV_NW : mt;
+      nv_load_codes<NKC, LSC>(l, mn, nxt, lsc, t0);
+      if (hasB) nv_load_codes<NKC, LSC>(lB, mn, nxtB, lsc, t0);
+      nv_quant_tile<NKC, TWO, SR, LSC>(a, cur, bop, gin, row, mt, lane, gq, inv_g, rtab, qo, so, l, rok, lsc, t0);
+      if (hasB) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
+        for (int k = 0; k < 8; ++k)
 #pragma unroll
-        for (int c = 0; c < NKC; ++c) curB.aop[k][c] = cur.aop[k][c];
-      nv_quant_tile<NKC, TWO, SR>(a, curB, bopB, gin, rowB, mt, lane, gq, inv_g, rtab, qoB, so, lB, rokB);
+          for (int c = 0; c < NKC; ++c) curB.aop[k][c] = cur.aop[k][c];
+        nv_quant_tile<NKC, TWO, SR, LSC>(a, curB, bopB, gin, rowB, mt, lane, gq, inv_g, rtab, qoB, so, lB, rokB, lsc,
+                                         t0);
+      }
+      cur.codes = nxt.codes;
+      cur.sc = nxt.sc;
+      curB.codes = nxtB.codes;
+      curB.sc = nxtB.sc;
     }
-    cur.codes = nxt.codes;
-    cur.sc = nxt.sc;
-    curB.codes = nxtB.codes;
-    curB.sc = nxtB.sc;
+  }
+  if constexpr (LSC) {
+    __syncthreads();
+    nv_lsc_store(a, row0, t0, t1, lsc);
   }
 }
 
@@ -419,6 +479,8 @@ DEV int nv_chunk_end(const NvArgs& a) {
   const int t1 = ((int)blockIdx.y + 1) * NV_CHUNK, nt = (int)(a.N >> 7);
   return t1 < nt ? t1 : nt;
 }
+// (single tensors read the scales from global memory: with 4 tiles per wave
+// the staging measured slower, [14336, 4096] stochastic 0.0503 -> 0.0515 ms)
 template <int NKC, bool SR, bool TWO>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant(NvArgs a) {
   __shared__ float rtab[8];
@@ -428,17 +490,19 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant(NvArgs a) {
   nv_quant_body<NKC, TWO, SR>(a, (int64_t)blockIdx.x * 32, (int)blockIdx.y * NV_CHUNK, nv_chunk_end(a), rtab,
                               TWO ? red[0] : 0u, TWO ? red[1] : 0u);
 }
-// TWO: every item of the launch is two-level (the host splits a mixed stack)
-template <int NKC, bool SR, bool TWO>
+// TWO: every item of the launch is two-level (the host splits a mixed stack);
+// LSC: block scales staged in LDS, every item's rows have at most
+// NV_LSC_TILES macro tiles (the staging's barrier also covers rtab)
+template <int NKC, bool SR, bool TWO, bool LSC>
 __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant_stack(const NvStackItem* __restrict__ items, int count) {
   __shared__ float rtab[8];
   if (threadIdx.x < 8) rtab[threadIdx.x] = kRcpE4M3[threadIdx.x];
-  __syncthreads();
+  if constexpr (!LSC) __syncthreads();
   const int i = nv_find(items, count, blockIdx.x);
   const NvArgs& a = items[i].a;
   const LM_GLOBAL uint32_t* red = (const LM_GLOBAL uint32_t*)a.red;
-  nv_quant_body<NKC, TWO, SR>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 32, 0, (int)(a.N >> 7), rtab,
-                              TWO ? red[0] : 0u, TWO ? red[1] : 0u);
+  nv_quant_body<NKC, TWO, SR, LSC>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 32, 0, (int)(a.N >> 7), rtab,
+                                   TWO ? red[0] : 0u, TWO ? red[1] : 0u);
 }
 // ---- the pruned per-tensor amax (two-level) ---------------------------------
 // max |merged| over a tensor without merging every element.  For element

@@ -225,6 +225,9 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
   const int nkc = preps[0].rpad / 16;
   const dim3 block(NV_NW * 64);
   const NvStackItem* d = (const NvStackItem*)dev_items;
+  // block scales staged in LDS: plain layout, rows of at most NV_LSC_TILES macro tiles
+  bool lsc = !swizzled;
+  for (int i = 0; i < count; ++i) lsc = lsc && (items[i].N >> 7) <= NV_LSC_TILES;
   if (rc == LM_OK && n_two > 0) {
     TimedLaunch timed("nvfp4", st);
     NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_bound_stack<NKC_>), dim3((unsigned)bounds), block, 0, st, d,
@@ -236,20 +239,22 @@ static int nv_stack_fast(const lm_stack_item* items, int32_t count, int32_t swiz
   }
   if (rc == LM_OK && n_two > 0) {
     TimedLaunch timed("nvfp4", st);
-#define NQ2(SR_)                                                                                                      \
-  NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, SR_, true>), dim3((unsigned)tiles[0]), block, 0, \
-                                                 st, d, n_two))
-    if (sr) { NQ2(true); } else { NQ2(false); }
+#define NQ2(SR_, LSC_)                                                                                     \
+  NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, SR_, true, LSC_>), dim3((unsigned)tiles[0]), \
+                                                 block, 0, st, d, n_two))
+    if (lsc) { if (sr) { NQ2(true, true); } else { NQ2(false, true); } }
+    else { if (sr) { NQ2(true, false); } else { NQ2(false, false); } }
 #undef NQ2
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 quant launch: %s", hipGetErrorString(e));
   }
   if (rc == LM_OK && tiles[1] > 0) {
     TimedLaunch timed("nvfp4", st);
-#define NQ(SR_)                                                                                                 \
-  NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, SR_, false>), dim3((unsigned)tiles[1]), block, \
-                                                 0, st, d + n_two, count - n_two))
-    if (sr) { NQ(true); } else { NQ(false); }
+#define NQ(SR_, LSC_)                                                                                       \
+  NKC_SWITCH(nkc_bucket(nkc), hipLaunchKernelGGL((k_nv_quant_stack<NKC_, SR_, false, LSC_>), dim3((unsigned)tiles[1]), \
+                                                 block, 0, st, d + n_two, count - n_two))
+    if (lsc) { if (sr) { NQ(true, true); } else { NQ(false, true); } }
+    else { if (sr) { NQ(true, false); } else { NQ(false, false); } }
 #undef NQ
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) rc = fail(LM_EHIP, "nvfp4 quant launch: %s", hipGetErrorString(e));
