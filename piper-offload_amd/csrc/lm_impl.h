@@ -954,9 +954,10 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
 }
 
 // Rank 16 with the 8-tile cache fits 128 VGPRs: two 512-thread workgroups per
-// CU (4 waves per SIMD), which the bound below holds the compiler to.
+// CU (4 waves per SIMD), which the bound below holds the compiler to (and the
+// 16-wave kernel's 10-tile cache to 128 VGPRs as well).
 template <int NKC, int CACHE>
-constexpr int fast_min_waves() { return (NKC == 1 && CACHE <= 8) || (NKC == 2 && CACHE <= 4) ? 4 : 1; }
+constexpr int fast_min_waves() { return (NKC == 1 && CACHE <= 10) || (NKC == 2 && CACHE <= 4) ? 4 : 1; }
 
 template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0,
           bool SBF = false>
@@ -1805,8 +1806,14 @@ template <int NKC>
 constexpr int row_lds_cache() { return NKC == 2 ? 4 : 0; }
 static constexpr int ROW_DEEP_CACHE = 16;
 static constexpr int ROW_NW_WIDE = 16;
-// 16-wave rows keep 4 more tiles per wave in LDS (128 KiB per workgroup, one
-// workgroup per CU)
+// 16-wave rows keep 10 tiles per wave in registers and 4 more in LDS (128 KiB
+// per workgroup, one workgroup per CU), so a 14336-column row (224 tiles) is
+// merged once; the A^T operands run 2 tiles ahead instead of 4 to make room
+// (128 VGPRs, a few spilled).  The 32 down_proj of the 8B stack, against 8
+// register tiles and 4 ahead (2 of 14 tiles merged twice): SR 1.298 -> 1.268
+// ms, RTN 1.140 -> 1.074 ms.
+static constexpr int ROW_WIDE_CACHE = 10;
+static constexpr int ROW_WIDE_PF = 2;
 static constexpr int ROW_WIDE_LDS = 4;
 enum RowsMode : int { ROWS_REGULAR = 0, ROWS_WIDE = 1, ROWS_DEEP = 2 };
 static inline int rows_long_mode(int nkc, bool sr, int64_t N) {
@@ -1823,7 +1830,7 @@ static int launch_rows_fast(const RowArgs& a, hipStream_t st) {
   const int mode = rows_long_mode(NKC, SR, a.N);
   if (mode == ROWS_WIDE) {
     if constexpr (NKC == 1)
-      hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<NKC, SR>(), ROW_WIDE_LDS, SBF>),
+      hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW_WIDE, ROW_WIDE_CACHE, ROW_WIDE_PF, ROW_WIDE_LDS, SBF>),
                          grid, dim3(ROW_NW_WIDE * 64), 0, st, a);
   } else if (mode == ROWS_DEEP) {
     if constexpr (NKC == 4 || !SR)

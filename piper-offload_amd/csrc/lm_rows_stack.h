@@ -32,11 +32,11 @@ static int int8_stack_fast_launch(const RowStackItem* d0, const int32_t* begins,
     if (nkc_bucket(nkc_max) == 1) {  // ROWS_WIDE: 16-wave workgroups
       const dim3 wblock(ROW_NW_WIDE * 64);
       if (sr)
-        hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, true, 1, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<1, true>(),
+        hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, true, 1, ROW_NW_WIDE, ROW_WIDE_CACHE, ROW_WIDE_PF,
                                               ROW_WIDE_LDS, true, SBF>),
                            grid, wblock, 0, st, d1, begins + n_regular, n_deep);
       else
-        hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, false, 1, ROW_NW_WIDE, ROW_CACHE, fast_prefetch<1, false>(),
+        hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, false, 1, ROW_NW_WIDE, ROW_WIDE_CACHE, ROW_WIDE_PF,
                                               ROW_WIDE_LDS, true, SBF>),
                            grid, wblock, 0, st, d1, begins + n_regular, n_deep);
     } else {  // ROWS_DEEP
