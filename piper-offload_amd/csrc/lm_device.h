@@ -522,6 +522,16 @@ DEV uint32_t sr_fp8(float v, uint32_t h, float /*limit*/) { return cvt_sr_fp8<FM
 // threadIdx.x alone the compiler treats it as per-lane, and every address
 // derived from it (tile offsets) then costs 64-bit VALU adds per tile
 DEV int wave_index() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+// The dispatcher places workgroup b of a launch on XCD b % 8.  xcd_unit maps
+// it to a unit index so that each XCD takes one contiguous eighth of the n
+// units, and operands that neighbouring units share (a grouped item's A^T)
+// stay in that XCD's L2 instead of being fetched into all eight.  It is a
+// bijection on [0, n) whatever the placement: XCD x's workgroups b = 8 k + x
+// get units x q + min(x, r) + k, q = n / 8, r = n % 8.
+DEV int64_t xcd_unit(int64_t b, int64_t n) {
+  const int64_t q = n >> 3, r = n & 7, x = b & 7, k = b >> 3;
+  return x * q + (x < r ? x : r) + k;
+}
 
 // max(acc, |a|, |b|) in one v_max3_f32 (IEEE maxNum: a NaN operand is
 // ignored, as fmaxf does).  Written as asm because the builtin form makes the

@@ -993,7 +993,7 @@ template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch
 __global__ __launch_bounds__(NW * 64, (fast_min_waves<NKC, CACHE>())) void k_rows_fast_stack(const RowStackItem* __restrict__ items,
                                                                                              const int32_t* __restrict__ begins,
                                                                                              int count) {
-  const int32_t t = (int32_t)blockIdx.x;
+  const int32_t t = (int32_t)xcd_unit(blockIdx.x, gridDim.x);
   const int it = __builtin_amdgcn_readfirstlane(stack_item_of(begins, count, t));
   const RowArgs a = items[it].a;
   rows_fast_body<KIND, SR, NKC, NW, CACHE, PF_, LCACHE, R16, SBF>(a, (int64_t)(t - begins[it]) * 16);

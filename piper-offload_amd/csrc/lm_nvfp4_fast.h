@@ -498,10 +498,11 @@ __global__ __launch_bounds__(NV_NW * 64) void k_nv_quant_stack(const NvStackItem
   __shared__ float rtab[8];
   if (threadIdx.x < 8) rtab[threadIdx.x] = kRcpE4M3[threadIdx.x];
   if constexpr (!LSC) __syncthreads();
-  const int i = nv_find(items, count, blockIdx.x);
+  const int64_t t = xcd_unit(blockIdx.x, gridDim.x);
+  const int i = nv_find(items, count, t);
   const NvArgs& a = items[i].a;
   const LM_GLOBAL uint32_t* red = (const LM_GLOBAL uint32_t*)a.red;
-  nv_quant_body<NKC, TWO, SR, LSC>(a, ((int64_t)blockIdx.x - items[i].tile_begin) * 32, 0, (int)(a.N >> 7), rtab,
+  nv_quant_body<NKC, TWO, SR, LSC>(a, (t - items[i].tile_begin) * 32, 0, (int)(a.N >> 7), rtab,
                                    TWO ? red[0] : 0u, TWO ? red[1] : 0u);
 }
 // ---- the pruned per-tensor amax (two-level) ---------------------------------
