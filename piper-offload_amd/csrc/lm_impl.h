@@ -721,15 +721,25 @@ __device__ __forceinline__ void fast_tile_delta(const v4i16 (&aop)[4][NKC], cons
 // merged values of one tile before their bf16 rounding into m[16], given the
 // codes and deltas; with AMAX, amax = max(amax, |m|) (the maximum of the
 // bf16-rounded values is bf16r of it)
-template <int KIND, bool AMAX = true>
+// LUT: INT8 only, lut = the lane's row of bf16(RN(q s)) for the 256 code
+// bytes (rows_fast_body), read instead of converting and scaling each code
+template <int KIND, bool AMAX = true, bool LUT = false>
 __device__ __forceinline__ void fast_merge_vals(const RowArgs& a, const uint4& raw, const float (&d)[16], float s_in,
-                                                float (&m)[16], float& amax) {
+                                                float (&m)[16], float& amax, const float* lut = nullptr) {
+  static_assert(!LUT || KIND == K_INT8, "the dequant table is for INT8 codes");
   const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const uint32_t word = w[k >> 1];
     float x0, x1;
-    if constexpr (KIND == K_INT8) {
+    if constexpr (LUT) {
+      const int b0 = (2 * k) & 3, b1 = (2 * k + 1) & 3;
+      const float base0 = lut[(word >> (8 * b0)) & 0xffu], base1 = lut[(word >> (8 * b1)) & 0xffu];
+      m[2 * k] = __builtin_fmaf(d[2 * k], a.strength, base0);
+      m[2 * k + 1] = __builtin_fmaf(d[2 * k + 1], a.strength, base1);
+      if constexpr (AMAX) amax = max3_abs(amax, m[2 * k], m[2 * k + 1]);
+      continue;
+    } else if constexpr (KIND == K_INT8) {
       // signed byte -> fp32 is one sign-extending SDWA convert; RN(q * s)
       const int b0 = (2 * k) & 3, b1 = (2 * k + 1) & 3;
       x0 = (float)(int8_t)(word >> (8 * b0)) * s_in;
@@ -745,20 +755,21 @@ __device__ __forceinline__ void fast_merge_vals(const RowArgs& a, const uint4& r
     if constexpr (AMAX) amax = max3_abs(amax, m[2 * k], m[2 * k + 1]);
   }
 }
-template <int KIND, int NKC, bool AMAX = true>
+template <int KIND, int NKC, bool AMAX = true, bool LUT = false>
 __device__ __forceinline__ void fast_merged_f32(const RowArgs& a, const uint4& raw, const v4i16 (&aop)[4][NKC],
-                                                const v4i16 (&bop)[NKC], float s_in, float (&m)[16], float& amax) {
+                                                const v4i16 (&bop)[NKC], float s_in, float (&m)[16], float& amax,
+                                                const float* lut = nullptr) {
   float d[16];
   fast_tile_delta<NKC>(aop, bop, d);
-  fast_merge_vals<KIND, AMAX>(a, raw, d, s_in, m, amax);
+  fast_merge_vals<KIND, AMAX, LUT>(a, raw, d, s_in, m, amax, lut);
 }
 // merged bf16 pairs of one tile into out[8]; amax = max(amax, |merged|) in fp32
-template <int KIND, int NKC>
+template <int KIND, int NKC, bool LUT = false>
 __device__ __forceinline__ void fast_merged_tile(const RowArgs& a, const uint4& raw, const v4i16 (&aop)[4][NKC],
                                                  const v4i16 (&bop)[NKC], float s_in,
-                                                 uint32_t (&out)[8], float& amax) {
+                                                 uint32_t (&out)[8], float& amax, const float* lut = nullptr) {
   float m[16];
-  fast_merged_f32<KIND, NKC>(a, raw, aop, bop, s_in, m, amax);
+  fast_merged_f32<KIND, NKC, true, LUT>(a, raw, aop, bop, s_in, m, amax, lut);
 #pragma unroll
   for (int k = 0; k < 8; ++k) out[k] = pack_bf16x2(m[2 * k], m[2 * k + 1]);
 }
@@ -856,20 +867,57 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
                      : SBF ? bf16_val(((const LM_GLOBAL uint16_t*)a.scale)[row]) : ((const LM_GLOBAL float*)a.scale)[row];
   uint32_t cache[CACHE][8];
   float amax = 0.0f;
-  if (wave + (CACHE - 1) * NW < ntiles) {
-    // every cache slot holds a tile: branch-free.  The codes of all CACHE
-    // tiles (4 VGPRs each) are requested at once, so a wave keeps CACHE KiB of
-    // HBM reads in flight; the A^T operands (L2-resident, 4 NKC VGPRs per MFMA)
-    // run PF tiles ahead.
-    uint4 raw[CACHE];
-    v4i16 aop[PF][4][NKC];
+  // INT8 without an LDS tile cache: the dequantized base bf16(RN(q s)) comes
+  // from a per-row table of the 256 code bytes in LDS (16 KiB), two address
+  // instructions per element instead of the sign-extending convert, the
+  // product and the bf16 rounding; the values are the same.  8B stack
+  // (bench.py, bit-identical): RTN 3.79 -> 3.43 ms per step, SR 4.14 ->
+  // 4.06 ms.  (Kernels with an LDS tile cache keep the arithmetic: the table
+  // would cost them a workgroup per CU, or registers.)
+  constexpr bool LUT = KIND == K_INT8 && LCACHE == 0;
+  static_assert(!LUT || NW == 8, "the table build assigns 32 threads to each of the 16 rows");
+  // rows 260 floats apart: lanes of different rows reading the same code byte
+  // fall in different banks
+  constexpr int LSTRIDE = 260;
+  __shared__ __attribute__((aligned(16))) float lut[LUT ? 16 * LSTRIDE : 1];
+  const float* lrow = lut + (LUT ? rl * LSTRIDE : 0);
+  const bool bfree = wave + (CACHE - 1) * NW < ntiles;  // wave-uniform
+  uint4 raw[CACHE];
+  if (bfree) {
+    // every cache slot holds a tile: the codes of all CACHE tiles (4 VGPRs
+    // each) are requested at once, before the table is built, so a wave
+    // keeps CACHE KiB of HBM reads in flight
 #pragma unroll
     for (int i = 0; i < CACHE; ++i) raw[i] = fast_load_codes(L, wave + i * NW);
+  }
+  if constexpr (LUT) {
+    // thread t fills row t / 32 for the codes q = 4 (t % 32) .. + 3 and -q
+    // (RN and the bf16 rounding are odd functions, so the entry of -q is the
+    // negated entry of q); the row's first thread also fills -128
+    const int r = (int)(threadIdx.x >> 5), q0 = 4 * (int)(threadIdx.x & 31);
+    const float s = row0 + r >= a.M ? 0.0f  // (rows past M: s_in is 0 as well)
+                    : SBF ? bf16_val(((const LM_GLOBAL uint16_t*)a.scale)[row0 + r])
+                          : ((const LM_GLOBAL float*)a.scale)[row0 + r];
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = bf16r((float)(q0 + j) * s);
+    float* lr = lut + r * LSTRIDE;
+    *(float4*)(lr + q0) = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (q0 + j > 0) lr[256 - q0 - j] = -v[j];
+    if (q0 == 0) lr[128] = bf16r(-128.0f * s);
+    __syncthreads();
+  }
+  if (bfree) {
+    // branch-free; the A^T operands (L2-resident, 4 NKC VGPRs per MFMA) run
+    // PF tiles ahead
+    v4i16 aop[PF][4][NKC];
 #pragma unroll
     for (int i = 0; i < PF; ++i) fast_load_aop<NKC, R16>(L, wave + i * NW, aop[i]);
 #pragma unroll
     for (int i = 0; i < CACHE; ++i) {
-      fast_merged_tile<KIND, NKC>(a, raw[i], aop[i % PF], bop, s_in, cache[i], amax);
+      fast_merged_tile<KIND, NKC, LUT>(a, raw[i], aop[i % PF], bop, s_in, cache[i], amax, lrow);
       if (i + PF < CACHE) fast_load_aop<NKC, R16>(L, wave + (i + PF) * NW, aop[i % PF]);
     }
   } else {
@@ -879,7 +927,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
       if (mt < ntiles) {
         FastTileIn<NKC> in;
         fast_load_tile<NKC, R16>(L, mt, in);
-        fast_merged_tile<KIND, NKC>(a, in.raw, in.aop, bop, s_in, cache[i], amax);
+        fast_merged_tile<KIND, NKC, LUT>(a, in.raw, in.aop, bop, s_in, cache[i], amax, lrow);
       }
     }
   }
@@ -894,7 +942,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
       FastTileIn<NKC> nxt;
       fast_load_tile<NKC, R16>(L, mt + NW < ntiles ? mt + NW : mt, nxt);
       uint32_t t[8];
-      fast_merged_tile<KIND, NKC>(a, cur.raw, cur.aop, bop, s_in, t, amax);
+      fast_merged_tile<KIND, NKC, LUT>(a, cur.raw, cur.aop, bop, s_in, t, amax, lrow);
       if (LCACHE > 0 && l < LCACHE) {
         lcache[l][wave][0][lane] = lm_u32x4{t[0], t[1], t[2], t[3]};
         lcache[l][wave][1][lane] = lm_u32x4{t[4], t[5], t[6], t[7]};
@@ -946,7 +994,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
       fast_load_tile<NKC, R16>(L, mt + NW < ntiles ? mt + NW : mt, nxt);
       uint32_t t[8];
       float unused = 0.0f;
-      fast_merged_tile<KIND, NKC>(a, cur.raw, cur.aop, bop, s_in, t, unused);
+      fast_merged_tile<KIND, NKC, LUT>(a, cur.raw, cur.aop, bop, s_in, t, unused, lrow);
       fast_quant_store<KIND, SR, SBF>(a, L, rok, mt, qp, t);
       cur = nxt;
     }
