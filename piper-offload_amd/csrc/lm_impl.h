@@ -872,9 +872,9 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
   // instructions per element instead of the sign-extending convert, the
   // product and the bf16 rounding; the values are the same.  8B stack
   // (bench.py, bit-identical): RTN 3.79 -> 3.43 ms per step, SR 4.14 ->
-  // 4.06 ms.  (Kernels with an LDS tile cache keep the arithmetic: the table
-  // would cost them a workgroup per CU, or registers.)
-  constexpr bool LUT = KIND == K_INT8 && LCACHE == 0;
+  // 4.06 ms.  (The 16-wave kernel with 4 LDS tiles per wave keeps the
+  // arithmetic: the table would cost it registers it does not have.)
+  constexpr bool LUT = KIND == K_INT8 && (LCACHE == 0 || (NW == 8 && LCACHE <= 2));
   static_assert(!LUT || NW == 8, "the table build assigns 32 threads to each of the 16 rows");
   // rows 260 floats apart: lanes of different rows reading the same code byte
   // fall in different banks
@@ -1003,9 +1003,10 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
 
 // Rank 16 with the 8-tile cache fits 128 VGPRs: two 512-thread workgroups per
 // CU (4 waves per SIMD), which the bound below holds the compiler to (and the
-// 16-wave kernel's 10-tile cache to 128 VGPRs as well).
+// 16-wave kernel's 10-tile cache, and rank 32's 6 register tiles, to 128
+// VGPRs as well).
 template <int NKC, int CACHE>
-constexpr int fast_min_waves() { return (NKC == 1 && CACHE <= 10) || (NKC == 2 && CACHE <= 4) ? 4 : 1; }
+constexpr int fast_min_waves() { return (NKC == 1 && CACHE <= 10) || (NKC == 2 && CACHE <= 6) ? 4 : 1; }
 
 template <int KIND, bool SR, int NKC, int NW, int CACHE, int PF_ = fast_prefetch<NKC, SR>(), int LCACHE = 0,
           bool SBF = false>
@@ -1847,11 +1848,14 @@ static inline bool rows_fast_ok(int kind, int cd, int sdt, bool asym, int nkc, i
 //   costs (those rows recompute).
 // Rows of up to 8 tiles per wave: rank 16 caches them all in registers; rank
 // 32 keeps 4 in registers and 4 in LDS (64 KiB per workgroup), which brings
-// it to 106 VGPRs and two workgroups per CU instead of one.
-template <int NKC>
-constexpr int row_reg_cache() { return NKC == 2 ? 4 : 8; }
-template <int NKC>
-constexpr int row_lds_cache() { return NKC == 2 ? 4 : 0; }
+// it to 106 VGPRs and two workgroups per CU instead of one.  INT8 at rank 32
+// keeps 6 in registers and 2 in LDS (116 VGPRs, 32 KiB), which leaves room
+// for the dequantization table: config 2 ([14336, 4096] r32) SR 0.0499 ->
+// 0.0481 ms, RTN 0.0424 -> 0.0420 ms, bit-identical.
+template <int KIND, int NKC>
+constexpr int row_reg_cache() { return NKC == 2 ? (KIND == K_INT8 ? 6 : 4) : 8; }
+template <int KIND, int NKC>
+constexpr int row_lds_cache() { return NKC == 2 ? (KIND == K_INT8 ? 2 : 4) : 0; }
 static constexpr int ROW_DEEP_CACHE = 16;
 static constexpr int ROW_NW_WIDE = 16;
 // 16-wave rows keep 10 tiles per wave in registers and 4 more in LDS (128 KiB
@@ -1885,8 +1889,8 @@ static int launch_rows_fast(const RowArgs& a, hipStream_t st) {
       hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, ROW_DEEP_CACHE, NKC == 4 ? 1 : 2, 0, SBF>), grid,
                          dim3(ROW_NW * 64), 0, st, a);
   } else {
-    hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, row_reg_cache<NKC>(), fast_prefetch<NKC, SR>(),
-                                    row_lds_cache<NKC>(), SBF>),
+    hipLaunchKernelGGL((k_rows_fast<KIND, SR, NKC, ROW_NW, row_reg_cache<KIND, NKC>(), fast_prefetch<NKC, SR>(),
+                                    row_lds_cache<KIND, NKC>(), SBF>),
                        grid, dim3(ROW_NW * 64), 0, st, a);
   }
   LAUNCH_CHECK();

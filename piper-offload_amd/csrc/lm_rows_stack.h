@@ -19,8 +19,9 @@ static int int8_stack_fast_launch(const RowStackItem* d0, const int32_t* begins,
     const dim3 grid((unsigned)tiles[0]);
 #define RF(SR_)                                                                                                     \
   NKC_SWITCH(nkc_bucket(nkc_max),                                                                                   \
-             hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, row_reg_cache<NKC_>(),                 \
-                                                   fast_prefetch<NKC_, SR_>(), row_lds_cache<NKC_>(), NKC_ == 1, SBF>), \
+             hipLaunchKernelGGL((k_rows_fast_stack<K_INT8, SR_, NKC_, ROW_NW, row_reg_cache<K_INT8, NKC_>(),         \
+                                                   fast_prefetch<NKC_, SR_>(), row_lds_cache<K_INT8, NKC_>(), NKC_ == 1,  \
+                                                   SBF>),                                                             \
                                 grid, block, 0, st, d0, begins, n_regular))
     if (sr) { RF(true); } else { RF(false); }
 #undef RF
