@@ -867,15 +867,14 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
                      : SBF ? bf16_val(((const LM_GLOBAL uint16_t*)a.scale)[row]) : ((const LM_GLOBAL float*)a.scale)[row];
   uint32_t cache[CACHE][8];
   float amax = 0.0f;
-  // INT8 without an LDS tile cache: the dequantized base bf16(RN(q s)) comes
+  // INT8 in 8-wave workgroups: the dequantized base bf16(RN(q s)) comes
   // from a per-row table of the 256 code bytes in LDS (16 KiB), two address
   // instructions per element instead of the sign-extending convert, the
   // product and the bf16 rounding; the values are the same.  8B stack
   // (bench.py, bit-identical): RTN 3.79 -> 3.43 ms per step, SR 4.14 ->
-  // 4.06 ms.  (The 16-wave kernel with 4 LDS tiles per wave keeps the
-  // arithmetic: the table would cost it registers it does not have.)
-  constexpr bool LUT = KIND == K_INT8 && (LCACHE == 0 || (NW == 8 && LCACHE <= 2));
-  static_assert(!LUT || NW == 8, "the table build assigns 32 threads to each of the 16 rows");
+  // 4.06 ms.  (The 16-wave long-row kernel, one workgroup per CU with 4 LDS
+  // tiles per wave, measured slower with it and keeps the arithmetic.)
+  constexpr bool LUT = KIND == K_INT8 && NW == 8 && LCACHE <= 2;
   // rows 260 floats apart: lanes of different rows reading the same code byte
   // fall in different banks
   constexpr int LSTRIDE = 260;
@@ -891,7 +890,7 @@ __device__ __forceinline__ void rows_fast_body(const RowArgs& a, int64_t row0) {
     for (int i = 0; i < CACHE; ++i) raw[i] = fast_load_codes(L, wave + i * NW);
   }
   if constexpr (LUT) {
-    // thread t fills row t / 32 for the codes q = 4 (t % 32) .. + 3 and -q
+    // thread t of the 512 fills row t / 32 for the codes q = 4 (t % 32) .. + 3 and -q
     // (RN and the bf16 rounding are odd functions, so the entry of -q is the
     // negated entry of q); the row's first thread also fills -128
     const int r = (int)(threadIdx.x >> 5), q0 = 4 * (int)(threadIdx.x & 31);
