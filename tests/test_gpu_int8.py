@@ -121,6 +121,34 @@ def test_int8_fused_equals_requant_of_gpu_dense(shape, rank, strength, sr, scale
     assert not oz.any()
 
 
+# The 8-wave row kernels read the dequantized base from a per-row table of the
+# 256 code bytes built from the row's scale (entries for negative codes are the
+# negated positive ones).  Scales of exactly 0, negative scales and full-range
+# codes (-128 included) against the dense merge, which converts and scales each
+# code: rank 16 and rank 32 take the table, 14336 columns the 16-wave kernel.
+@pytest.mark.parametrize("shape,rank", [((40, 1024), 16), ((64, 4096), 32), ((33, 14336), 16)])
+@pytest.mark.parametrize("sr", [False, True])
+@pytest.mark.parametrize("scale_dtype", [torch.float32, torch.bfloat16])
+def test_int8_fused_table_edge_scales(shape, rank, sr, scale_dtype):
+    rows, cols = shape
+    q, s, b, a = _int8_case(rows, cols, rank, seed=7, scale_dtype=scale_dtype)
+    g = torch.Generator().manual_seed(11)
+    q[3] = torch.randint(-128, 128, (cols,), generator=g, dtype=torch.int8)  # every code byte
+    q[3, :4] = torch.tensor([-128, 127, 0, -1], dtype=torch.int8)
+    s[3] = -s[3]          # a negative scale
+    s[5] = 0.0            # a zero scale with non-zero codes
+    s[rows - 1] = -0.0    # a negative zero
+    qd, sd, bd, ad = q.to(DEV), s.to(DEV), b.to(DEV), a.to(DEV)
+    seed = derive_seed("int8.table", rows) if sr else None
+    oq, os_, _ = K.merge_int8_lora(qd, sd, None, (1, cols), bd, ad, 1.0, asymmetric=False, reduce_range=False,
+                                   rounding_seed=seed)
+    dense = K.dequantize_int8(qd, sd, None, (1, cols), lora=(bd, ad, 1.0))
+    rq, rs, _ = O.int8_requant(bf16_np(dense), cols, scale_dt=O.DT_F32 if scale_dtype is torch.float32 else O.DT_BF16,
+                               sr_mode=O.SR_PHILOX8 if sr else O.SR_OFF, seed=seed or 0)
+    assert np.array_equal(oq.cpu().numpy(), rq)
+    assert np.array_equal(_scale_np(os_), rs)
+
+
 # two-pass long rows (rank above 32, rows of more than 4096 columns): rows that
 # end inside a 64-row wave tile and a partial last tile range, merged out of
 # place and then in place (outputs aliasing the inputs)
