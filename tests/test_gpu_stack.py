@@ -166,6 +166,10 @@ def _nvfp4_errors(side: str, i: int, q, s, pts, expected) -> list[str]:  # noqa:
 
 @pytest.mark.parametrize("shapes", [[(64, 256), (40, 512), (16, 128), (128, 1024)],  # fast kernels (N % 128 == 0)
                                     [(32, 256), (16, 96)],                           # per-target block kernels
+                                    # plain-layout block scales staged in LDS up to 128 macro tiles per row:
+                                    # the limit itself with ragged row groups, then one item past it
+                                    [(40, 16384), (33, 4096), (17, 128)],
+                                    [(24, 16512), (40, 256)],
                                     LAYER])                                          # one 8B layer at full size
 @pytest.mark.parametrize("swizzled", [False, True])
 @pytest.mark.parametrize("sr", [False, True])
